@@ -1,0 +1,160 @@
+// glu.hip -- SwiGLU (silu(gate) * up) and GeGLU (gelu_tanh(gate) * up) on
+// gfx950.
+//
+// A pure stream: every element of gate and up is read once and every output
+// written once. Each thread owns U 16-byte chunks spaced one block-width apart
+// (so every load instruction of the block covers a contiguous 4 KB), issues all
+// 2U loads before any arithmetic, and writes with non-temporal stores.
+//
+// SwiGLU arithmetic is MLX's CPU composition, bit for bit:
+//   sig = round_T(sigmoid(g)); s = round_T(g * sig); out = round_T(s * u)
+// with MLX's sigmoid (1/(1+exp(|g|)), complemented for g >= 0) and MLX's
+// polynomial exp, built from IEEE operations only.
+// GeGLU runs in f32 (mlx-rs builds gelu_approximate from f32 scalar arrays,
+// which promote a bf16 input): 0.5*g*(1+tanh(k0*(g + k1*g^3))) is evaluated as
+// the identical g / (1 + exp(-2*k0*(g + k1*g^3))), using the hardware exp2 and
+// reciprocal (relative error ~1e-6), and the product with up is rounded once.
+#include "../../include/higgs_hip.h"
+#include "hgk_common.h"
+#include "hgk_host.h"
+
+namespace hgk {
+
+struct GluArgs {
+  const void* g;
+  int64_t gs;
+  const void* u;
+  int64_t us;
+  void* o;
+  int64_t os;
+  uint32_t cpr;    // 16-byte chunks per row
+  uint32_t total;  // chunks overall
+  int contig;      // all three tensors densely packed
+};
+
+template <class X, int ACT>
+__device__ inline float glu1(float g, float u) {
+  if constexpr (ACT == HGK_ACT_SILU) {
+    const float sg = X::round(mlx_sigmoid(g));
+    const float s = X::round(g * sg);
+    return X::round(s * u);
+  } else {
+    const float k0 = 0.7978845608028654f, k1 = 0.044715f;
+    const float g3 = g * g * g;
+    const float inner = k0 * (g + k1 * g3);
+    const float e = __builtin_amdgcn_exp2f(inner * -2.8853900817779268f);  // exp(-2*inner)
+    const float gl = g * __builtin_amdgcn_rcpf(1.0f + e);
+    return gl * u;
+  }
+}
+
+template <class X, class Y, int ACT, int U>
+__global__ __launch_bounds__(256) void glu_kernel(GluArgs a) {
+  constexpr int V = Vec<X>::N;
+  const uint32_t base = blockIdx.x * (256u * U) + threadIdx.x;
+  float gv[U][V], uv[U][V];
+  int64_t oo[U];
+  bool ok[U];
+#pragma unroll
+  for (int k = 0; k < U; ++k) {
+    const uint32_t q = base + 256u * k;
+    ok[k] = q < a.total;
+    const uint32_t qq = ok[k] ? q : 0u;
+    int64_t go, uo;
+    if (a.contig) {
+      go = uo = oo[k] = (int64_t)qq * V;
+    } else {
+      const uint32_t row = qq / a.cpr, c = qq - row * a.cpr;
+      go = (int64_t)row * a.gs + (int64_t)c * V;
+      uo = (int64_t)row * a.us + (int64_t)c * V;
+      oo[k] = (int64_t)row * a.os + (int64_t)c * V;
+    }
+    load_chunk<X>(a.g, go, gv[k]);
+    load_chunk<X>(a.u, uo, uv[k]);
+  }
+#pragma unroll
+  for (int k = 0; k < U; ++k) {
+    float o[V];
+#pragma unroll
+    for (int e = 0; e < V; ++e) o[e] = glu1<X, ACT>(gv[k][e], uv[k][e]);
+    if (ok[k]) store_elems<Y, V>(a.o, oo[k], o);
+  }
+}
+
+// Any alignment / width: one element per thread.
+template <class X, class Y, int ACT>
+__global__ __launch_bounds__(256) void glu_generic_kernel(GluArgs a, int64_t n, int64_t rows) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n * rows) return;
+  const int64_t row = i / n, c = i - row * n;
+  const float g = load1<X>(a.g, row * a.gs + c), u = load1<X>(a.u, row * a.us + c);
+  store1<Y>(a.o, row * a.os + c, glu1<X, ACT>(g, u));
+}
+
+namespace {
+
+template <class X, class Y, int ACT>
+void launch(const GluArgs& a, bool vec_ok, int64_t rows, int64_t n, hipStream_t s) {
+  if (vec_ok) {
+    if (a.total >= 256u * 4u * 1024u) {
+      const unsigned blocks = (a.total + 1024u - 1u) / 1024u;
+      hipLaunchKernelGGL((glu_kernel<X, Y, ACT, 4>), dim3(blocks), dim3(256), 0, s, a);
+    } else {
+      const unsigned blocks = (a.total + 255u) / 256u;
+      hipLaunchKernelGGL((glu_kernel<X, Y, ACT, 1>), dim3(blocks), dim3(256), 0, s, a);
+    }
+    return;
+  }
+  const int64_t blocks = (n * rows + 255) / 256;
+  hipLaunchKernelGGL((glu_generic_kernel<X, Y, ACT>), dim3((unsigned)blocks), dim3(256), 0, s,
+                     a, n, rows);
+}
+
+template <int ACT>
+int dispatch(const GluArgs& a, int xdt, int ydt, bool vec_ok, int64_t rows, int64_t n, hipStream_t s) {
+  if (xdt == DT_BF16 && ydt == DT_BF16) launch<BF16, BF16, ACT>(a, vec_ok, rows, n, s);
+  else if (xdt == DT_BF16 && ydt == DT_F32) launch<BF16, F32, ACT>(a, vec_ok, rows, n, s);
+  else if (xdt == DT_F16 && ydt == DT_F16) launch<F16, F16, ACT>(a, vec_ok, rows, n, s);
+  else if (xdt == DT_F16 && ydt == DT_F32) launch<F16, F32, ACT>(a, vec_ok, rows, n, s);
+  else if (xdt == DT_F32 && ydt == DT_F32) launch<F32, F32, ACT>(a, vec_ok, rows, n, s);
+  else
+    return fail(HGK_ERR_UNSUPPORTED, "hgk_glu: output dtype %s for input %s is not implemented",
+                dtype_name(ydt), dtype_name(xdt));
+  return launch_status("hgk_glu");
+}
+
+}  // namespace
+}  // namespace hgk
+
+using namespace hgk;
+
+extern "C" int hgk_glu(int act, int dtype, const void* gate, int64_t gate_row_stride,
+                       const void* up, int64_t up_row_stride, void* out, int out_dtype,
+                       int64_t out_row_stride, int64_t rows, int64_t n, void* stream) {
+  clear_error();
+  if (act != HGK_ACT_SILU && act != HGK_ACT_GELU_TANH)
+    return fail(HGK_ERR_ARG, "hgk_glu: unknown activation %d", act);
+  if (!is_float_dtype(dtype) || !is_float_dtype(out_dtype))
+    return fail(HGK_ERR_ARG, "hgk_glu: dtypes must be f32, bf16 or f16");
+  if (rows < 0 || n < 0) return fail(HGK_ERR_ARG, "hgk_glu: negative shape");
+  if (!gate || !up || !out) return fail(HGK_ERR_ARG, "hgk_glu: null pointer");
+  if (rows > 1 && (gate_row_stride < n || up_row_stride < n || out_row_stride < n))
+    return fail(HGK_ERR_ARG, "hgk_glu: row stride smaller than n");
+  if (rows == 0 || n == 0) return HGK_OK;
+  const int V = 16 / dtype_bytes(dtype);
+  const int64_t chunks = (n / V) * rows;
+  if (chunks >= ((int64_t)1 << 32) || n * rows >= ((int64_t)1 << 40))
+    return fail(HGK_ERR_UNSUPPORTED, "hgk_glu: problem too large");
+  GluArgs a{};
+  a.g = gate; a.gs = gate_row_stride; a.u = up; a.us = up_row_stride;
+  a.o = out; a.os = out_row_stride;
+  a.cpr = (uint32_t)(n / V);
+  a.total = (uint32_t)chunks;
+  a.contig = (rows == 1) || (gate_row_stride == n && up_row_stride == n && out_row_stride == n);
+  const int ob = dtype_bytes(out_dtype);
+  const bool vec_ok = aligned16(gate) && aligned16(up) && aligned16(out) && n % V == 0 &&
+                      gate_row_stride % V == 0 && up_row_stride % V == 0 &&
+                      (out_row_stride * ob) % 16 == 0;
+  if (act == HGK_ACT_SILU) return dispatch<HGK_ACT_SILU>(a, dtype, out_dtype, vec_ok, rows, n, as_stream(stream));
+  return dispatch<HGK_ACT_GELU_TANH>(a, dtype, out_dtype, vec_ok, rows, n, as_stream(stream));
+}

@@ -1,0 +1,232 @@
+// hgk_common.h -- shared device helpers for the gfx950 per-layer op kernels.
+//
+// Element types travel as 16-bit or 32-bit storage words; every kernel loads
+// and stores 16-byte chunks (8 x bf16/f16 or 4 x f32 per lane), converts to
+// f32, and rounds back to the storage type exactly where MLX's CPU-device
+// composition of the op materialises an intermediate.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace hgk {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+enum Dtype { DT_F32 = 0, DT_BF16 = 1, DT_F16 = 2, DT_U32 = 3, DT_I32 = 4 };
+
+__host__ __device__ inline uint32_t f2u(float f) { return __builtin_bit_cast(uint32_t, f); }
+__host__ __device__ inline float u2f(uint32_t u) { return __builtin_bit_cast(float, u); }
+
+// Materialise an f32 value in a register before it is narrowed. Without it
+// the backend may fold `fptrunc(a * b)` into a mixed-precision FMA
+// (v_fma_mixlo_f16: a*b rounded once, straight to 16 bits), whereas the ops
+// being reproduced round the product to f32 first and then to 16 bits.
+__device__ inline float f32_barrier(float x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
+// ---------------------------------------------------------------- types
+struct BF16 {
+  static constexpr int kCode = DT_BF16;
+  static constexpr int kBytes = 2;
+  __device__ static float lo(uint32_t w) { return u2f(w << 16); }
+  __device__ static float hi(uint32_t w) { return u2f(w & 0xffff0000u); }
+  // Two f32 -> packed pair, round-to-nearest-even (v_cvt_pk_bf16_f32).
+  __device__ static uint32_t pack(float a, float b) {
+    f32x2 v = {f32_barrier(a), f32_barrier(b)};
+    bf16x2 h = __builtin_convertvector(v, bf16x2);
+    return __builtin_bit_cast(uint32_t, h);
+  }
+  __device__ static float round(float a) { return u2f(pack(a, 0.0f) << 16); }
+};
+
+struct F16 {
+  static constexpr int kCode = DT_F16;
+  static constexpr int kBytes = 2;
+  __device__ static float lo(uint32_t w) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xffffu));
+  }
+  __device__ static float hi(uint32_t w) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
+  }
+  __device__ static uint32_t pack(float a, float b) {
+    f32x2 v = {f32_barrier(a), f32_barrier(b)};
+    f16x2 h = __builtin_convertvector(v, f16x2);
+    return __builtin_bit_cast(uint32_t, h);
+  }
+  __device__ static float round(float a) { return lo(pack(a, 0.0f)); }
+};
+
+struct F32 {
+  static constexpr int kCode = DT_F32;
+  static constexpr int kBytes = 4;
+  __device__ static float round(float a) { return a; }
+};
+
+// Elements of T per 16-byte chunk.
+template <class T> struct Vec { static constexpr int N = 16 / T::kBytes; };
+
+// ---------------------------------------------------------------- chunk I/O
+template <class T>
+__device__ inline void unpack16(u32x4 r, float* v) {
+  if constexpr (T::kBytes == 2) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      v[2 * k] = T::lo(r[k]);
+      v[2 * k + 1] = T::hi(r[k]);
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) v[k] = u2f(r[k]);
+  }
+}
+
+// Load Vec<T>::N elements of T starting at element `e` (16-byte aligned).
+template <class T>
+__device__ inline void load_chunk(const void* base, int64_t e, float* v) {
+  const u32x4* p = reinterpret_cast<const u32x4*>(
+      reinterpret_cast<const char*>(base) + e * T::kBytes);
+  unpack16<T>(*p, v);
+}
+
+// Load N elements of T starting at element e (N * sizeof(T) a multiple of 16).
+template <class T, int N>
+__device__ inline void load_elems(const void* base, int64_t e, float* v) {
+  constexpr int kPer = Vec<T>::N;
+  if constexpr (N * T::kBytes == 8) {
+    // half chunk: 4 x 16-bit (8-byte aligned)
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    const u32x2 r = *reinterpret_cast<const u32x2*>(reinterpret_cast<const char*>(base) +
+                                                    e * T::kBytes);
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      v[2 * k] = T::lo(r[k]);
+      v[2 * k + 1] = T::hi(r[k]);
+    }
+  } else {
+    static_assert(N % kPer == 0, "whole chunks only");
+#pragma unroll
+    for (int c = 0; c < N / kPer; ++c) load_chunk<T>(base, e + c * kPer, v + c * kPer);
+  }
+}
+
+// Store N f32 values as T at element e (values are rounded to T, RNE).
+template <class T, int N, bool NT = true>
+__device__ inline void store_elems(void* base, int64_t e, const float* v) {
+  constexpr int kPer = Vec<T>::N;
+  static_assert(N % kPer == 0, "whole chunks only");
+#pragma unroll
+  for (int c = 0; c < N / kPer; ++c) {
+    u32x4 w;
+    if constexpr (T::kBytes == 2) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) w[k] = T::pack(v[c * kPer + 2 * k], v[c * kPer + 2 * k + 1]);
+    } else {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) w[k] = f2u(v[c * kPer + k]);
+    }
+    u32x4* p = reinterpret_cast<u32x4*>(reinterpret_cast<char*>(base) +
+                                        (e + c * kPer) * T::kBytes);
+    if constexpr (NT) __builtin_nontemporal_store(w, p);
+    else *p = w;
+  }
+}
+
+// Load N weights of runtime dtype wdt (bf16/f16/f32) starting at element e.
+template <int N>
+__device__ inline void load_weights(const void* w, int wdt, int64_t e, float* v) {
+  if (wdt == DT_BF16) load_elems<BF16, N>(w, e, v);
+  else if (wdt == DT_F16) load_elems<F16, N>(w, e, v);
+  else load_elems<F32, N>(w, e, v);
+}
+
+// Scalar load / store for the generic (unaligned / odd-size) fallbacks.
+template <class T>
+__device__ inline float load1(const void* base, int64_t e) {
+  if constexpr (T::kBytes == 2) {
+    uint16_t h = reinterpret_cast<const uint16_t*>(base)[e];
+    return T::lo((uint32_t)h);
+  } else {
+    return reinterpret_cast<const float*>(base)[e];
+  }
+}
+
+__device__ inline float load1_dt(const void* base, int dt, int64_t e) {
+  if (dt == DT_BF16) return load1<BF16>(base, e);
+  if (dt == DT_F16) return load1<F16>(base, e);
+  return load1<F32>(base, e);
+}
+
+template <class T>
+__device__ inline void store1(void* base, int64_t e, float v) {
+  if constexpr (T::kBytes == 2) {
+    reinterpret_cast<uint16_t*>(base)[e] = (uint16_t)(T::pack(v, 0.0f) & 0xffffu);
+  } else {
+    reinterpret_cast<float*>(base)[e] = v;
+  }
+}
+
+// ---------------------------------------------------------------- math
+// MLX's CPU exp for float types: x*log2(e) split into integer and fractional
+// parts, 2^frac by the degree-6 Cephes exp2f minimax polynomial (Moshier),
+// 2^int assembled in the exponent field; NaN passes through, x > 88 -> inf,
+// x < -88 -> 0. Built only from IEEE mul/add/fma/floor, so host and device
+// give bit-identical results (requires -ffp-contract=off).
+__host__ __device__ inline float mlx_exp(float x_init) {
+  float x = x_init * 1.442695f;
+  float ipart = floorf(x + 0.5f);
+  float fpart = x - ipart;
+  float p = 1.535336188319500e-4f;
+  p = fmaf(p, fpart, 1.339887440266574e-3f);
+  p = fmaf(p, fpart, 9.618437357674640e-3f);
+  p = fmaf(p, fpart, 5.550332471162809e-2f);
+  p = fmaf(p, fpart, 2.402264791363012e-1f);
+  p = fmaf(p, fpart, 6.931472028550421e-1f);
+  p = fmaf(p, fpart, 1.000000000000000f);
+  float ic = ipart > 200.0f ? 200.0f : (ipart < -200.0f ? -200.0f : ipart);
+  uint32_t eb = (uint32_t)((int32_t)ic + 127) << 23;
+  float r = u2f(eb) * p;
+  if (x_init > 88.0f) r = __builtin_inff();
+  if (x_init < -88.0f) r = 0.0f;
+  if (x_init != x_init) r = x_init;
+  return r;
+}
+
+// MLX CPU Sigmoid: y = 1/(1+exp(|x|)); x < 0 -> y, else 1 - y. The division is
+// IEEE (correctly rounded) on both host and device.
+__host__ __device__ inline float mlx_sigmoid(float x) {
+  float y = 1.0f / (1.0f + mlx_exp(fabsf(x)));
+  return x < 0.0f ? y : 1.0f - y;
+}
+
+// Sum over aligned groups of W lanes (W a power of two <= 64); every lane of
+// the group receives the same bit pattern.
+template <int W>
+__device__ inline float group_sum(float v) {
+#pragma unroll
+  for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, W);
+  return v;
+}
+
+template <int W>
+__device__ inline double group_sum(double v) {
+#pragma unroll
+  for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, W);
+  return v;
+}
+
+// RMS scale r = 1/sqrt(f32(sum) * inv_n + eps) from an f64 sum of squares.
+// Squares of f32 values are exact in f64 and the f64 sum is rounded once, so
+// the result does not depend on the reduction order (MLX's mean(square(x)) is
+// sum * f32(1/n) in f32; both sqrt and division are correctly rounded here).
+__device__ inline float rms_scale(double ss, float inv_n, float eps) {
+  const float ms = (float)ss * inv_n;
+  return 1.0f / sqrtf(ms + eps);
+}
+
+}  // namespace hgk

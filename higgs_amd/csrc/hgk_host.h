@@ -1,0 +1,40 @@
+// hgk_host.h -- host-side helpers shared by the C-ABI entry points.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace hgk {
+
+// Record a thread-local error message and return `status`.
+int fail(int status, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+
+// Clear the thread-local error message (called on entry by every ABI call).
+void clear_error();
+
+// After a launch: HGK_OK, or HGK_ERR_HIP with the HIP error text.
+int launch_status(const char* what);
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+inline int dtype_bytes(int dt) { return (dt == 1 || dt == 2) ? 2 : 4; }
+
+inline bool is_float_dtype(int dt) { return dt == 0 || dt == 1 || dt == 2; }
+
+inline const char* dtype_name(int dt) {
+  switch (dt) {
+    case 0: return "f32";
+    case 1: return "bf16";
+    case 2: return "f16";
+    case 3: return "u32";
+    case 4: return "i32";
+    default: return "?";
+  }
+}
+
+// MLX promote_types restricted to the float dtypes.
+inline int promote(int a, int b) { return a == b ? a : 0; }
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+}  // namespace hgk

@@ -1,0 +1,292 @@
+// norm.hip -- RMSNorm, Gemma (1+w) RMSNorm, per-head q/k RMSNorm and the
+// Qwen3-Next gated RMSNorm on gfx950.
+//
+// Layout: rows of n contiguous elements, arbitrary row stride. A group of LPR
+// lanes owns one row (LPR = 64 for hidden-size rows, fewer for head_dim rows,
+// so a wave64 covers 64/LPR rows); each lane holds CPL 16-byte chunks of its
+// row in registers, strided by LPR so the wave's loads are fully coalesced.
+// The f32 sum of squares is reduced across the group with xor shuffles, then
+// the same registers are scaled and written: x crosses HBM once, y once.
+//
+// Arithmetic follows MLX's CPU composition (fast::rms_norm fallback):
+//   r = 1 / sqrt(f32(sum(x*x)) * f32(1/n) + eps)   (sum accumulated in f64)
+//   n = round_T(x * r);  y = round_T(n * w')        (T = promote(x, w'))
+// and, gated, out = round_T(round_T(z * round_T(sigmoid(z))) * y).
+#include "../../include/higgs_hip.h"
+#include "hgk_common.h"
+#include "hgk_host.h"
+
+namespace hgk {
+
+struct NormArgs {
+  const void* x;
+  int64_t xs;
+  const void* z;  // gated only: row r at (r / zg) * zgs + (r % zg) * zs
+  int64_t zs;
+  int64_t zg;
+  int64_t zgs;
+  const void* w;  // may be null
+  int wdt;
+  int plus_one;
+  int round_x;  // computation type is the activation type (else f32)
+  float eps;
+  float inv_n;
+  void* y;
+  int64_t ys;
+  int64_t rows;
+  int n;
+};
+
+__device__ inline int64_t z_row_offset(const NormArgs& a, int64_t r) {
+  const int64_t g = r / a.zg;
+  return g * a.zgs + (r - g * a.zg) * a.zs;
+}
+
+template <class X, class Y, int LPR, int CPL, bool GATED>
+__global__ __launch_bounds__(256) void rms_norm_kernel(NormArgs a) {
+  constexpr int V = Vec<X>::N;
+  constexpr int RPW = 64 / LPR;
+  const int lane = threadIdx.x & 63;
+  const int64_t wave = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int64_t row = wave * RPW + lane / LPR;
+  const int j = lane % LPR;
+  const bool live = row < a.rows;
+  const int64_t r = live ? row : a.rows - 1;
+  const int nchunks = a.n / V;
+
+  float v[CPL][V];
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    const int ch = j + c * LPR;
+    if (ch < nchunks) {
+      load_chunk<X>(a.x, r * a.xs + (int64_t)ch * V, v[c]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < V; ++e) v[c][e] = 0.0f;
+    }
+  }
+  double ss = 0.0;
+#pragma unroll
+  for (int c = 0; c < CPL; ++c)
+#pragma unroll
+    for (int e = 0; e < V; ++e) ss = __builtin_fma((double)v[c][e], (double)v[c][e], ss);
+  ss = group_sum<LPR>(ss);
+  const float rr = rms_scale(ss, a.inv_n, a.eps);
+
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    const int ch = j + c * LPR;
+    if (ch >= nchunks) continue;
+    float w[V];
+    if (a.w) {
+      load_weights<V>(a.w, a.wdt, (int64_t)ch * V, w);
+    } else {
+#pragma unroll
+      for (int e = 0; e < V; ++e) w[e] = 1.0f;
+    }
+    float zc[V];
+    if constexpr (GATED) load_chunk<X>(a.z, z_row_offset(a, r) + (int64_t)ch * V, zc);
+    float o[V];
+#pragma unroll
+    for (int e = 0; e < V; ++e) {
+      float nv = v[c][e] * rr;
+      nv = a.round_x ? X::round(nv) : nv;
+      const float we = a.plus_one ? w[e] + 1.0f : w[e];
+      nv = nv * we;
+      nv = a.round_x ? X::round(nv) : nv;
+      if constexpr (GATED) {
+        const float zz = zc[e];
+        const float sg = X::round(mlx_sigmoid(zz));
+        const float act = X::round(zz * sg);
+        nv = act * nv;
+        nv = a.round_x ? X::round(nv) : nv;
+      }
+      o[e] = nv;
+    }
+    if (live) store_elems<Y, V>(a.y, r * a.ys + (int64_t)ch * V, o);
+  }
+}
+
+// Any n, any alignment: one wave per row, element-strided, two passes over x.
+template <class X, class Y, bool GATED>
+__global__ __launch_bounds__(256) void rms_norm_generic_kernel(NormArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (row >= a.rows) return;  // whole wave leaves together
+  double ss = 0.0;
+  for (int i = lane; i < a.n; i += 64) {
+    const double xv = (double)load1<X>(a.x, row * a.xs + i);
+    ss = __builtin_fma(xv, xv, ss);
+  }
+  ss = group_sum<64>(ss);
+  const float rr = rms_scale(ss, a.inv_n, a.eps);
+  for (int i = lane; i < a.n; i += 64) {
+    float nv = load1<X>(a.x, row * a.xs + i) * rr;
+    nv = a.round_x ? X::round(nv) : nv;
+    float we = a.w ? load1_dt(a.w, a.wdt, i) : 1.0f;
+    we = a.plus_one ? we + 1.0f : we;
+    nv = nv * we;
+    nv = a.round_x ? X::round(nv) : nv;
+    if constexpr (GATED) {
+      const float zz = load1<X>(a.z, z_row_offset(a, row) + i);
+      const float sg = X::round(mlx_sigmoid(zz));
+      const float act = X::round(zz * sg);
+      nv = act * nv;
+      nv = a.round_x ? X::round(nv) : nv;
+    }
+    store1<Y>(a.y, row * a.ys + i, nv);
+  }
+}
+
+namespace {
+
+template <class X, class Y, int LPR, int CPL, bool GATED>
+void launch_fast(const NormArgs& a, hipStream_t s) {
+  constexpr int RPW = 64 / LPR;
+  const int64_t waves = (a.rows + RPW - 1) / RPW;
+  const int wpb = waves >= 4096 ? 4 : 1;  // small problems: spread over CUs
+  const int64_t blocks = (waves + wpb - 1) / wpb;
+  hipLaunchKernelGGL((rms_norm_kernel<X, Y, LPR, CPL, GATED>), dim3((unsigned)blocks),
+                     dim3(64 * wpb), 0, s, a);
+}
+
+template <class X, class Y, bool GATED>
+void launch_generic(const NormArgs& a, hipStream_t s) {
+  const int wpb = a.rows >= 4096 ? 4 : 1;
+  const int64_t blocks = (a.rows + wpb - 1) / wpb;
+  hipLaunchKernelGGL((rms_norm_generic_kernel<X, Y, GATED>), dim3((unsigned)blocks),
+                     dim3(64 * wpb), 0, s, a);
+}
+
+// Pick (LPR, CPL) for a row of `nchunks` 16-byte chunks; false -> generic.
+template <class X, class Y, bool GATED>
+bool launch_by_shape(const NormArgs& a, int nchunks, hipStream_t s) {
+  if (nchunks <= 4) { launch_fast<X, Y, 4, 1, GATED>(a, s); return true; }
+  if (nchunks <= 8) { launch_fast<X, Y, 8, 1, GATED>(a, s); return true; }
+  if (nchunks <= 16) { launch_fast<X, Y, 16, 1, GATED>(a, s); return true; }
+  if (nchunks <= 32) { launch_fast<X, Y, 32, 1, GATED>(a, s); return true; }
+  if (nchunks <= 64) { launch_fast<X, Y, 64, 1, GATED>(a, s); return true; }
+  if (nchunks <= 128) { launch_fast<X, Y, 64, 2, GATED>(a, s); return true; }
+  if constexpr (!GATED) {
+    const int cpl = (nchunks + 63) / 64;
+    switch (cpl) {
+      case 3: launch_fast<X, Y, 64, 3, false>(a, s); return true;
+      case 4: launch_fast<X, Y, 64, 4, false>(a, s); return true;
+      case 5: launch_fast<X, Y, 64, 5, false>(a, s); return true;
+      case 6: launch_fast<X, Y, 64, 6, false>(a, s); return true;
+      case 7: launch_fast<X, Y, 64, 7, false>(a, s); return true;
+      case 8: launch_fast<X, Y, 64, 8, false>(a, s); return true;
+      case 9: case 10: launch_fast<X, Y, 64, 10, false>(a, s); return true;
+      case 11: case 12: launch_fast<X, Y, 64, 12, false>(a, s); return true;
+      case 13: case 14: case 15: case 16:
+        launch_fast<X, Y, 64, 16, false>(a, s); return true;
+      default: break;
+    }
+  }
+  return false;
+}
+
+template <class X, class Y, bool GATED>
+void launch_xy(const NormArgs& a, bool vec_ok, hipStream_t s) {
+  const int nchunks = a.n / Vec<X>::N;
+  if (vec_ok && launch_by_shape<X, Y, GATED>(a, nchunks, s)) return;
+  launch_generic<X, Y, GATED>(a, s);
+}
+
+template <bool GATED>
+int dispatch(const NormArgs& a, int xdt, int ydt, bool vec_ok, hipStream_t s) {
+  if (xdt == DT_BF16 && ydt == DT_BF16) launch_xy<BF16, BF16, GATED>(a, vec_ok, s);
+  else if (xdt == DT_BF16 && ydt == DT_F32) launch_xy<BF16, F32, GATED>(a, vec_ok, s);
+  else if (xdt == DT_F16 && ydt == DT_F16) launch_xy<F16, F16, GATED>(a, vec_ok, s);
+  else if (xdt == DT_F16 && ydt == DT_F32) launch_xy<F16, F32, GATED>(a, vec_ok, s);
+  else if (xdt == DT_F32 && ydt == DT_F32) launch_xy<F32, F32, GATED>(a, vec_ok, s);
+  else
+    return fail(HGK_ERR_UNSUPPORTED, "%s: output dtype %s for input %s is not implemented "
+                "(output must be the input dtype or f32)",
+                GATED ? "hgk_gated_rms_norm" : "hgk_rms_norm", dtype_name(ydt),
+                dtype_name(xdt));
+  return launch_status(GATED ? "hgk_gated_rms_norm" : "hgk_rms_norm");
+}
+
+int check_common(const char* fn, const void* x, int xdt, int64_t xs, const void* w, int wdt,
+                 void* y, int ydt, int64_t ys, int64_t rows, int64_t n, float eps) {
+  if (rows < 0 || n < 0) return fail(HGK_ERR_ARG, "%s: negative shape rows=%lld n=%lld", fn,
+                                     (long long)rows, (long long)n);
+  if (n > (int64_t)1 << 30) return fail(HGK_ERR_UNSUPPORTED, "%s: n=%lld too large", fn, (long long)n);
+  if (!x || !y) return fail(HGK_ERR_ARG, "%s: null x or y", fn);
+  if (!is_float_dtype(xdt) || !is_float_dtype(ydt))
+    return fail(HGK_ERR_ARG, "%s: x/y dtype must be f32, bf16 or f16 (got %d, %d)", fn, xdt, ydt);
+  if (w && !is_float_dtype(wdt)) return fail(HGK_ERR_ARG, "%s: bad weight dtype %d", fn, wdt);
+  if (rows > 1 && (xs < n || ys < n))
+    return fail(HGK_ERR_ARG, "%s: row strides (%lld, %lld) smaller than n=%lld", fn,
+                (long long)xs, (long long)ys, (long long)n);
+  if (!(eps >= 0.0f)) return fail(HGK_ERR_ARG, "%s: eps must be >= 0", fn);
+  return HGK_OK;
+}
+
+}  // namespace
+}  // namespace hgk
+
+using namespace hgk;
+
+extern "C" int hgk_rms_norm(const void* x, int x_dtype, int64_t x_row_stride, const void* w,
+                            int w_dtype, int w_plus_one, float eps, void* y, int y_dtype,
+                            int64_t y_row_stride, int64_t rows, int64_t n, void* stream) {
+  clear_error();
+  int st = check_common("hgk_rms_norm", x, x_dtype, x_row_stride, w, w_dtype, y, y_dtype,
+                        y_row_stride, rows, n, eps);
+  if (st) return st;
+  if (w_plus_one && !w) return fail(HGK_ERR_ARG, "hgk_rms_norm: w_plus_one needs a weight");
+  if (rows == 0 || n == 0) return HGK_OK;
+  const int w_eff = w ? (w_plus_one ? DT_F32 : w_dtype) : x_dtype;
+  const int t_out = promote(x_dtype, w_eff);
+  if (t_out != x_dtype && t_out != DT_F32)
+    return fail(HGK_ERR_UNSUPPORTED, "hgk_rms_norm: computation type %s not implemented",
+                dtype_name(t_out));
+  NormArgs a{};
+  a.x = x; a.xs = x_row_stride; a.w = w; a.wdt = w_dtype; a.plus_one = w_plus_one ? 1 : 0;
+  a.round_x = (t_out == x_dtype) ? 1 : 0;
+  a.eps = eps; a.inv_n = (float)(1.0 / (double)n);
+  a.y = y; a.ys = y_row_stride; a.rows = rows; a.n = (int)n;
+  a.zg = 1;
+  const int vx = 16 / dtype_bytes(x_dtype);
+  const bool vec_ok = aligned16(x) && aligned16(y) && (!w || aligned16(w)) && n % vx == 0 &&
+                      x_row_stride % vx == 0 && (y_row_stride * dtype_bytes(y_dtype)) % 16 == 0 &&
+                      (n * dtype_bytes(y_dtype)) % 16 == 0;
+  return dispatch<false>(a, x_dtype, y_dtype, vec_ok, as_stream(stream));
+}
+
+extern "C" int hgk_gated_rms_norm(int dtype, const void* x, int64_t x_row_stride, const void* z,
+                                  int64_t z_row_stride, int64_t z_group_rows,
+                                  int64_t z_group_stride, const void* w, int w_dtype, float eps,
+                                  void* out, int out_dtype, int64_t out_row_stride, int64_t rows,
+                                  int64_t n, void* stream) {
+  clear_error();
+  int st = check_common("hgk_gated_rms_norm", x, dtype, x_row_stride, w, w_dtype, out,
+                        out_dtype, out_row_stride, rows, n, eps);
+  if (st) return st;
+  if (!w || !z) return fail(HGK_ERR_ARG, "hgk_gated_rms_norm: null z or weight");
+  if (z_group_rows <= 0 || z_group_rows > rows) {
+    z_group_rows = rows > 0 ? rows : 1;
+    z_group_stride = 0;
+  }
+  if ((z_group_rows > 1 && z_row_stride < n) || z_row_stride < 0 ||
+      (rows > z_group_rows && z_group_stride < (z_group_rows - 1) * z_row_stride + n))
+    return fail(HGK_ERR_ARG, "hgk_gated_rms_norm: z rows overlap (row stride %lld, group %lld x %lld)",
+                (long long)z_row_stride, (long long)z_group_rows, (long long)z_group_stride);
+  if (rows == 0 || n == 0) return HGK_OK;
+  const int t_n = promote(dtype, w_dtype);
+  NormArgs a{};
+  a.x = x; a.xs = x_row_stride; a.z = z; a.zs = z_row_stride; a.zg = z_group_rows;
+  a.zgs = z_group_stride; a.w = w; a.wdt = w_dtype;
+  a.plus_one = 0; a.round_x = (t_n == dtype) ? 1 : 0;
+  a.eps = eps; a.inv_n = (float)(1.0 / (double)n);
+  a.y = out; a.ys = out_row_stride; a.rows = rows; a.n = (int)n;
+  const int vx = 16 / dtype_bytes(dtype);
+  const bool vec_ok = aligned16(x) && aligned16(z) && aligned16(out) && aligned16(w) &&
+                      n % vx == 0 && x_row_stride % vx == 0 && z_row_stride % vx == 0 &&
+                      z_group_stride % vx == 0 &&
+                      (out_row_stride * dtype_bytes(out_dtype)) % 16 == 0 &&
+                      (n * dtype_bytes(out_dtype)) % 16 == 0;
+  return dispatch<true>(a, dtype, out_dtype, vec_ok, as_stream(stream));
+}

@@ -1,0 +1,310 @@
+"""Host-side mirror of the mlx-rs calls higgs-models makes on this path, over
+the C ABI of libhiggs_hip.so. torch supplies device memory and the stream only.
+
+Each function keeps the reference call's name and argument meaning:
+
+    rms_norm(x, weight, eps)                 mlx_rs::fast::rms_norm / nn::RmsNorm
+    rope(x, dims, traditional, base, scale, offset, freqs)
+                                             mlx_rs::fast::rope (utils.rs:16-26)
+    qk_norm_rope(...)                        q_norm/k_norm + transpose + apply_rope
+                                             (transformer.rs:264-287)
+    swiglu(gate, x)                          qwen3_next.rs:275-277
+    silu_mul(gate, up)                       nn::silu(gate) * up (transformer.rs:349-353)
+    gelu_approximate_mul(gate, up)           nn::gelu_approximate(gate) * up (gemma2.rs:422-427)
+    gated_rms_norm(x, z, weight, eps)        swiglu(z, norm(x)) (qwen3_next.rs:1204-1205)
+    QuantizedEmbedding(...).forward(ids)     nn::QuantizedEmbedding / QEmbedding::forward
+
+Errors surface as HgkError (the reference returns Err(Exception::custom(..))).
+Every op enqueues on torch's current CUDA/HIP stream and never synchronises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import math
+from typing import Optional, Sequence
+
+import torch
+
+from ._lib import (ACT_GELU_TANH, ACT_SILU, BF16, F16, F32, I32, U32, HgkError, check,
+                   f32_array, i64_array, lib)
+
+_DT = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16, torch.int32: I32}
+if hasattr(torch, "uint32"):
+    _DT[torch.uint32] = U32
+_TORCH = {F32: torch.float32, BF16: torch.bfloat16, F16: torch.float16}
+
+
+def dtype_code(t: torch.dtype) -> int:
+    try:
+        return _DT[t]
+    except KeyError:
+        raise HgkError(1, f"unsupported dtype {t}") from None
+
+
+def _promote(a: int, b: int) -> int:
+    return a if a == b else F32
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else C.c_void_p(t.data_ptr())
+
+
+def _stream(device: torch.device):
+    return C.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _rows2d(x: torch.Tensor):
+    """View x as [rows, n] with unit stride on n; returns (rows, n, row_stride)."""
+    if x.dim() == 0:
+        raise HgkError(1, "expected at least 1 dimension")
+    n = x.shape[-1]
+    if n > 1 and x.stride(-1) != 1:
+        raise HgkError(1, "last axis must be unit-stride")
+    if x.dim() == 1:
+        return 1, n, n
+    try:
+        x2 = x.view(-1, n)
+    except RuntimeError:
+        raise HgkError(1, "leading axes must collapse to a single row stride") from None
+    return x2.shape[0], n, x2.stride(0)
+
+
+# ---------------------------------------------------------------- RMSNorm
+def rms_norm(x: torch.Tensor, weight: Optional[torch.Tensor], eps: float, *,
+             plus_one: bool = False, out_dtype: Optional[torch.dtype] = None,
+             out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """fast::rms_norm(x, weight, eps) over the last axis. ``plus_one`` applies
+    Gemma's (1 + weight) in f32 (the reference bakes it into the weight at load
+    time, gemma2.rs:799-826). The default output dtype is MLX's promotion of x
+    and the effective weight."""
+    xd = dtype_code(x.dtype)
+    wd = dtype_code(weight.dtype) if weight is not None else xd
+    w_eff = (F32 if plus_one else wd) if weight is not None else xd
+    od = dtype_code(out_dtype) if out_dtype is not None else _promote(xd, w_eff)
+    rows, n, xs = _rows2d(x)
+    if weight is not None and (weight.dim() != 1 or weight.shape[0] != n):
+        raise HgkError(1, f"weight shape {tuple(weight.shape)} does not match ({n},)")
+    if out is None:
+        out = torch.empty(x.shape, dtype=_TORCH[od], device=x.device)
+    _, _, ys = _rows2d(out)
+    check(lib().hgk_rms_norm(_ptr(x), xd, xs, _ptr(weight), wd, int(plus_one), eps,
+                             _ptr(out), od, ys, rows, n, _stream(x.device)))
+    return out
+
+
+def _z_layout(z: torch.Tensor, rows: int, n: int):
+    """(row_stride, group_rows, group_stride) addressing z's rows in place."""
+    try:
+        zr, zn, zs = _rows2d(z)
+        if (zr, zn) == (rows, n):
+            return zs, 0, 0
+    except HgkError:
+        pass
+    if z.dim() >= 3 and z.shape[-1] == n and z.stride(-1) == 1:
+        try:
+            z3 = z.view(-1, z.shape[-2], n)
+        except RuntimeError:
+            raise HgkError(1, "z layout is not expressible as (groups, rows, n)") from None
+        if z3.shape[0] * z3.shape[1] == rows:
+            return z3.stride(1), z3.shape[1], z3.stride(0)
+    raise HgkError(1, f"z shape {tuple(z.shape)} does not match {rows} rows of {n}")
+
+
+def gated_rms_norm(x: torch.Tensor, z: torch.Tensor, weight: torch.Tensor, eps: float, *,
+                   out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """swiglu(z, rms_norm(x, weight, eps)) = z * sigmoid(z) * norm(x).
+
+    z may be a strided view such as the z slice of Qwen3-Next's in_proj_qkvz
+    output viewed as [..., v_per_k, head_v_dim]; it is read in place."""
+    xd = dtype_code(x.dtype)
+    wd = dtype_code(weight.dtype)
+    od = _promote(xd, _promote(xd, wd))
+    rows, n, xs = _rows2d(x)
+    if z.dtype != x.dtype:
+        raise HgkError(1, "z must have x's dtype")
+    zs, zg, zgs = _z_layout(z, rows, n)
+    if out is None:
+        out = torch.empty(x.shape, dtype=_TORCH[od], device=x.device)
+    _, _, os_ = _rows2d(out)
+    check(lib().hgk_gated_rms_norm(xd, _ptr(x), xs, _ptr(z), zs, zg, zgs, _ptr(weight), wd,
+                                   eps, _ptr(out), od, os_, rows, n, _stream(x.device)))
+    return out
+
+
+# ---------------------------------------------------------------- RoPE
+def rope_inv_freq(base: float, dims: int, freqs: Optional[Sequence[float]] = None):
+    inv = (C.c_float * (dims // 2))()
+    fr = None if freqs is None else f32_array(list(freqs))
+    check(lib().hgk_rope_inv_freq(base, dims, fr, inv))
+    return list(inv)
+
+
+def llama3_rope_freqs(base: float, dims: int, factor: float, low_freq_factor: float,
+                      high_freq_factor: float, original_max_position: float):
+    """mlx-lm Llama3RoPE frequency table (pass as ``freqs`` to rope)."""
+    f = (C.c_float * (dims // 2))()
+    check(lib().hgk_llama3_rope_freqs(base, dims, factor, low_freq_factor, high_freq_factor,
+                                      original_max_position, f))
+    return list(f)
+
+
+def _freqs_arg(freqs):
+    if freqs is None:
+        return None
+    if isinstance(freqs, torch.Tensor):
+        freqs = freqs.detach().to("cpu", torch.float32).tolist()
+    return f32_array(list(freqs))
+
+
+def _offsets_arg(offsets, batch, device):
+    if offsets is None:
+        return None, None
+    if not isinstance(offsets, torch.Tensor):
+        offsets = torch.tensor(list(offsets), dtype=torch.int32, device=device)
+    if offsets.dtype != torch.int32 or offsets.device != device or offsets.numel() != batch:
+        raise HgkError(1, f"offsets must be int32[{batch}] on {device}")
+    offsets = offsets.contiguous()
+    return offsets, _ptr(offsets)
+
+
+def rope(x: torch.Tensor, dims: int, traditional: bool = False, base: Optional[float] = 10000.0,
+         scale: float = 1.0, offset: int = 0, freqs=None, *, offsets=None,
+         out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """fast::rope(x, dims, traditional, base, scale, offset, freqs).
+
+    x is [..., L, D] with positions along axis -2, as MLX's rope; leading axes
+    are flattened to [N, ...]. For 4-D x [B, H, L, D] (the reference's
+    post-transpose layout), ``offsets`` (int32[B]) gives each sequence its own
+    offset, replacing forward_batched's per-request loop."""
+    if (freqs is None) == (base is None):
+        raise HgkError(1, "exactly one of base and freqs must be given")
+    if x.dim() < 3:
+        raise HgkError(1, "rope expects at least 3 dimensions")
+    D, L = x.shape[-1], x.shape[-2]
+    if x.dim() == 3:
+        B, H = x.shape[0], 1
+        xs = (x.stride(0), x.stride(1), 0)
+    else:
+        xv = x.reshape(-1, x.shape[-3], L, D) if x.dim() > 4 else x
+        B, H = xv.shape[0], xv.shape[1]
+        xs = (xv.stride(0), xv.stride(2), xv.stride(1))
+        x = xv
+    if out is None:
+        out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    if out.dim() == 3:
+        ys = (out.stride(0), out.stride(1), 0)
+    else:
+        ys = (out.stride(0), out.stride(2), out.stride(1))
+    offs, offs_p = _offsets_arg(offsets, B, x.device)
+    check(lib().hgk_rope(dtype_code(x.dtype), _ptr(x), i64_array(xs), _ptr(out), i64_array(ys),
+                         B, L, H, D, dims, int(traditional), float(base or 0.0), scale,
+                         _freqs_arg(freqs), offset, offs_p, _stream(x.device)))
+    return out
+
+
+def qk_norm_rope(q: torch.Tensor, k: Optional[torch.Tensor], q_norm_w: Optional[torch.Tensor],
+                 k_norm_w: Optional[torch.Tensor], eps: float, dims: int, base: float = 10000.0,
+                 scale: float = 1.0, offset: int = 0, freqs=None, *, offsets=None,
+                 q_out: Optional[torch.Tensor] = None,
+                 k_out: Optional[torch.Tensor] = None):
+    """Per-head RMSNorm + RoPE for q [B, L, Hq, D] and k [B, L, Hk, D] (the
+    projection layout, any strides with unit D stride). Outputs default to the
+    reference's post-transpose [B, H, L, D] contiguous layout."""
+    B, L, Hq, D = q.shape
+    wd = dtype_code(q_norm_w.dtype if q_norm_w is not None else
+                    (k_norm_w.dtype if k_norm_w is not None else q.dtype))
+    if q_out is None:
+        q_out = torch.empty((B, Hq, L, D), dtype=q.dtype, device=q.device)
+    qos = (q_out.stride(0), q_out.stride(2), q_out.stride(1))
+    Hk = 0
+    ks = kos = (0, 0, 0)
+    if k is not None:
+        Hk = k.shape[2]
+        if k_out is None:
+            k_out = torch.empty((B, Hk, L, D), dtype=k.dtype, device=k.device)
+        ks = (k.stride(0), k.stride(1), k.stride(2))
+        kos = (k_out.stride(0), k_out.stride(2), k_out.stride(1))
+    offs, offs_p = _offsets_arg(offsets, B, q.device)
+    qs = (q.stride(0), q.stride(1), q.stride(2))
+    check(lib().hgk_qk_norm_rope(
+        dtype_code(q.dtype), _ptr(q), i64_array(qs), _ptr(q_out), i64_array(qos), Hq,
+        _ptr(q_norm_w), _ptr(k), i64_array(ks), _ptr(k_out), i64_array(kos), Hk,
+        _ptr(k_norm_w), wd, eps, B, L, D, dims, float(base or 0.0), scale,
+        _freqs_arg(freqs), offset, offs_p, _stream(q.device)))
+    return q_out, k_out
+
+
+# ---------------------------------------------------------------- GLU
+def _glu(act: int, gate: torch.Tensor, up: torch.Tensor, out_dtype, out):
+    if gate.shape != up.shape or gate.dtype != up.dtype:
+        raise HgkError(1, "gate and up must match in shape and dtype")
+    xd = dtype_code(gate.dtype)
+    od = dtype_code(out_dtype) if out_dtype is not None else xd
+    rows, n, gs = _rows2d(gate)
+    _, _, us = _rows2d(up)
+    if out is None:
+        out = torch.empty(gate.shape, dtype=_TORCH[od], device=gate.device)
+    _, _, os_ = _rows2d(out)
+    check(lib().hgk_glu(act, xd, _ptr(gate), gs, _ptr(up), us, _ptr(out), od, os_, rows, n,
+                        _stream(gate.device)))
+    return out
+
+
+def silu_mul(gate, up, *, out_dtype=None, out=None):
+    """nn::silu(gate) * up (transformer.rs:349-353)."""
+    return _glu(ACT_SILU, gate, up, out_dtype, out)
+
+
+def swiglu(gate, x, *, out=None):
+    """swiglu(gate, x) = gate * sigmoid(gate) * x (qwen3_next.rs:275-277)."""
+    return _glu(ACT_SILU, gate, x, None, out)
+
+
+def gelu_approximate_mul(gate, up, *, out_dtype=None, out=None):
+    """nn::gelu_approximate(gate) * up (gemma2.rs:422-427)."""
+    return _glu(ACT_GELU_TANH, gate, up, out_dtype, out)
+
+
+def fused_gate_up_swiglu(gate_up: torch.Tensor, *, out=None):
+    """phi3-style fused projection [.., 2I]: silu(first half) * second half
+    (phi3.rs:261-265), read in place through row strides."""
+    I2 = gate_up.shape[-1]
+    return _glu(ACT_SILU, gate_up[..., : I2 // 2], gate_up[..., I2 // 2:], None, out)
+
+
+# ---------------------------------------------------------------- embedding
+class QuantizedEmbedding:
+    """nn::QuantizedEmbedding: 4-bit affine table (weight u32 [V, H/8], scales
+    and biases [V, H/group] in bf16/f16). forward(ids) gathers and
+    dequantizes only the requested rows; out_scale applies Gemma's
+    bf16(sqrt(H)) embedding scale in the same pass (gemma2.rs:587-600)."""
+
+    def __init__(self, weight: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
+                 group_size: int = 64, bits: int = 4):
+        if weight.dtype not in (torch.int32, getattr(torch, "uint32", torch.int32)):
+            raise HgkError(1, "weight must hold packed 32-bit words")
+        self.weight, self.scales, self.biases = weight, scales, biases
+        self.group_size, self.bits = group_size, bits
+        self.vocab = weight.shape[0]
+        self.hidden = weight.shape[1] * 32 // bits
+
+    def forward(self, ids: torch.Tensor, *, out_scale: float = 0.0,
+                out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        idd = dtype_code(ids.dtype)
+        sd = dtype_code(self.scales.dtype)
+        flat = ids.reshape(-1).contiguous()
+        if out is None:
+            out = torch.empty((flat.numel(), self.hidden), dtype=_TORCH[sd], device=ids.device)
+        check(lib().hgk_quantized_embedding(
+            _ptr(flat), idd, flat.numel(), _ptr(self.weight), _ptr(self.scales),
+            _ptr(self.biases), sd, self.vocab, self.hidden, self.group_size, self.bits,
+            out_scale, _ptr(out), out.stride(0), _stream(ids.device)))
+        return out.reshape(*ids.shape, self.hidden)
+
+    __call__ = forward
+
+
+def gemma_embed_scale(hidden: int) -> float:
+    """sqrt(hidden) as the reference computes it (f32), before the cast to the
+    activation dtype that the kernel applies."""
+    return float(math.sqrt(float(hidden)))

@@ -1,0 +1,192 @@
+/*
+ * higgs_hip.h -- C ABI of the MI355X (gfx950) per-layer op library
+ * (libhiggs_hip.so). This is the drop-in boundary for the ops that
+ * panbanda/higgs' higgs-models crate calls through mlx-rs; each entry point
+ * names the reference call it replaces.
+ *
+ * Conventions (all entry points):
+ *  - Device pointers in, device pointers out; the caller owns every buffer and
+ *    pre-sizes every output. Nothing here allocates device memory or retains a
+ *    pointer after returning.
+ *  - Sizes and strides are int64 counts of ELEMENTS. The last (innermost) axis
+ *    is always unit-stride.
+ *  - `stream` is a hipStream_t (NULL = the default stream). Work is enqueued
+ *    on it; no entry point synchronises.
+ *  - Return value: HGK_OK (0) or an error status; hgk_last_error() gives a
+ *    thread-local message for the last failure on the calling thread. Invalid
+ *    arguments never reach the GPU.
+ *  - Floating-point results follow MLX's CPU-device composition of each op,
+ *    including its intermediate roundings to the activation dtype.
+ */
+#ifndef HIGGS_HIP_H
+#define HIGGS_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+  HGK_F32 = 0,
+  HGK_BF16 = 1,
+  HGK_F16 = 2,
+  HGK_U32 = 3,
+  HGK_I32 = 4
+} hgk_dtype;
+
+typedef enum {
+  HGK_OK = 0,
+  HGK_ERR_ARG = 1,         /* null pointer, bad shape / stride / dtype */
+  HGK_ERR_UNSUPPORTED = 2, /* valid request this build does not implement */
+  HGK_ERR_HIP = 3          /* HIP launch / runtime error */
+} hgk_status;
+
+typedef enum { HGK_ACT_SILU = 0, HGK_ACT_GELU_TANH = 1 } hgk_act;
+
+#define HGK_ABI_VERSION 1
+
+/* Error message of the last failed call on this thread ("" if none).
+ * Mirrors the mlx_set_error_handler last-error convention at
+ * crates/higgs-models/src/qwen3_next.rs:28-51. */
+const char* hgk_last_error(void);
+
+/* HGK_ABI_VERSION of the loaded library. */
+int hgk_abi_version(void);
+
+/*
+ * RMSNorm over the last axis of x[rows, n]:
+ *   y = w' * round_T(x * rsqrt(mean(x^2) + eps)),  T = promote(x, w')
+ * Replaces mlx_rs::fast::rms_norm as called by nn::RmsNorm::forward
+ * (crates/higgs-models/src/transformer.rs:407,415,525;
+ *  qwen3_next.rs:1518,1540,1547; qwen3_moe.rs:385,389,509; gemma2.rs:491-503).
+ * w may be NULL (no weight). w_plus_one != 0 applies Gemma's (1 + w) in f32,
+ * exactly the weight that apply_rmsnorm_plus_one (gemma2.rs:799-826) bakes in
+ * at load time; the computation type is then f32. y_dtype may differ from the
+ * computation type (the result is rounded to it). Also serves the Qwen3
+ * q_norm/k_norm (transformer.rs:264-269) when they are not fused with RoPE:
+ * rows = tokens*heads, n = head_dim.
+ */
+int hgk_rms_norm(const void* x, int x_dtype, int64_t x_row_stride,
+                 const void* w, int w_dtype, int w_plus_one, float eps,
+                 void* y, int y_dtype, int64_t y_row_stride,
+                 int64_t rows, int64_t n, void* stream);
+
+/*
+ * Host helper: the dims/2 inverse frequencies fast::rope uses,
+ *   inv[i] = freqs ? 1/freqs[i] : exp(-i * log(base) / (dims/2)).
+ * Mirrors the frequency derivation inside mlx_rs::fast::rope
+ * (utils.rs:17-25; deepseek_v2.rs:222-225 for explicit freqs).
+ */
+int hgk_rope_inv_freq(float base, int dims, const float* freqs, float* inv_freq_out);
+
+/*
+ * Host helper: llama3 rope_scaling frequency table (mlx-lm Llama3RoPE), the
+ * `rope_scaling` block that transformer.rs:91-92 parses. Pass the result as
+ * `freqs` to hgk_rope / hgk_qk_norm_rope.
+ */
+int hgk_llama3_rope_freqs(float base, int dims, float factor, float low_freq_factor,
+                          float high_freq_factor, float original_max_position,
+                          float* freqs_out);
+
+/*
+ * RoPE (non-traditional / NeoX half split) over a heads tensor viewed as
+ * [batch, seq_len, heads, head_dim]; element (b,l,h,d) is at
+ * x + b*x_strides[0] + l*x_strides[1] + h*x_strides[2] + d, likewise y.
+ * Position of (b,l) = (offsets ? offsets[b] : offset) + l, times `scale`.
+ * Rotates dims [0, dims) (partial rotary when dims < head_dim); the rest is
+ * copied unchanged. freqs: optional HOST array of dims/2 frequencies (else
+ * `base`). offsets: optional DEVICE int32[batch] (per-sequence offsets).
+ * Replaces mlx_rs::fast::rope via apply_rope (utils.rs:16-26) at
+ * transformer.rs:277-287, gemma2.rs:246-256, qwen3_moe.rs:194-204,
+ * qwen3_next.rs:754-756 and the per-request loop of forward_batched
+ * (transformer.rs:747-802). Only traditional == 0 is implemented (the
+ * setting every in-scope model uses). y may alias x when both have the same
+ * strides.
+ */
+int hgk_rope(int dtype, const void* x, const int64_t x_strides[3],
+             void* y, const int64_t y_strides[3],
+             int64_t batch, int64_t seq_len, int64_t heads, int64_t head_dim,
+             int dims, int traditional, float base, float scale, const float* freqs,
+             int32_t offset, const int32_t* offsets, void* stream);
+
+/*
+ * Qwen3 per-head q/k RMSNorm fused with RoPE, for q and (optionally) k in one
+ * launch: y = rope(rms_norm(x, norm_w, eps)) per head row; a NULL norm weight
+ * skips the norm for that tensor. Layouts as in hgk_rope, so the [B,L,H,D]
+ * projection output can be read and [B,H,L,D] written directly (the
+ * transpose at transformer.rs:271-275 is folded in). norm weights have
+ * norm_w_dtype == dtype. k may be NULL (k_heads == 0).
+ * Replaces q_norm/k_norm + transpose + apply_rope at transformer.rs:264-287
+ * (and 730-735 + 747-802 in forward_batched), qwen3_moe.rs:170-204 and
+ * qwen3_next.rs:741-756 (strided q view, partial rotary).
+ */
+int hgk_qk_norm_rope(int dtype,
+                     const void* q, const int64_t q_strides[3],
+                     void* q_out, const int64_t q_out_strides[3],
+                     int64_t q_heads, const void* q_norm_w,
+                     const void* k, const int64_t k_strides[3],
+                     void* k_out, const int64_t k_out_strides[3],
+                     int64_t k_heads, const void* k_norm_w,
+                     int norm_w_dtype, float eps,
+                     int64_t batch, int64_t seq_len, int64_t head_dim,
+                     int dims, float base, float scale, const float* freqs,
+                     int32_t offset, const int32_t* offsets, void* stream);
+
+/*
+ * Gated linear unit over rows: out = act(gate) * up.
+ *   HGK_ACT_SILU:      swiglu / nn::silu(gate) * up   (transformer.rs:349-353,
+ *                      qwen3_next.rs:275-277 used at 809 and 886,
+ *                      qwen3_moe.rs:338, phi3.rs:261-265)
+ *   HGK_ACT_GELU_TANH: nn::gelu_approximate(gate) * up (gemma2.rs:422-427)
+ * A fused gate_up projection [rows, 2n] is passed as gate = p, up = p + n,
+ * both with row stride 2n.
+ */
+int hgk_glu(int act, int dtype, const void* gate, int64_t gate_row_stride,
+            const void* up, int64_t up_row_stride,
+            void* out, int out_dtype, int64_t out_row_stride,
+            int64_t rows, int64_t n, void* stream);
+
+/*
+ * Qwen3-Next gated RMSNorm: out = z * sigmoid(z) * rms_norm(x, w, eps), i.e.
+ * swiglu(z, norm(y)) at qwen3_next.rs:1204-1205 (norm built at 1062-1064).
+ * rows = tokens*value_heads, n = head_v_dim. Row r of z starts at
+ *   z + (r / z_group_rows) * z_group_stride + (r % z_group_rows) * z_row_stride
+ * so z can be read in place from the in_proj_qkvz output, where each key
+ * head's block holds v_per_k value-head rows of z (qwen3_next.rs:1214-1265:
+ * z_group_rows = v_per_k, z_row_stride = head_v_dim, z_group_stride = the
+ * per-key-head block width). z_group_rows <= 0 means one group (uniform
+ * z_row_stride).
+ */
+int hgk_gated_rms_norm(int dtype, const void* x, int64_t x_row_stride,
+                       const void* z, int64_t z_row_stride,
+                       int64_t z_group_rows, int64_t z_group_stride,
+                       const void* w, int w_dtype, float eps,
+                       void* out, int out_dtype, int64_t out_row_stride,
+                       int64_t rows, int64_t n, void* stream);
+
+/*
+ * Affine-quantized embedding gather + dequantize:
+ *   out[t, k] = s * q + b,  q = nibble (k % 8) of w_q[id, k/8] (low first),
+ *   s, b = scales/biases[id, k/group_size], id = ids[t];
+ * then, if out_scale != 0, out *= round(out_scale) (Gemma's sqrt(hidden)
+ * embedding scale, gemma2.rs:587-600). Output dtype = scales_dtype.
+ * Replaces nn::QuantizedEmbedding::forward (transformer.rs:494, gemma2.rs:588)
+ * and QEmbedding::forward = dequantize(...).take_axis(ids, 0)
+ * (qwen3_next.rs:248-257, qwen3_moe.rs:402-416) without dequantizing the
+ * table. ids are int32 (negative counts from the end) or uint32; an id outside
+ * [0, vocab) yields a zero row. Implemented: bits == 4, group_size in
+ * {32, 64, 128}.
+ */
+int hgk_quantized_embedding(const void* ids, int ids_dtype, int64_t n_ids,
+                            const uint32_t* w_q, const void* scales,
+                            const void* biases, int scales_dtype,
+                            int64_t vocab, int64_t hidden, int group_size, int bits,
+                            float out_scale, void* out, int64_t out_row_stride,
+                            void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HIGGS_HIP_H */

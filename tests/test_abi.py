@@ -1,0 +1,127 @@
+"""The C ABI without a GPU: the library loads, exports exactly what
+include/higgs_hip.h declares, its host-side helpers agree with the oracle bit
+for bit, and invalid arguments come back as error statuses with a message
+(validation runs before any HIP call, so none of this touches a device)."""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+import oracle as O
+from higgs_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "higgs_hip.h")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(hgk_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.lib()
+    declared = header_functions()
+    assert declared, "no declarations parsed"
+    for name in declared:
+        assert hasattr(L, name), f"{name} missing from {_lib.LIB_PATH}"
+    assert sorted(_lib.PROTOTYPES) == declared, "ctypes prototypes drift from the header"
+    nm = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True,
+                        text=True, check=True).stdout
+    exported = sorted(set(re.findall(r"\b(hgk_\w+)$", nm, flags=re.M)))
+    assert exported == declared, f"exported {exported} != declared {declared}"
+
+
+def test_abi_version():
+    assert _lib.lib().hgk_abi_version() == 1
+
+
+@pytest.mark.parametrize("base,dims", [(500000.0, 64), (1e6, 128), (1e4, 256), (1e7, 64),
+                                       (10000.0, 80)])
+def test_inv_freq_helper_matches_oracle_bitexact(base, dims):
+    got = (C.c_float * (dims // 2))()
+    _lib.check(_lib.lib().hgk_rope_inv_freq(base, dims, None, got))
+    assert np.array_equal(np.frombuffer(got, np.float32), O.rope_inv_freq(base, dims))
+
+
+def test_llama3_helper_matches_oracle_bitexact():
+    for args in ((500000.0, 64, 32.0, 1.0, 4.0, 8192.0), (500000.0, 128, 8.0, 1.0, 4.0, 8192.0)):
+        got = (C.c_float * (args[1] // 2))()
+        _lib.check(_lib.lib().hgk_llama3_rope_freqs(*args, got))
+        ref = O.llama3_freqs(*args)
+        assert np.array_equal(np.frombuffer(got, np.float32), ref)
+        inv = (C.c_float * (args[1] // 2))()
+        _lib.check(_lib.lib().hgk_rope_inv_freq(0.0, args[1], got, inv))
+        assert np.array_equal(np.frombuffer(inv, np.float32), O.rope_inv_freq(0.0, args[1], ref))
+
+
+def _status(fn, *args):
+    st = fn(*args)
+    return st, _lib.lib().hgk_last_error().decode()
+
+
+def test_error_paths_return_status_and_message():
+    L = _lib.lib()
+    fake = C.c_void_p(0x1000)  # never dereferenced: every call below fails validation
+    st, msg = _status(L.hgk_rms_norm, None, 1, 8, None, 1, 0, 1e-5, fake, 1, 8, 4, 8, None)
+    assert st == _lib.ERR_ARG and "null" in msg
+    st, msg = _status(L.hgk_rms_norm, fake, 7, 8, None, 1, 0, 1e-5, fake, 1, 8, 4, 8, None)
+    assert st == _lib.ERR_ARG and "dtype" in msg
+    st, msg = _status(L.hgk_rms_norm, fake, 1, 4, None, 1, 0, 1e-5, fake, 1, 8, 4, 8, None)
+    assert st == _lib.ERR_ARG and "stride" in msg
+    st, msg = _status(L.hgk_rms_norm, fake, 1, 8, None, 1, 1, 1e-5, fake, 1, 8, 4, 8, None)
+    assert st == _lib.ERR_ARG and "plus_one" in msg
+    st, msg = _status(L.hgk_rms_norm, fake, 1, 8, None, 1, 0, 1e-5, fake, 2, 8, 4, 8, None)
+    assert st == _lib.ERR_UNSUPPORTED
+    strides = _lib.i64_array([64, 64, 64])
+    st, msg = _status(L.hgk_rope, 1, fake, strides, fake, strides, 1, 1, 1, 64, 64, 1,
+                      1e4, 1.0, None, 0, None, None)
+    assert st == _lib.ERR_UNSUPPORTED and "traditional" in msg
+    st, msg = _status(L.hgk_rope, 1, fake, strides, fake, strides, 1, 1, 1, 64, 65, 0,
+                      1e4, 1.0, None, 0, None, None)
+    assert st == _lib.ERR_ARG and "dims" in msg
+    st, msg = _status(L.hgk_rope, 1, fake, None, fake, strides, 1, 1, 1, 64, 64, 0,
+                      1e4, 1.0, None, 0, None, None)
+    assert st == _lib.ERR_ARG
+    st, msg = _status(L.hgk_qk_norm_rope, 1, fake, strides, fake, strides, 1, fake,
+                      None, None, None, None, 0, None, 0, 1e-6, 1, 1, 64, 64, 1e4, 1.0, None,
+                      0, None, None)
+    assert st == _lib.ERR_UNSUPPORTED and "weight dtype" in msg
+    st, msg = _status(L.hgk_glu, 5, 1, fake, 8, fake, 8, fake, 1, 8, 1, 8, None)
+    assert st == _lib.ERR_ARG and "activation" in msg
+    st, msg = _status(L.hgk_glu, 0, 1, fake, 8, fake, 8, fake, 2, 8, 1, 8, None)
+    assert st == _lib.ERR_UNSUPPORTED
+    st, msg = _status(L.hgk_gated_rms_norm, 1, fake, 128, None, 128, 0, 0, fake, 1, 1e-6,
+                      fake, 1, 128, 4, 128, None)
+    assert st == _lib.ERR_ARG
+    st, msg = _status(L.hgk_gated_rms_norm, 1, fake, 128, fake, 128, 2, 128, fake, 1, 1e-6,
+                      fake, 1, 128, 4, 128, None)
+    assert st == _lib.ERR_ARG and "overlap" in msg
+    st, msg = _status(L.hgk_quantized_embedding, fake, 4, 4, fake, fake, fake, 1, 10, 2048,
+                      64, 8, 0.0, fake, 2048, None)
+    assert st == _lib.ERR_UNSUPPORTED and "bits" in msg
+    st, msg = _status(L.hgk_quantized_embedding, fake, 4, 4, fake, fake, fake, 1, 10, 2048,
+                      48, 4, 0.0, fake, 2048, None)
+    assert st == _lib.ERR_UNSUPPORTED
+    st, msg = _status(L.hgk_quantized_embedding, fake, 1, 4, fake, fake, fake, 1, 10, 2048,
+                      64, 4, 0.0, fake, 2048, None)
+    assert st == _lib.ERR_ARG and "ids" in msg
+    # empty problems succeed without launching anything
+    assert L.hgk_rms_norm(fake, 1, 8, None, 1, 0, 1e-5, fake, 1, 8, 0, 8, None) == 0
+    assert L.hgk_glu(0, 1, fake, 8, fake, 8, fake, 1, 8, 0, 8, None) == 0
+    assert L.hgk_quantized_embedding(fake, 4, 0, fake, fake, fake, 1, 10, 2048, 64, 4, 0.0,
+                                     fake, 2048, None) == 0
+    assert _lib.lib().hgk_last_error() == b""
+
+
+def test_python_mirror_raises_on_missing_library(monkeypatch, tmp_path):
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "LIB_PATH", str(tmp_path / "missing.so"))
+    with pytest.raises(_lib.HgkError):
+        _lib.lib()

@@ -1,0 +1,392 @@
+"""Pins for the CPU oracle (no GPU). Each check compares the oracle with
+something it does not compute itself: the reference's own known answers,
+numpy/torch float64 mathematics, IEEE conversions done by numpy/torch, closed
+forms and invariants. Sizes keep the whole file to a few seconds."""
+from __future__ import annotations
+
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from bits import assert_close, exact_frac, ulp_dist
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def bf16_bits_torch(a_f32: np.ndarray) -> np.ndarray:
+    t = torch.from_numpy(np.ascontiguousarray(a_f32, np.float32)).to(torch.bfloat16)
+    return t.view(torch.int16).numpy().view(np.uint16)
+
+
+def from_bf16_bits(b: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(b, np.uint16).view(np.int16)).view(torch.bfloat16)
+
+
+# ------------------------------------------------------------------ conversions
+def test_bf16_rounding_matches_torch():
+    x = O.normal(11, (200_000,)) * np.float32(3.0)
+    edge = np.array([0.0, -0.0, 1.0, 1.00390625, 1.005859375, 1.0078125, 3.3895314e38,
+                     3.4e38, -3.4e38, 1e-39, -1e-40, 1e-45, np.inf, -np.inf], np.float32)
+    # exact halfway cases between neighbouring bf16 values
+    halves = (np.arange(1, 2000, dtype=np.uint32) << 16) | 0x8000
+    x = np.concatenate([x, edge, halves.view(np.float32)])
+    assert np.array_equal(O.from_f32(x, O.BF16), bf16_bits_torch(x))
+
+
+def test_f16_rounding_matches_numpy():
+    x = O.normal(12, (200_000,)) * np.float32(300.0)
+    edge = np.array([65504.0, 65519.9, 65520.0, 70000.0, 6.1e-5, 5.96e-8, 2.98e-8, 2.99e-8,
+                     1e-9, -0.0, np.inf], np.float32)
+    x = np.concatenate([x, edge, O.normal(13, (10_000,)) * np.float32(1e-5)])
+    assert np.array_equal(O.from_f32(x, O.F16), x.astype(np.float16).view(np.uint16))
+    back = O.to_f32(x.astype(np.float16).view(np.uint16), O.F16)
+    assert np.array_equal(back, x.astype(np.float16).astype(np.float32))
+
+
+# ------------------------------------------------------------------ MLX math
+def test_mlx_exp_accuracy_and_specials():
+    L = O.lib()
+    xs = np.concatenate([np.linspace(-87.0, 87.9, 40_001), np.linspace(-2, 2, 4001)])
+    got = np.array([L.or_mlx_exp(float(v)) for v in xs.astype(np.float32)], np.float64)
+    ref = np.exp(xs.astype(np.float32).astype(np.float64))
+    rel = np.abs(got - ref) / ref
+    # MLX's polynomial exp: the f32 product x*1.442695f carries an absolute
+    # error up to ulp(x*log2 e)/2, i.e. ~|x| * 2^-24 * 1.44 relative; near 0 it
+    # is within a few f32 ulps. A wrong polynomial coefficient breaks both.
+    small = np.abs(xs) <= 2
+    assert rel[small].max() < 4 * 2.0 ** -23, rel[small].max()
+    bound = 3e-7 + np.abs(xs.astype(np.float32).astype(np.float64)) * 1.5 * 2.0 ** -23
+    assert np.all(rel <= bound), (rel / bound).max()
+    assert L.or_mlx_exp(0.0) == 1.0
+    # 2^int is built in the exponent field, so once int(x*log2 e + 0.5) reaches
+    # -127 the result is 0 instead of a subnormal
+    assert L.or_mlx_exp(-87.9) == 0.0 and L.or_mlx_exp(-87.5) > 0.0
+    assert L.or_mlx_exp(89.0) == math.inf
+    assert L.or_mlx_exp(-89.0) == 0.0
+    assert math.isnan(L.or_mlx_exp(float("nan")))
+
+
+def test_mlx_sigmoid_matches_float64():
+    L = O.lib()
+    xs = np.linspace(-30, 30, 60_001).astype(np.float32)
+    got = np.array([L.or_mlx_sigmoid(float(v)) for v in xs], np.float64)
+    ref = 1.0 / (1.0 + np.exp(-xs.astype(np.float64)))
+    assert np.abs(got - ref).max() < 2e-7
+    # relative error in the left tail is exp's (|x| * 1.5 * 2^-23 at most)
+    bound = (3e-7 + np.abs(xs.astype(np.float64)) * 1.5 * 2.0 ** -23) * ref + 2.0 ** -25
+    assert np.all(np.abs(got - ref) <= bound)
+    assert L.or_mlx_sigmoid(0.0) == 0.5
+
+
+# ------------------------------------------------------------------ SwiGLU
+def _glu_f32(act, g, u):
+    g = np.ascontiguousarray(g, np.float32).reshape(1, -1)
+    u = np.ascontiguousarray(u, np.float32).reshape(1, -1)
+    return O.glu(act, g, u, O.F32)[0]
+
+
+def test_swiglu_reference_known_answers():
+    ka = json.load(open(os.path.join(GOLDEN, "reference_known_answers.json")))
+    for c in ka["swiglu_numeric_correctness"]["cases"]:
+        got = _glu_f32(O.ACT_SILU, [c["gate"]], [c["x"]])[0]
+        assert abs(got - c["expected"]) < c["tol"], (c, got)
+    s = ka["swiglu_shape"]
+    got = _glu_f32(O.ACT_SILU, s["gate"][0], s["x"][0])
+    assert got.shape == (3,) and got[0] > s["first_greater_than"]
+
+
+def test_silu_f32_matches_torch_float64():
+    g = O.normal(21, (64, 512)) * np.float32(4)
+    u = O.normal(22, (64, 512))
+    got = O.glu(O.ACT_SILU, g, u, O.F32)
+    ref = (torch.nn.functional.silu(torch.from_numpy(g).double()) * torch.from_numpy(u).double()).numpy()
+    np.testing.assert_allclose(got, ref, rtol=2e-6, atol=1e-7)
+
+
+def test_gelu_tanh_f32_matches_torch_float64():
+    g = O.normal(23, (64, 512)) * np.float32(3)
+    u = O.normal(24, (64, 512))
+    got = O.glu(O.ACT_GELU_TANH, g, u, O.F32)
+    ref = (torch.nn.functional.gelu(torch.from_numpy(g).double(), approximate="tanh") *
+           torch.from_numpy(u).double()).numpy()
+    # the reference formula 0.5*g*(1+tanh(.)) cancels in f32 for g << 0
+    np.testing.assert_allclose(got, ref, rtol=1e-5, atol=2e-6)
+
+
+def test_silu_bf16_rounding_sequence_matches_torch_ops():
+    """MLX's composition sig=bf16(sigmoid(g)); s=bf16(g*sig); out=bf16(s*u)
+    restated with torch's bf16 ops (each computes in f32 and rounds)."""
+    g = O.from_f32(O.normal(25, (256, 512)) * np.float32(3), O.BF16)
+    u = O.from_f32(O.normal(26, (256, 512)), O.BF16)
+    got = O.glu(O.ACT_SILU, g, u, O.BF16)
+    tg, tu = from_bf16_bits(g), from_bf16_bits(u)
+    ref = (tg * torch.sigmoid(tg)) * tu
+    ref_bits = ref.view(torch.int16).numpy().view(np.uint16)
+    # torch's sigmoid uses a different exp: rare one-ulp flips only
+    assert exact_frac(got, ref_bits, O.BF16) > 0.999
+    assert ulp_dist(got, ref_bits, O.BF16).max() <= 1
+    # dropping the intermediate roundings is a different function
+    fused = bf16_bits_torch((tg.float() * torch.sigmoid(tg.float()) * tu.float()).numpy())
+    assert exact_frac(got, fused, O.BF16) < 0.99
+
+
+# ------------------------------------------------------------------ RMSNorm
+def test_rms_norm_f32_matches_float64():
+    x = O.normal(31, (64, 2048))
+    w = O.normal(32, (2048,), 1.0, 0.02)
+    got = O.rms_norm(x, O.F32, w, O.F32, 1e-5)
+    xd = x.astype(np.float64)
+    ref = xd / np.sqrt((xd * xd).mean(-1, keepdims=True) + 1e-5) * w.astype(np.float64)
+    np.testing.assert_allclose(got, ref, rtol=1e-5)
+
+
+def test_rms_norm_constant_row_closed_form():
+    for c in (0.5, -3.0, 1e-3):
+        x = np.full((3, 512), c, np.float32)
+        w = O.normal(33, (512,), 1.0, 0.02)
+        got = O.rms_norm(x, O.F32, w, O.F32, 1e-6)
+        ref = w.astype(np.float64) * c / math.sqrt(c * c + 1e-6)
+        np.testing.assert_allclose(got, np.broadcast_to(ref, got.shape), rtol=4e-7)
+    z = O.rms_norm(np.zeros((2, 64), np.float32), O.F32, None, O.F32, 1e-5)
+    assert not z.any()
+
+
+def test_rms_norm_bf16_rounding_sequence_matches_torch_ops():
+    """astype(f32) -> x*rsqrt(mean(x^2)+eps) -> astype(bf16) -> * w (bf16)."""
+    x = O.from_f32(O.normal(34, (512, 2048)), O.BF16)
+    w = O.from_f32(O.normal(35, (2048,), 1.0, 0.02), O.BF16)
+    got = O.rms_norm(x, O.BF16, w, O.BF16, 1e-5)
+    tx, tw = from_bf16_bits(x), from_bf16_bits(w)
+    xf = tx.float()
+    r = torch.rsqrt((xf * xf).mean(-1, keepdim=True) + 1e-5)
+    ref = ((xf * r).to(torch.bfloat16) * tw).view(torch.int16).numpy().view(np.uint16)
+    # torch sums in f32 pairwise: a one-bit change in r can flip the bf16 cast
+    # of x*r, which the second rounding (after * w) can widen to 2 ulp
+    assert exact_frac(got, ref, O.BF16) > 0.998
+    assert ulp_dist(got, ref, O.BF16).max() <= 2
+    single = bf16_bits_torch((xf * r * tw.float()).numpy())
+    assert exact_frac(got, single, O.BF16) < 0.99  # the cast before * w matters
+
+
+def test_gemma_plus_one_is_f32_weight_shift():
+    x = O.from_f32(O.normal(36, (64, 3584)), O.BF16)
+    w = O.from_f32(O.normal(37, (3584,), 0.0, 0.02), O.BF16)
+    got = O.rms_norm(x, O.BF16, w, O.BF16, 1e-6, plus_one=True)
+    assert got.dtype == np.float32  # promoted by the f32 shift (gemma2.rs:802)
+    w1 = O.to_f32(w, O.BF16) + np.float32(1.0)
+    same = O.rms_norm(x, O.BF16, w1, O.F32, 1e-6)
+    assert np.array_equal(got, same)
+    xd = O.to_f32(x, O.BF16).astype(np.float64)
+    ref = xd / np.sqrt((xd * xd).mean(-1, keepdims=True) + 1e-6) * w1.astype(np.float64)
+    np.testing.assert_allclose(got, ref, rtol=1e-5)
+
+
+# ------------------------------------------------------------------ RoPE
+def _rope_ref64(x, inv, pos):
+    """float64 NeoX rotation of x[..., D] at positions pos (broadcast)."""
+    half = inv.size
+    th = pos[..., None].astype(np.float64) * inv.astype(np.float64)
+    c, s = np.cos(th), np.sin(th)
+    x1, x2 = x[..., :half].astype(np.float64), x[..., half:2 * half].astype(np.float64)
+    return np.concatenate([x1 * c - x2 * s, x1 * s + x2 * c, x[..., 2 * half:]], -1)
+
+
+def test_default_inv_freq_matches_closed_form():
+    for base, dims in ((500000.0, 64), (1e6, 128), (1e4, 256), (1e7, 64)):
+        inv = O.rope_inv_freq(base, dims)
+        ref = base ** (-np.arange(dims // 2) / (dims / 2))
+        # MLX's polynomial exp of arguments down to -ln(base) (~-16)
+        np.testing.assert_allclose(inv, ref, rtol=4e-6)
+        assert inv[0] == 1.0
+
+
+def test_llama3_freq_bands():
+    f = O.llama3_freqs(500000.0, 64, 32.0, 1.0, 4.0, 8192.0)
+    e = np.arange(0, 64, 2, dtype=np.float32) / np.float32(64)
+    plain = np.array([np.float32(500000.0) ** v for v in e], np.float32)
+    wl = 2 * np.pi * plain.astype(np.float64)
+    hi = wl < 2048            # high-frequency band: unchanged
+    lo = wl > 8192            # low-frequency band: exactly x factor
+    mid = ~hi & ~lo
+    assert hi[:15].all() and lo[18:].all() and mid[15:18].all()
+    np.testing.assert_allclose(f[hi], plain[hi], rtol=2e-7)
+    np.testing.assert_allclose(f[lo], plain[lo] * 32.0, rtol=2e-7)
+    sm = (8192.0 / wl[mid] - 1.0) / 3.0
+    np.testing.assert_allclose(f[mid], plain[mid] / ((1 - sm) / 32.0 + sm), rtol=1e-5)
+
+
+def test_rope_f32_matches_float64_and_invariants():
+    B, L, H, D = 2, 33, 3, 128
+    x = O.normal(41, (B, L, H, D))
+    inv = O.rope_inv_freq(1e6, D)
+    y = O.norm_rope(x, O.F32, dims=D, inv_freq=inv, offset=5)
+    pos = (np.arange(L) + 5.0)[None, :, None]
+    ref = _rope_ref64(x, inv, np.broadcast_to(pos, (B, L, H)))
+    np.testing.assert_allclose(y, ref, rtol=1e-5, atol=2e-5)
+    # the rotation preserves each (x1_i, x2_i) pair's norm
+    h = D // 2
+    n0 = x[..., :h].astype(np.float64) ** 2 + x[..., h:].astype(np.float64) ** 2
+    n1 = y[..., :h].astype(np.float64) ** 2 + y[..., h:].astype(np.float64) ** 2
+    np.testing.assert_allclose(n1, n0, rtol=1e-5, atol=1e-6)
+
+
+def test_rope_position_zero_is_identity_bitexact():
+    for dt in (O.BF16, O.F32):
+        x = O.from_f32(O.normal(42, (1, 1, 8, 64)), dt)
+        y = O.norm_rope(x, dt, dims=64, inv_freq=O.rope_inv_freq(1e4, 64))
+        assert np.array_equal(y, x)
+
+
+def test_rope_offset_shift_invariance_and_per_sequence_offsets():
+    D, p = 64, 37
+    inv = O.rope_inv_freq(500000.0, D)
+    x = O.from_f32(O.normal(43, (1, p + 1, 4, D)), O.BF16)
+    full = O.norm_rope(x, O.BF16, dims=D, inv_freq=inv)
+    last = O.norm_rope(np.ascontiguousarray(x[:, p:]), O.BF16, dims=D, inv_freq=inv, offset=p)
+    assert np.array_equal(full[:, p:], last)
+    # per-sequence offsets equal separate scalar-offset calls (forward_batched loop)
+    xb = O.from_f32(O.normal(44, (5, 1, 4, D)), O.BF16)
+    offs = np.array([0, 7, 1000, 32768, 12345], np.int32)
+    batched = O.norm_rope(xb, O.BF16, dims=D, inv_freq=inv, offsets=offs)
+    for b in range(5):
+        one = O.norm_rope(np.ascontiguousarray(xb[b:b + 1]), O.BF16, dims=D, inv_freq=inv,
+                          offset=int(offs[b]))
+        assert np.array_equal(batched[b:b + 1], one)
+
+
+def test_rope_inverse_rotation_recovers_input():
+    x = O.normal(45, (1, 50, 2, 128))
+    inv = O.rope_inv_freq(1e4, 128)
+    y = O.norm_rope(x, O.F32, dims=128, inv_freq=inv, offset=3)
+    back = O.norm_rope(y, O.F32, dims=128, inv_freq=inv, offset=3, scale=-1.0)
+    np.testing.assert_allclose(back, x, rtol=1e-5, atol=1e-5)
+
+
+def test_partial_rope_passes_tail_through_bitexact():
+    x = O.from_f32(O.normal(46, (4, 1, 16, 256)), O.BF16)
+    offs = O.offsets(47, 4, 1, 32768)
+    y = O.norm_rope(x, O.BF16, dims=64, inv_freq=O.rope_inv_freq(1e7, 64), offsets=offs)
+    assert np.array_equal(y[..., 64:], x[..., 64:])
+    assert not np.array_equal(y[..., :64], x[..., :64])
+
+
+def test_rope_bf16_rounding_sequence_matches_torch_ops():
+    B, L, H, D = 1, 300, 4, 128
+    x = O.from_f32(O.normal(48, (B, L, H, D)), O.BF16)
+    inv = O.rope_inv_freq(1e6, D)
+    got = O.norm_rope(x, O.BF16, dims=D, inv_freq=inv, offset=100)
+    tx = from_bf16_bits(x)
+    th = ((torch.arange(L, dtype=torch.float32) + 100.0)[:, None] * torch.from_numpy(inv)[None, :])
+    c = torch.cos(th).to(torch.bfloat16)[None, :, None, :]
+    s = torch.sin(th).to(torch.bfloat16)[None, :, None, :]
+    x1, x2 = tx[..., :64], tx[..., 64:]
+    ref = torch.cat([x1 * c - x2 * s, x1 * s + x2 * c], -1)
+    rb = ref.view(torch.int16).numpy().view(np.uint16)
+    assert exact_frac(got, rb, O.BF16) > 0.999
+
+
+def test_norm_rope_equals_norm_then_rope():
+    B, L, H, D = 2, 16, 5, 128
+    x = O.from_f32(O.normal(49, (B, L, H, D)), O.BF16)
+    w = O.from_f32(O.normal(50, (D,), 1.0, 0.02), O.BF16)
+    inv = O.rope_inv_freq(1e6, D)
+    fused = O.norm_rope(x, O.BF16, dims=D, inv_freq=inv, norm_w=w, w_dt=O.BF16, eps=1e-6)
+    n = O.rms_norm(x.reshape(-1, D), O.BF16, w, O.BF16, 1e-6).reshape(B, L, H, D)
+    two = O.norm_rope(n, O.BF16, dims=D, inv_freq=inv)
+    assert np.array_equal(fused, two)
+
+
+# ------------------------------------------------------------------ gated norm
+def test_gated_norm_is_swiglu_of_norm():
+    y = O.from_f32(O.normal(51, (128, 128)), O.BF16)
+    z = O.from_f32(O.normal(52, (128, 128)), O.BF16)
+    w = O.from_f32(O.normal(53, (128,), 1.0, 0.02), O.BF16)
+    got = O.gated_rms_norm(y, z, O.BF16, w, O.BF16, 1e-6)
+    n = O.rms_norm(y, O.BF16, w, O.BF16, 1e-6)
+    ref = O.glu(O.ACT_SILU, z, n, O.BF16)
+    assert np.array_equal(got, ref)
+    yf, zf, wf = (O.to_f32(a, O.BF16).astype(np.float64) for a in (y, z, w))
+    exact = zf / (1 + np.exp(-zf)) * yf / np.sqrt((yf ** 2).mean(-1, keepdims=True) + 1e-6) * wf
+    # four bf16 roundings in the composition: within a few ulp of exact math
+    assert_close(got, O.from_f32(exact.astype(np.float32), O.BF16), O.BF16, max_ulp=4,
+                 rtol=3e-2, what="gated vs float64")
+
+
+# ------------------------------------------------------------------ embedding
+def _unpack_nibbles(words: np.ndarray) -> np.ndarray:
+    shifts = (4 * np.arange(8, dtype=np.uint32))
+    return ((words[..., None] >> shifts) & 0xF).reshape(*words.shape[:-1], -1)
+
+
+def test_qembed_unit_scale_returns_codes_bitexact():
+    V, H = 97, 256
+    wq = O.u32(61, (V, H // 8))
+    one = O.from_f32(np.ones((V, H // 64), np.float32), O.BF16)
+    zero = O.from_f32(np.zeros((V, H // 64), np.float32), O.BF16)
+    ids = O.ids(62, 300, V)
+    got = O.to_f32(O.qembed(ids, wq, one, zero, O.BF16), O.BF16)
+    assert np.array_equal(got, _unpack_nibbles(wq)[ids].astype(np.float32))
+
+
+def test_qembed_matches_torch_composition_and_table_rows():
+    V, H, g = 211, 512, 64
+    wq = O.u32(63, (V, H // 8))
+    s = O.from_f32(O.uniform(64, (V, H // g), 0.005, 0.02), O.BF16)
+    b = O.from_f32(O.uniform(65, (V, H // g), -0.1, 0.1), O.BF16)
+    ids = O.ids(66, 500, V)
+    got = O.qembed(ids, wq, s, b, O.BF16)
+    q = torch.from_numpy(_unpack_nibbles(wq).astype(np.float32))
+    ts = from_bf16_bits(s).float().repeat_interleave(g, 1)
+    tb = from_bf16_bits(b).repeat_interleave(g, 1)
+    table = (q * ts).to(torch.bfloat16) + tb  # bf16 add rounds once more
+    ref = table[torch.from_numpy(ids.astype(np.int64))].view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, ref)
+    full = O.qembed(np.arange(V, dtype=np.uint32), wq, s, b, O.BF16)
+    assert np.array_equal(got, full[ids])  # gather-then-dequant == dequant-then-take
+
+
+def test_qembed_zero_code_gives_bias_and_ids_edge_cases():
+    V, H = 16, 64
+    wq = np.zeros((V, H // 8), np.uint32)
+    s = O.from_f32(O.uniform(67, (V, 1), 0.005, 0.02), O.BF16)
+    b = O.from_f32(O.uniform(68, (V, 1), -0.1, 0.1), O.BF16)
+    ids = np.array([3, -1, -16, 16, -17, 0], np.int32)
+    got = O.qembed(ids, wq, s, b, O.BF16)
+    assert np.array_equal(got[0], np.repeat(b[3], H))
+    assert np.array_equal(got[1], np.repeat(b[15], H))   # -1 -> last row
+    assert np.array_equal(got[2], np.repeat(b[0], H))
+    assert not got[3].any() and not got[4].any()         # out of range -> zeros
+    assert np.array_equal(got[5], np.repeat(b[0], H))
+
+
+def test_gemma_embedding_scale():
+    assert O.to_f32(O.from_f32(np.array([math.sqrt(3584.0)], np.float32), O.BF16), O.BF16)[0] == 59.75
+    V, H = 31, 3584
+    wq = O.u32(69, (V, H // 8))
+    s = O.from_f32(O.uniform(70, (V, H // 64), 0.005, 0.02), O.BF16)
+    b = O.from_f32(O.uniform(71, (V, H // 64), -0.1, 0.1), O.BF16)
+    ids = O.ids(72, 40, V)
+    plain = O.qembed(ids, wq, s, b, O.BF16)
+    scaled = O.qembed(ids, wq, s, b, O.BF16, out_scale=math.sqrt(3584.0))
+    ref = (from_bf16_bits(plain) * torch.tensor(59.75, dtype=torch.bfloat16))
+    assert np.array_equal(scaled, ref.view(torch.int16).numpy().view(np.uint16))
+
+
+# ------------------------------------------------------------------ inputs
+def test_rng_is_deterministic_and_well_formed():
+    a = O.normal(1001, (1_000_001,))
+    assert np.array_equal(a, O.normal(1001, (1_000_001,)))
+    assert abs(a.mean()) < 5e-3 and abs(a.std() - 1) < 5e-3
+    c = O.u32(1002, (100_000,))
+    nib = _unpack_nibbles(c).ravel()
+    counts = np.bincount(nib, minlength=16) / nib.size
+    assert np.abs(counts - 1 / 16).max() < 2e-3
+    i = O.ids(1003, 100_000, 128256)
+    assert i.max() < 128256 and i.min() >= 0
+    o = O.offsets(1004, 10_000, 1, 32768)
+    assert o.min() >= 1 and o.max() <= 32768
