@@ -38,10 +38,26 @@ def _i64s(vals):
 
 
 class Kernel:
-    """One launch type: `launch(set_index)` enqueues it on the current stream."""
+    """One launch type: a C-ABI entry point with one pre-built ctypes argument
+    tuple per buffer set (the stream is the last argument).
 
-    def __init__(self, name, nbytes, launch, tokens=0):
-        self.name, self.bytes, self.launch, self.tokens = name, nbytes, launch, tokens
+    The tuples carry raw device addresses only, so `keep` must hold every
+    tensor they point into: a tensor freed after the builder returns would go
+    back to torch's caching allocator, and graph capture (which empties that
+    cache) would unmap it under the launches."""
+
+    def __init__(self, name, nbytes, fn, argsets, tokens=0, keep=()):
+        self.name, self.bytes, self.fn, self.tokens = name, nbytes, fn, tokens
+        self.argsets = [tuple(a) for a in argsets]
+        self.keep = keep
+
+    def launch(self, s):
+        st = self.fn(*self.argsets[s])
+        if st:
+            raise RuntimeError(f"{self.name}: status {st}")
+
+    def restream(self, stream):
+        self.argsets = [a[:-1] + (stream,) for a in self.argsets]
 
 
 class Workload:
@@ -102,36 +118,30 @@ def nsets_for(set_bytes, target=1 << 30):
     return max(2, math.ceil(target / max(set_bytes, 1)))
 
 
+def _f(x):
+    return C.c_float(x)
+
+
 def k_embed(cx, name, sets, tab, V, Hd, n, scale=0.0, group=64):
     wq, sc, bi = tab
     nbytes = n * (Hd // 2 + 2 * 2 * (Hd // group) + 4 + Hd * 2)
-
-    def launch(s, sets=sets):
-        ids, out = sets[s]
-        cx.check(cx.lib.hgk_quantized_embedding(
-            _vp(ids), I32, n, _vp(wq), _vp(sc), _vp(bi), BF16, V, Hd, group, 4, scale,
-            _vp(out), Hd, cx.stream))
-    return Kernel(name, nbytes, launch, n)
+    args = [(_vp(ids), I32, n, _vp(wq), _vp(sc), _vp(bi), BF16, V, Hd, group, 4, _f(scale),
+             _vp(out), Hd, cx.stream) for ids, out in sets]
+    return Kernel(name, nbytes, cx.lib.hgk_quantized_embedding, args, n, keep=(sets, tab))
 
 
 def k_rmsnorm(cx, name, sets, w, rows, n, eps, plus_one=0, ydt=BF16):
     nbytes = rows * n * 2 + rows * n * (4 if ydt == F32 else 2) + n * 2
-
-    def launch(s):
-        x, y = sets[s]
-        cx.check(cx.lib.hgk_rms_norm(_vp(x), BF16, n, _vp(w), BF16, plus_one, eps, _vp(y), ydt,
-                                     n, rows, n, cx.stream))
-    return Kernel(name, nbytes, launch, rows)
+    args = [(_vp(x), BF16, n, _vp(w), BF16, plus_one, _f(eps), _vp(y), ydt, n, rows, n,
+             cx.stream) for x, y in sets]
+    return Kernel(name, nbytes, cx.lib.hgk_rms_norm, args, rows, keep=(sets, w))
 
 
 def k_glu(cx, name, sets, rows, n, act):
     nbytes = 3 * rows * n * 2
-
-    def launch(s):
-        g, u, o = sets[s]
-        cx.check(cx.lib.hgk_glu(act, BF16, _vp(g), n, _vp(u), n, _vp(o), BF16, n, rows, n,
-                                cx.stream))
-    return Kernel(name, nbytes, launch, rows)
+    args = [(act, BF16, _vp(g), n, _vp(u), n, _vp(o), BF16, n, rows, n, cx.stream)
+            for g, u, o in sets]
+    return Kernel(name, nbytes, cx.lib.hgk_glu, args, rows, keep=(sets,))
 
 
 def k_qkrope(cx, name, sets, B, L, Hq, Hk, D, dims, base, freqs=None, wq=None, wk=None,
@@ -149,24 +159,19 @@ def k_qkrope(cx, name, sets, B, L, Hq, Hk, D, dims, base, freqs=None, wq=None, w
     qos = _i64s([Hq * L * D, D, L * D])
     kos = _i64s([Hk * L * D, D, L * D])
 
-    def launch(s):
-        q, k, qo, ko = sets[s]
-        cx.check(cx.lib.hgk_qk_norm_rope(
-            BF16, _vp(q), qs, _vp(qo), qos, Hq, None if wq is None else _vp(wq),
-            _vp(k), ks, _vp(ko), kos, Hk, None if wk is None else _vp(wk), BF16, eps,
-            B, L, D, dims, base, 1.0, fr, 0, None if offsets is None else _vp(offsets),
-            cx.stream))
-    return Kernel(name, nbytes, launch, B * L)
+    args = [(BF16, _vp(q), qs, _vp(qo), qos, Hq, None if wq is None else _vp(wq),
+             _vp(k), ks, _vp(ko), kos, Hk, None if wk is None else _vp(wk), BF16, _f(eps),
+             B, L, D, dims, _f(base), _f(1.0), fr, 0,
+             None if offsets is None else _vp(offsets), cx.stream) for q, k, qo, ko in sets]
+    return Kernel(name, nbytes, cx.lib.hgk_qk_norm_rope, args, B * L,
+                  keep=(sets, wq, wk, offsets, fr, qs, ks, qos, kos))
 
 
 def k_gated(cx, name, sets, w, rows, n, eps, zrow, zgroup, zgs):
     nbytes = 3 * rows * n * 2 + n * 2
-
-    def launch(s):
-        y, z, o = sets[s]
-        cx.check(cx.lib.hgk_gated_rms_norm(BF16, _vp(y), n, _vp(z), zrow, zgroup, zgs, _vp(w),
-                                           BF16, eps, _vp(o), BF16, n, rows, n, cx.stream))
-    return Kernel(name, nbytes, launch, rows)
+    args = [(BF16, _vp(y), n, _vp(z), zrow, zgroup, zgs, _vp(w), BF16, _f(eps), _vp(o), BF16,
+             n, rows, n, cx.stream) for y, z, o in sets]
+    return Kernel(name, nbytes, cx.lib.hgk_gated_rms_norm, args, rows, keep=(sets, w))
 
 
 def wl_llama_chain(cx):
@@ -311,66 +316,109 @@ WORKLOADS = {
 
 
 # ---------------------------------------------------------------- measurement
+class HipEvents:
+    """HIP events through the runtime's C API, recorded on the stream the
+    kernels are launched on (the C ABI gets the same stream handle)."""
+
+    def __init__(self):
+        h = C.CDLL("libamdhip64.so")
+        h.hipEventCreate.argtypes = [C.POINTER(C.c_void_p)]
+        h.hipEventRecord.argtypes = [C.c_void_p, C.c_void_p]
+        h.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), C.c_void_p, C.c_void_p]
+        h.hipEventDestroy.argtypes = [C.c_void_p]
+        h.hipEventSynchronize.argtypes = [C.c_void_p]
+        self.h = h
+
+    def create(self, n):
+        out = []
+        for _ in range(n):
+            e = C.c_void_p()
+            if self.h.hipEventCreate(C.byref(e)):
+                raise RuntimeError("hipEventCreate failed")
+            out.append(e)
+        return out
+
+    def elapsed_ms(self, a, b):
+        ms = C.c_float()
+        if self.h.hipEventElapsedTime(C.byref(ms), a, b):
+            raise RuntimeError("hipEventElapsedTime failed")
+        return ms.value
+
+    def destroy(self, evs):
+        for e in evs:
+            self.h.hipEventDestroy(e)
+
+
 def measure(cx, wl, steps, warmup):
     torch = cx.torch
-    Ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
+    he = HipEvents()
+    rec = he.h.hipEventRecord
     if wl.graph:
-        # launch-bound sequence: capture one step per buffer set, replay
+        # launch-bound sequence: one captured graph per buffer set, replayed
+        side = torch.cuda.Stream(cx.dev)
+        sh = C.c_void_p(side.cuda_stream)
+        for k in wl.kernels:
+            k.restream(sh)
         graphs = []
-        s = torch.cuda.Stream(cx.dev)
         for si in range(wl.nsets):
             g = torch.cuda.CUDAGraph()
-            with torch.cuda.stream(s):
-                cx.stream = C.c_void_p(s.cuda_stream)
+            with torch.cuda.stream(side):
                 for k in wl.kernels:
-                    k.launch(si)  # eager run on the side stream before capture
-                s.synchronize()
-                with torch.cuda.graph(g, stream=s):
-                    cx.stream = C.c_void_p(s.cuda_stream)
+                    k.launch(si)  # eager pass on the capture stream first
+                side.synchronize()
+                with torch.cuda.graph(g, stream=side):
                     for k in wl.kernels:
                         k.launch(si)
             graphs.append(g)
-        cx.stream = C.c_void_p(torch.cuda.current_stream(cx.dev).cuda_stream)
+        for k in wl.kernels:
+            k.restream(cx.stream)
         for i in range(warmup):
             graphs[i % wl.nsets].replay()
         torch.cuda.synchronize()
-        t0, t1 = Ev(), Ev()
+        t0, t1 = he.create(2)
         w0 = time.perf_counter()
-        t0.record()
+        rec(t0, cx.stream)
         for i in range(steps):
             graphs[i % wl.nsets].replay()
-        t1.record()
+        rec(t1, cx.stream)
         torch.cuda.synchronize()
         wall = time.perf_counter() - w0
-        ms = t0.elapsed_time(t1) / steps
+        ms = he.elapsed_ms(t0, t1) / steps
+        he.destroy([t0, t1])
         return {"ms_per_step": ms, "wall_ms_per_step": wall * 1e3 / steps, "kernels": None}
     for i in range(warmup):
         wl.step(i)
     torch.cuda.synchronize()
     nk = len(wl.kernels)
-    evs = [[Ev() for _ in range(nk + 1)] for _ in range(steps)]
-    t0, t1 = Ev(), Ev()
+    evs = [he.create(nk + 1) for _ in range(steps)]
+    t0, t1 = he.create(2)
+    st = cx.stream
+    plan = [[(k.fn, k.argsets[i % wl.nsets], k.name) for k in wl.kernels] for i in range(steps)]
+    torch.cuda.synchronize()
     w0 = time.perf_counter()
-    t0.record()
+    rec(t0, st)
     for i in range(steps):
         e = evs[i]
-        s = i % wl.nsets
-        e[0].record()
-        for j, k in enumerate(wl.kernels):
-            k.launch(s)
-            e[j + 1].record()
-    t1.record()
+        rec(e[0], st)
+        for j, (fn, args, name) in enumerate(plan[i]):
+            if fn(*args):
+                raise RuntimeError(f"{name}: {cx.lib.hgk_last_error().decode()}")
+            rec(e[j + 1], st)
+    rec(t1, st)
     torch.cuda.synchronize()
     wall = time.perf_counter() - w0
-    ms = t0.elapsed_time(t1) / steps
+    ms = he.elapsed_ms(t0, t1) / steps
     per = []
     for j, k in enumerate(wl.kernels):
-        d = sorted(evs[i][j].elapsed_time(evs[i][j + 1]) for i in range(steps))
+        d = sorted(he.elapsed_ms(evs[i][j], evs[i][j + 1]) for i in range(steps))
         avg = sum(d) / len(d)
         per.append({"kernel": k.name, "bytes": k.bytes, "avg_us": avg * 1e3,
                     "median_us": d[len(d) // 2] * 1e3, "best_us": d[0] * 1e3,
                     "gbs": k.bytes / (avg * 1e-3) / 1e9,
                     "frac_of_peak": k.bytes / (avg * 1e-3) / 1e9 / PEAK_HBM_GBS})
+    for e in evs:
+        he.destroy(e)
+    he.destroy([t0, t1])
     return {"ms_per_step": ms, "wall_ms_per_step": wall * 1e3 / steps, "kernels": per}
 
 

@@ -14,11 +14,39 @@
 // which promote a bf16 input): 0.5*g*(1+tanh(k0*(g + k1*g^3))) is evaluated as
 // the identical g / (1 + exp(-2*k0*(g + k1*g^3))), using the hardware exp2 and
 // reciprocal (relative error ~1e-6), and the product with up is rounded once.
+//
+// Large 16-bit SwiGLU: the exact sigmoid costs ~40 VALU operations per element,
+// which would make the kernel compute-bound. But round_T(g * round_T(sig(g)))
+// depends only on the 16 bits of g, so a 64K-entry table of it (built once per
+// device by the exact code path) is held in LDS (128 KB of gfx950's 160 KB per
+// CU) by one 1024-thread block per CU; each element then costs one LDS lookup,
+// one multiply and one conversion, bit-identical to the direct path.
+#include <mutex>
+
 #include "../../include/higgs_hip.h"
 #include "hgk_common.h"
 #include "hgk_host.h"
 
 namespace hgk {
+
+// s = round_T(g * round_T(sigmoid(g))) for every 16-bit pattern g.
+__device__ uint16_t g_silu_lut_bf16[65536];
+__device__ uint16_t g_silu_lut_f16[65536];
+
+template <class X>
+__device__ inline uint16_t* silu_lut() {
+  if constexpr (X::kCode == DT_BF16) return g_silu_lut_bf16;
+  else return g_silu_lut_f16;
+}
+
+template <class X>
+__global__ __launch_bounds__(256) void silu_lut_init_kernel() {
+  const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+  const float g = X::lo(i);
+  const float sg = X::round(mlx_sigmoid(g));
+  const float s = X::round(g * sg);
+  silu_lut<X>()[i] = (uint16_t)(X::pack(s, 0.0f) & 0xffffu);
+}
 
 struct GluArgs {
   const void* g;
@@ -91,10 +119,112 @@ __global__ __launch_bounds__(256) void glu_generic_kernel(GluArgs a, int64_t n, 
   store1<Y>(a.o, row * a.os + c, glu1<X, ACT>(g, u));
 }
 
+constexpr int kLutBlock = 1024;
+constexpr int kLutUnroll = 4;
+
+// Persistent SwiGLU for 16-bit X: one 1024-thread block per CU loads the silu
+// table into LDS once, then strides over the tensor kLutUnroll chunks per
+// thread at a time (all loads of a step issued before any lookup).
+template <class X, class Y>
+__global__ __launch_bounds__(kLutBlock) void swiglu_lut_kernel(GluArgs a) {
+  constexpr int V = Vec<X>::N;
+  constexpr int U = kLutUnroll;
+  __shared__ uint16_t lut[65536];
+  {
+    const u32x4* src = reinterpret_cast<const u32x4*>(silu_lut<X>());
+    u32x4* dst = reinterpret_cast<u32x4*>(lut);
+#pragma unroll
+    for (int i = 0; i < 65536 * 2 / 16 / kLutBlock; ++i)
+      dst[i * kLutBlock + threadIdx.x] = src[i * kLutBlock + threadIdx.x];
+  }
+  __syncthreads();
+  const uint32_t per_iter = (uint32_t)kLutBlock * U;
+  for (uint32_t base = blockIdx.x * per_iter + threadIdx.x; base < a.total;
+       base += gridDim.x * per_iter) {
+    u32x4 gr[U];
+    float uv[U][V];
+    int64_t oo[U];
+    bool ok[U];
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      const uint32_t q = base + (uint32_t)kLutBlock * k;
+      ok[k] = q < a.total;
+      const uint32_t qq = ok[k] ? q : 0u;
+      int64_t go, uo;
+      if (a.contig) {
+        go = uo = oo[k] = (int64_t)qq * V;
+      } else {
+        const uint32_t row = qq / a.cpr, c = qq - row * a.cpr;
+        go = (int64_t)row * a.gs + (int64_t)c * V;
+        uo = (int64_t)row * a.us + (int64_t)c * V;
+        oo[k] = (int64_t)row * a.os + (int64_t)c * V;
+      }
+      gr[k] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(a.g) + go * 2);
+      load_chunk<X>(a.u, uo, uv[k]);
+    }
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      float o[V];
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float s0 = X::lo((uint32_t)lut[gr[k][w] & 0xffffu]);
+        const float s1 = X::lo((uint32_t)lut[gr[k][w] >> 16]);
+        o[2 * w] = s0 * uv[k][2 * w];
+        o[2 * w + 1] = s1 * uv[k][2 * w + 1];
+        if constexpr (Y::kCode != X::kCode) {  // MLX's result is X; widen after rounding
+          o[2 * w] = X::round(o[2 * w]);
+          o[2 * w + 1] = X::round(o[2 * w + 1]);
+        }
+      }
+      if (ok[k]) store_elems<Y, V>(a.o, oo[k], o);
+    }
+  }
+}
+
 namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_lut_mu;
+bool g_lut_ready[2][kMaxDevices];
+int g_cu_count[kMaxDevices];
+
+// Build the table for X on the current device once; false when that cannot be
+// done right now (stream under graph capture), in which case the caller takes
+// the direct path.
+template <class X>
+bool ensure_silu_lut(hipStream_t s, int* cus) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return false;
+  const int which = X::kCode == DT_BF16 ? 0 : 1;
+  std::lock_guard<std::mutex> lk(g_lut_mu);
+  if (!g_cu_count[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      return false;
+    g_cu_count[dev] = n;
+  }
+  *cus = g_cu_count[dev];
+  if (g_lut_ready[which][dev]) return true;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return false;
+  hipLaunchKernelGGL((silu_lut_init_kernel<X>), dim3(65536 / 256), dim3(256), 0, s);
+  if (hipGetLastError() != hipSuccess || hipStreamSynchronize(s) != hipSuccess) return false;
+  g_lut_ready[which][dev] = true;
+  return true;
+}
 
 template <class X, class Y, int ACT>
 void launch(const GluArgs& a, bool vec_ok, int64_t rows, int64_t n, hipStream_t s) {
+  if constexpr (ACT == HGK_ACT_SILU && X::kBytes == 2) {
+    int cus = 0;
+    if (vec_ok && a.total >= (1u << 18) && ensure_silu_lut<X>(s, &cus)) {
+      const uint32_t per_block = (uint32_t)kLutBlock * kLutUnroll;
+      const uint32_t need = (a.total + per_block - 1) / per_block;
+      const unsigned blocks = need < (uint32_t)cus ? need : (unsigned)cus;
+      hipLaunchKernelGGL((swiglu_lut_kernel<X, Y>), dim3(blocks), dim3(kLutBlock), 0, s, a);
+      return;
+    }
+  }
   if (vec_ok) {
     if (a.total >= 256u * 4u * 1024u) {
       const unsigned blocks = (a.total + 1024u - 1u) / 1024u;

@@ -50,47 +50,51 @@ __device__ inline float deq(uint32_t q, float s, float b) {
   return S::round(S::round((float)q * s) + b);
 }
 
+// One wave per token. At step s lane i owns packed word w = s*64 + i (8 codes,
+// one group): each load instruction of the wave reads 256 contiguous bytes of
+// the row and each store writes 1 KB contiguous, so no cache line is touched
+// by more than one instruction.
 template <class S, int STEPS>
 __global__ __launch_bounds__(256) void qembed_kernel(QembArgs a) {
   const int lane = threadIdx.x & 63;
-  const int64_t t = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int64_t t = (int64_t)blockIdx.x * (blockDim.x >> 6) +
+                    __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (t >= a.n) return;  // whole wave leaves together
   const int64_t id = load_id(a, t);
   const bool valid = id >= 0 && id < a.vocab;
   const int64_t row = valid ? id : 0;
   const float osc = S::round(a.scale);
+  const uint32_t* wrow = a.wq + row * a.wpr;
+  const int64_t grow = row * a.gpr;
 
-  u32x4 codes[STEPS];
+  uint32_t codes[STEPS];
   float sv[STEPS], bv[STEPS];
 #pragma unroll
   for (int s = 0; s < STEPS; ++s) {
-    const int w0 = (s * 64 + lane) * 4;
-    if (valid && w0 < a.wpr) {
-      codes[s] = *reinterpret_cast<const u32x4*>(a.wq + row * a.wpr + w0);
-      const int g = (w0 * 8) / a.group;
-      sv[s] = load1<S>(a.sc, row * a.gpr + g);
-      bv[s] = load1<S>(a.bi, row * a.gpr + g);
+    const int w = s * 64 + lane;
+    if (valid && w < a.wpr) {
+      codes[s] = wrow[w];
+      const int g = (w * 8) / a.group;
+      sv[s] = load1<S>(a.sc, grow + g);
+      bv[s] = load1<S>(a.bi, grow + g);
     } else {
-      codes[s] = u32x4{0u, 0u, 0u, 0u};
+      codes[s] = 0u;
       sv[s] = bv[s] = 0.0f;
     }
   }
 #pragma unroll
   for (int s = 0; s < STEPS; ++s) {
-    const int w0 = (s * 64 + lane) * 4;
-    if (w0 >= a.wpr) continue;
+    const int w = s * 64 + lane;
+    if (w >= a.wpr) continue;
+    float v[8];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      float v[8];
-#pragma unroll
-      for (int nib = 0; nib < 8; ++nib) {
-        const uint32_t q = (codes[s][k] >> (4 * nib)) & 0xfu;
-        float x = deq<S>(q, sv[s], bv[s]);
-        x = a.has_scale ? S::round(x * osc) : x;
-        v[nib] = valid ? x : 0.0f;
-      }
-      store_elems<S, 8>(a.out, t * a.os + (int64_t)(w0 + k) * 8, v);
+    for (int nib = 0; nib < 8; ++nib) {
+      const uint32_t q = (codes[s] >> (4 * nib)) & 0xfu;
+      float x = deq<S>(q, sv[s], bv[s]);
+      x = a.has_scale ? S::round(x * osc) : x;
+      v[nib] = valid ? x : 0.0f;
     }
+    store_elems<S, 8>(a.out, t * a.os + (int64_t)w * 8, v);
   }
 }
 
@@ -115,18 +119,18 @@ namespace {
 
 template <class S>
 void launch(const QembArgs& a, bool vec_ok, hipStream_t s) {
-  const int steps = (a.wpr + 255) / 256;
-  if (vec_ok && steps <= 8) {
+  const int steps = (a.wpr + 63) / 64;
+  if (vec_ok && steps <= 16) {
     const int wpb = a.n >= 1024 ? 4 : 1;
     const unsigned blocks = (unsigned)((a.n + wpb - 1) / wpb);
     const dim3 g(blocks), b(64 * wpb);
-    switch (steps) {
-      case 1: hipLaunchKernelGGL((qembed_kernel<S, 1>), g, b, 0, s, a); return;
-      case 2: hipLaunchKernelGGL((qembed_kernel<S, 2>), g, b, 0, s, a); return;
-      case 3: hipLaunchKernelGGL((qembed_kernel<S, 3>), g, b, 0, s, a); return;
-      case 4: hipLaunchKernelGGL((qembed_kernel<S, 4>), g, b, 0, s, a); return;
-      default: hipLaunchKernelGGL((qembed_kernel<S, 8>), g, b, 0, s, a); return;
-    }
+    if (steps <= 1) hipLaunchKernelGGL((qembed_kernel<S, 1>), g, b, 0, s, a);
+    else if (steps <= 2) hipLaunchKernelGGL((qembed_kernel<S, 2>), g, b, 0, s, a);
+    else if (steps <= 4) hipLaunchKernelGGL((qembed_kernel<S, 4>), g, b, 0, s, a);
+    else if (steps <= 7) hipLaunchKernelGGL((qembed_kernel<S, 7>), g, b, 0, s, a);
+    else if (steps <= 8) hipLaunchKernelGGL((qembed_kernel<S, 8>), g, b, 0, s, a);
+    else hipLaunchKernelGGL((qembed_kernel<S, 16>), g, b, 0, s, a);
+    return;
   }
   const int64_t blocks = (a.n * a.hidden + 255) / 256;
   hipLaunchKernelGGL((qembed_generic_kernel<S>), dim3((unsigned)blocks), dim3(256), 0, s, a);
@@ -168,7 +172,8 @@ extern "C" int hgk_quantized_embedding(const void* ids, int ids_dtype, int64_t n
   a.bi = biases; a.vocab = vocab; a.wpr = (int)(hidden / 8); a.gpr = (int)(hidden / group_size);
   a.group = group_size; a.scale = out_scale; a.has_scale = out_scale != 0.0f;
   a.out = out; a.os = out_row_stride; a.hidden = hidden;
-  const bool vec_ok = aligned16(w_q) && aligned16(out) && hidden % 32 == 0 && out_row_stride % 8 == 0;
+  const bool vec_ok = (reinterpret_cast<uintptr_t>(w_q) & 3u) == 0 && aligned16(out) &&
+                      hidden % 8 == 0 && out_row_stride % 8 == 0;
   if (scales_dtype == DT_BF16) launch<BF16>(a, vec_ok, as_stream(stream));
   else launch<F16>(a, vec_ok, as_stream(stream));
   return launch_status(fn);

@@ -220,7 +220,8 @@ def test_qk_norm_rope_f32(dev):
 # ------------------------------------------------------------------ GLU
 @pytest.mark.parametrize("dt", [O.BF16, O.F16, O.F32])
 def test_swiglu_bitexact(dev, dt):
-    rows, n = (4096, 8192) if dt == O.BF16 else (256, 1024)
+    """bf16/f16 at these sizes take the LDS-table kernel; f32 the direct one."""
+    rows, n = {O.BF16: (4096, 8192), O.F16: (2048, 2048), O.F32: (256, 1024)}[dt]
     g = O.from_f32(O.normal(1501 + dt, (rows, n)) * np.float32(2.0), dt)
     u = O.from_f32(O.normal(1511 + dt, (rows, n)), dt)
     ref = O.glu(O.ACT_SILU, g, u, dt)
@@ -252,10 +253,19 @@ def test_swiglu_layouts(dev):
     u = O.from_f32(O.normal(1525, (7, 1001)), O.BF16)
     assert np.array_equal(to_host(H.silu_mul(to_dev(g, O.BF16, dev), to_dev(u, O.BF16, dev))),
                           O.glu(O.ACT_SILU, g, u, O.BF16))
-    # bf16 in, f32 out: the bf16 result widened
+    # bf16 in, f32 out: the bf16 result widened (direct path, then table path)
     got = to_host(H.silu_mul(to_dev(g, O.BF16, dev), to_dev(u, O.BF16, dev),
                              out_dtype=torch.float32))
     assert np.array_equal(got, O.glu(O.ACT_SILU, g, u, O.BF16, out_dt=O.F32))
+    g = O.from_f32(O.normal(1526, (1024, 4096)) * np.float32(3.0), O.BF16)
+    u = O.from_f32(O.normal(1527, (1024, 4096)), O.BF16)
+    got = to_host(H.silu_mul(to_dev(g, O.BF16, dev), to_dev(u, O.BF16, dev),
+                             out_dtype=torch.float32))
+    assert np.array_equal(got, O.glu(O.ACT_SILU, g, u, O.BF16, out_dt=O.F32))
+    # strided rows through the table path: fused gate_up [rows, 2I]
+    gu = O.from_f32(O.normal(1528, (512, 2 * 4096)), O.BF16)
+    ref = O.glu(O.ACT_SILU, gu[:, :4096], gu[:, 4096:], O.BF16)
+    assert np.array_equal(to_host(H.fused_gate_up_swiglu(to_dev(gu, O.BF16, dev))), ref)
 
 
 @pytest.mark.parametrize("dt,odt", [(O.BF16, O.BF16), (O.BF16, O.F32), (O.F32, O.F32),
