@@ -389,36 +389,48 @@ def measure(cx, wl, steps, warmup):
     for i in range(warmup):
         wl.step(i)
     torch.cuda.synchronize()
-    nk = len(wl.kernels)
-    evs = [he.create(nk + 1) for _ in range(steps)]
-    t0, t1 = he.create(2)
     st = cx.stream
-    plan = [[(k.fn, k.argsets[i % wl.nsets], k.name) for k in wl.kernels] for i in range(steps)]
+
+    def run(plan):
+        for fn, args, name in plan:
+            if fn(*args):
+                raise RuntimeError(f"{name}: {cx.lib.hgk_last_error().decode()}")
+
+    # the K timed steps: events only at the two ends (an event between kernels
+    # costs the stream ~4 us on this part, more than a small kernel's work)
+    plan = [(k.fn, k.argsets[i % wl.nsets], k.name) for i in range(steps) for k in wl.kernels]
+    t0, t1 = he.create(2)
     torch.cuda.synchronize()
     w0 = time.perf_counter()
     rec(t0, st)
-    for i in range(steps):
-        e = evs[i]
-        rec(e[0], st)
-        for j, (fn, args, name) in enumerate(plan[i]):
-            if fn(*args):
-                raise RuntimeError(f"{name}: {cx.lib.hgk_last_error().decode()}")
-            rec(e[j + 1], st)
+    run(plan)
     rec(t1, st)
     torch.cuda.synchronize()
     wall = time.perf_counter() - w0
     ms = he.elapsed_ms(t0, t1) / steps
+    he.destroy([t0, t1])
+    # per-kernel launch duration: each kernel back to back over the rotating
+    # buffer sets, in groups bracketed by events on the same stream
+    groups, per_group = 5, max(4, steps // 5)
     per = []
-    for j, k in enumerate(wl.kernels):
-        d = sorted(he.elapsed_ms(evs[i][j], evs[i][j + 1]) for i in range(steps))
+    for k in wl.kernels:
+        evs = he.create(groups + 1)
+        kp = [(k.fn, k.argsets[i % wl.nsets], k.name) for i in range(per_group)]
+        run(kp)  # warm
+        torch.cuda.synchronize()
+        rec(evs[0], st)
+        for g in range(groups):
+            run(kp)
+            rec(evs[g + 1], st)
+        torch.cuda.synchronize()
+        d = sorted(he.elapsed_ms(evs[g], evs[g + 1]) / per_group for g in range(groups))
+        he.destroy(evs)
         avg = sum(d) / len(d)
         per.append({"kernel": k.name, "bytes": k.bytes, "avg_us": avg * 1e3,
                     "median_us": d[len(d) // 2] * 1e3, "best_us": d[0] * 1e3,
+                    "launches": groups * per_group,
                     "gbs": k.bytes / (avg * 1e-3) / 1e9,
                     "frac_of_peak": k.bytes / (avg * 1e-3) / 1e9 / PEAK_HBM_GBS})
-    for e in evs:
-        he.destroy(e)
-    he.destroy([t0, t1])
     return {"ms_per_step": ms, "wall_ms_per_step": wall * 1e3 / steps, "kernels": per}
 
 

@@ -76,36 +76,44 @@ __device__ inline float glu1(float g, float u) {
   }
 }
 
-template <class X, class Y, int ACT, int U>
+// Element offsets of chunk q in gate, up and out (rows of cpr chunks).
+template <int V, bool CONTIG>
+__device__ inline void glu_offsets(const GluArgs& a, uint32_t q, int64_t& go, int64_t& uo,
+                                   int64_t& oo) {
+  if constexpr (CONTIG) {
+    go = uo = oo = (int64_t)q * V;
+  } else {
+    const uint32_t row = q / a.cpr, c = q - row * a.cpr;
+    go = (int64_t)row * a.gs + (int64_t)c * V;
+    uo = (int64_t)row * a.us + (int64_t)c * V;
+    oo = (int64_t)row * a.os + (int64_t)c * V;
+  }
+}
+
+// Chunks past the end are clamped to the last chunk for the loads (so loads
+// are never predicated and can all issue before the first wait) and skipped
+// at the store.
+template <class X, class Y, int ACT, int U, bool CONTIG>
 __global__ __launch_bounds__(256) void glu_kernel(GluArgs a) {
   constexpr int V = Vec<X>::N;
   const uint32_t base = blockIdx.x * (256u * U) + threadIdx.x;
-  float gv[U][V], uv[U][V];
+  u32x4 gr[U], ur[U];
   int64_t oo[U];
-  bool ok[U];
 #pragma unroll
   for (int k = 0; k < U; ++k) {
     const uint32_t q = base + 256u * k;
-    ok[k] = q < a.total;
-    const uint32_t qq = ok[k] ? q : 0u;
+    const uint32_t qq = q < a.total ? q : a.total - 1;
     int64_t go, uo;
-    if (a.contig) {
-      go = uo = oo[k] = (int64_t)qq * V;
-    } else {
-      const uint32_t row = qq / a.cpr, c = qq - row * a.cpr;
-      go = (int64_t)row * a.gs + (int64_t)c * V;
-      uo = (int64_t)row * a.us + (int64_t)c * V;
-      oo[k] = (int64_t)row * a.os + (int64_t)c * V;
-    }
-    load_chunk<X>(a.g, go, gv[k]);
-    load_chunk<X>(a.u, uo, uv[k]);
+    glu_offsets<V, CONTIG>(a, qq, go, uo, oo[k]);
+    gr[k] = ld16<X>(a.g, go);
+    ur[k] = ld16<X>(a.u, uo);
   }
 #pragma unroll
   for (int k = 0; k < U; ++k) {
     float o[V];
 #pragma unroll
-    for (int e = 0; e < V; ++e) o[e] = glu1<X, ACT>(gv[k][e], uv[k][e]);
-    if (ok[k]) store_elems<Y, V>(a.o, oo[k], o);
+    for (int e = 0; e < V; ++e) o[e] = glu1<X, ACT>(elem<X>(gr[k], e), elem<X>(ur[k], e));
+    if (base + 256u * k < a.total) store_elems<Y, V>(a.o, oo[k], o);
   }
 }
 
@@ -125,11 +133,29 @@ constexpr int kLutUnroll = 4;
 // Persistent SwiGLU for 16-bit X: one 1024-thread block per CU loads the silu
 // table into LDS once, then strides over the tensor kLutUnroll chunks per
 // thread at a time (all loads of a step issued before any lookup).
-template <class X, class Y>
+template <class X, class Y, bool CONTIG>
 __global__ __launch_bounds__(kLutBlock) void swiglu_lut_kernel(GluArgs a) {
   constexpr int V = Vec<X>::N;
   constexpr int U = kLutUnroll;
   __shared__ uint16_t lut[65536];
+  const uint32_t per_iter = (uint32_t)kLutBlock * U;
+  const uint32_t stride = gridDim.x * per_iter;
+  u32x4 gr[U], ur[U];
+  int64_t oo[U];
+  auto load_step = [&](uint32_t base) {
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      const uint32_t q = base + (uint32_t)kLutBlock * k;
+      const uint32_t qq = q < a.total ? q : a.total - 1;
+      int64_t go, uo;
+      glu_offsets<V, CONTIG>(a, qq, go, uo, oo[k]);
+      gr[k] = ld16<X>(a.g, go);
+      ur[k] = ld16<X>(a.u, uo);
+    }
+  };
+  // the first step's loads go out before the 128 KB table copy
+  uint32_t base = blockIdx.x * per_iter + threadIdx.x;
+  load_step(base);
   {
     const u32x4* src = reinterpret_cast<const u32x4*>(silu_lut<X>());
     u32x4* dst = reinterpret_cast<u32x4*>(lut);
@@ -138,30 +164,7 @@ __global__ __launch_bounds__(kLutBlock) void swiglu_lut_kernel(GluArgs a) {
       dst[i * kLutBlock + threadIdx.x] = src[i * kLutBlock + threadIdx.x];
   }
   __syncthreads();
-  const uint32_t per_iter = (uint32_t)kLutBlock * U;
-  for (uint32_t base = blockIdx.x * per_iter + threadIdx.x; base < a.total;
-       base += gridDim.x * per_iter) {
-    u32x4 gr[U];
-    float uv[U][V];
-    int64_t oo[U];
-    bool ok[U];
-#pragma unroll
-    for (int k = 0; k < U; ++k) {
-      const uint32_t q = base + (uint32_t)kLutBlock * k;
-      ok[k] = q < a.total;
-      const uint32_t qq = ok[k] ? q : 0u;
-      int64_t go, uo;
-      if (a.contig) {
-        go = uo = oo[k] = (int64_t)qq * V;
-      } else {
-        const uint32_t row = qq / a.cpr, c = qq - row * a.cpr;
-        go = (int64_t)row * a.gs + (int64_t)c * V;
-        uo = (int64_t)row * a.us + (int64_t)c * V;
-        oo[k] = (int64_t)row * a.os + (int64_t)c * V;
-      }
-      gr[k] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(a.g) + go * 2);
-      load_chunk<X>(a.u, uo, uv[k]);
-    }
+  while (base < a.total) {
 #pragma unroll
     for (int k = 0; k < U; ++k) {
       float o[V];
@@ -169,15 +172,17 @@ __global__ __launch_bounds__(kLutBlock) void swiglu_lut_kernel(GluArgs a) {
       for (int w = 0; w < 4; ++w) {
         const float s0 = X::lo((uint32_t)lut[gr[k][w] & 0xffffu]);
         const float s1 = X::lo((uint32_t)lut[gr[k][w] >> 16]);
-        o[2 * w] = s0 * uv[k][2 * w];
-        o[2 * w + 1] = s1 * uv[k][2 * w + 1];
+        o[2 * w] = s0 * X::lo(ur[k][w]);
+        o[2 * w + 1] = s1 * X::hi(ur[k][w]);
         if constexpr (Y::kCode != X::kCode) {  // MLX's result is X; widen after rounding
           o[2 * w] = X::round(o[2 * w]);
           o[2 * w + 1] = X::round(o[2 * w + 1]);
         }
       }
-      if (ok[k]) store_elems<Y, V>(a.o, oo[k], o);
+      if (base + (uint32_t)kLutBlock * k < a.total) store_elems<Y, V>(a.o, oo[k], o);
     }
+    base += stride;
+    if (base < a.total) load_step(base);
   }
 }
 
@@ -217,21 +222,24 @@ template <class X, class Y, int ACT>
 void launch(const GluArgs& a, bool vec_ok, int64_t rows, int64_t n, hipStream_t s) {
   if constexpr (ACT == HGK_ACT_SILU && X::kBytes == 2) {
     int cus = 0;
-    if (vec_ok && a.total >= (1u << 18) && ensure_silu_lut<X>(s, &cus)) {
+    if (vec_ok && a.total >= (1u << 18) && a.total < (1u << 31) && ensure_silu_lut<X>(s, &cus)) {
       const uint32_t per_block = (uint32_t)kLutBlock * kLutUnroll;
       const uint32_t need = (a.total + per_block - 1) / per_block;
       const unsigned blocks = need < (uint32_t)cus ? need : (unsigned)cus;
-      hipLaunchKernelGGL((swiglu_lut_kernel<X, Y>), dim3(blocks), dim3(kLutBlock), 0, s, a);
+      if (a.contig) hipLaunchKernelGGL((swiglu_lut_kernel<X, Y, true>), dim3(blocks), dim3(kLutBlock), 0, s, a);
+      else hipLaunchKernelGGL((swiglu_lut_kernel<X, Y, false>), dim3(blocks), dim3(kLutBlock), 0, s, a);
       return;
     }
   }
   if (vec_ok) {
     if (a.total >= 256u * 4u * 1024u) {
       const unsigned blocks = (a.total + 1024u - 1u) / 1024u;
-      hipLaunchKernelGGL((glu_kernel<X, Y, ACT, 4>), dim3(blocks), dim3(256), 0, s, a);
+      if (a.contig) hipLaunchKernelGGL((glu_kernel<X, Y, ACT, 4, true>), dim3(blocks), dim3(256), 0, s, a);
+      else hipLaunchKernelGGL((glu_kernel<X, Y, ACT, 4, false>), dim3(blocks), dim3(256), 0, s, a);
     } else {
       const unsigned blocks = (a.total + 255u) / 256u;
-      hipLaunchKernelGGL((glu_kernel<X, Y, ACT, 1>), dim3(blocks), dim3(256), 0, s, a);
+      if (a.contig) hipLaunchKernelGGL((glu_kernel<X, Y, ACT, 1, true>), dim3(blocks), dim3(256), 0, s, a);
+      else hipLaunchKernelGGL((glu_kernel<X, Y, ACT, 1, false>), dim3(blocks), dim3(256), 0, s, a);
     }
     return;
   }

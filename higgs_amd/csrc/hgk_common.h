@@ -86,6 +86,26 @@ __device__ inline void unpack16(u32x4 r, float* v) {
   }
 }
 
+// Raw 16-byte load of the chunk starting at element `e` of T (kept packed in
+// registers until used: half the VGPRs of unpacked f32 for 16-bit types).
+template <class T>
+__device__ inline u32x4 ld16(const void* base, int64_t e) {
+  return *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(base) + e * T::kBytes);
+}
+
+// Element k of a packed run of T held in 32-bit words.
+template <class T>
+__device__ inline float elem(const uint32_t* w, int k) {
+  if constexpr (T::kBytes == 2) return (k & 1) ? T::hi(w[k >> 1]) : T::lo(w[k >> 1]);
+  else return u2f(w[k]);
+}
+
+template <class T>
+__device__ inline float elem(const u32x4& r, int k) {
+  if constexpr (T::kBytes == 2) return (k & 1) ? T::hi(r[k >> 1]) : T::lo(r[k >> 1]);
+  else return u2f(r[k]);
+}
+
 // Load Vec<T>::N elements of T starting at element `e` (16-byte aligned).
 template <class T>
 __device__ inline void load_chunk(const void* base, int64_t e, float* v) {

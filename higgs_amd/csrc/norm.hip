@@ -42,10 +42,14 @@ __device__ inline int64_t z_row_offset(const NormArgs& a, int64_t r) {
   return g * a.zgs + (r - g * a.zg) * a.zs;
 }
 
-template <class X, class Y, int LPR, int CPL, bool GATED>
+// X activation, Y output, W weight storage type (X's type or f32). Every load
+// of the row (x, weights, z) is issued before the reduction; all stay packed
+// in registers until the element is consumed.
+template <class X, class Y, class W, int LPR, int CPL, bool GATED>
 __global__ __launch_bounds__(256) void rms_norm_kernel(NormArgs a) {
   constexpr int V = Vec<X>::N;
   constexpr int RPW = 64 / LPR;
+  constexpr int WW = V * W::kBytes / 4;  // 32-bit words of weights per chunk
   const int lane = threadIdx.x & 63;
   const int64_t wave = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   const int64_t row = wave * RPW + lane / LPR;
@@ -53,23 +57,45 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(NormArgs a) {
   const bool live = row < a.rows;
   const int64_t r = live ? row : a.rows - 1;
   const int nchunks = a.n / V;
+  const bool has_w = a.w != nullptr;
 
-  float v[CPL][V];
+  // Loads are unconditional: chunk indices past the row are clamped to its
+  // last chunk (then ignored), so no select waits on a loaded value before
+  // the next load can issue.
+  u32x4 xr[CPL];
+  uint32_t wr[CPL][WW];
+  u32x4 zr[GATED ? CPL : 1];
+  const int64_t zoff = GATED ? z_row_offset(a, r) : 0;
 #pragma unroll
   for (int c = 0; c < CPL; ++c) {
     const int ch = j + c * LPR;
-    if (ch < nchunks) {
-      load_chunk<X>(a.x, r * a.xs + (int64_t)ch * V, v[c]);
-    } else {
+    const int chc = ch < nchunks ? ch : nchunks - 1;
+    xr[c] = ld16<X>(a.x, r * a.xs + (int64_t)chc * V);
+    if constexpr (GATED) zr[c] = ld16<X>(a.z, zoff + (int64_t)chc * V);
+  }
+  if (has_w) {
 #pragma unroll
-      for (int e = 0; e < V; ++e) v[c][e] = 0.0f;
+    for (int c = 0; c < CPL; ++c) {
+      const int ch = j + c * LPR;
+      const int chc = ch < nchunks ? ch : nchunks - 1;
+#pragma unroll
+      for (int q = 0; q < WW / 4; ++q) {
+        const u32x4 t = ld16<W>(a.w, (int64_t)chc * V + q * Vec<W>::N);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) wr[c][4 * q + k] = t[k];
+      }
     }
   }
   double ss = 0.0;
 #pragma unroll
-  for (int c = 0; c < CPL; ++c)
+  for (int c = 0; c < CPL; ++c) {
+    if (j + c * LPR >= nchunks) continue;
 #pragma unroll
-    for (int e = 0; e < V; ++e) ss = __builtin_fma((double)v[c][e], (double)v[c][e], ss);
+    for (int e = 0; e < V; ++e) {
+      const double d = (double)elem<X>(xr[c], e);
+      ss = __builtin_fma(d, d, ss);
+    }
+  }
   ss = group_sum<LPR>(ss);
   const float rr = rms_scale(ss, a.inv_n, a.eps);
 
@@ -77,25 +103,17 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(NormArgs a) {
   for (int c = 0; c < CPL; ++c) {
     const int ch = j + c * LPR;
     if (ch >= nchunks) continue;
-    float w[V];
-    if (a.w) {
-      load_weights<V>(a.w, a.wdt, (int64_t)ch * V, w);
-    } else {
-#pragma unroll
-      for (int e = 0; e < V; ++e) w[e] = 1.0f;
-    }
-    float zc[V];
-    if constexpr (GATED) load_chunk<X>(a.z, z_row_offset(a, r) + (int64_t)ch * V, zc);
     float o[V];
 #pragma unroll
     for (int e = 0; e < V; ++e) {
-      float nv = v[c][e] * rr;
+      float nv = elem<X>(xr[c], e) * rr;
       nv = a.round_x ? X::round(nv) : nv;
-      const float we = a.plus_one ? w[e] + 1.0f : w[e];
+      const float w0 = has_w ? elem<W>(wr[c], e) : 1.0f;
+      const float we = a.plus_one ? w0 + 1.0f : w0;
       nv = nv * we;
       nv = a.round_x ? X::round(nv) : nv;
       if constexpr (GATED) {
-        const float zz = zc[e];
+        const float zz = elem<X>(zr[c], e);
         const float sg = X::round(mlx_sigmoid(zz));
         const float act = X::round(zz * sg);
         nv = act * nv;
@@ -140,13 +158,13 @@ __global__ __launch_bounds__(256) void rms_norm_generic_kernel(NormArgs a) {
 
 namespace {
 
-template <class X, class Y, int LPR, int CPL, bool GATED>
+template <class X, class Y, class W, int LPR, int CPL, bool GATED>
 void launch_fast(const NormArgs& a, hipStream_t s) {
   constexpr int RPW = 64 / LPR;
   const int64_t waves = (a.rows + RPW - 1) / RPW;
   const int wpb = waves >= 4096 ? 4 : 1;  // small problems: spread over CUs
   const int64_t blocks = (waves + wpb - 1) / wpb;
-  hipLaunchKernelGGL((rms_norm_kernel<X, Y, LPR, CPL, GATED>), dim3((unsigned)blocks),
+  hipLaunchKernelGGL((rms_norm_kernel<X, Y, W, LPR, CPL, GATED>), dim3((unsigned)blocks),
                      dim3(64 * wpb), 0, s, a);
 }
 
@@ -159,37 +177,45 @@ void launch_generic(const NormArgs& a, hipStream_t s) {
 }
 
 // Pick (LPR, CPL) for a row of `nchunks` 16-byte chunks; false -> generic.
-template <class X, class Y, bool GATED>
+template <class X, class Y, class W, bool GATED>
 bool launch_by_shape(const NormArgs& a, int nchunks, hipStream_t s) {
-  if (nchunks <= 4) { launch_fast<X, Y, 4, 1, GATED>(a, s); return true; }
-  if (nchunks <= 8) { launch_fast<X, Y, 8, 1, GATED>(a, s); return true; }
-  if (nchunks <= 16) { launch_fast<X, Y, 16, 1, GATED>(a, s); return true; }
-  if (nchunks <= 32) { launch_fast<X, Y, 32, 1, GATED>(a, s); return true; }
-  if (nchunks <= 64) { launch_fast<X, Y, 64, 1, GATED>(a, s); return true; }
-  if (nchunks <= 128) { launch_fast<X, Y, 64, 2, GATED>(a, s); return true; }
+  if (nchunks <= 4) { launch_fast<X, Y, W, 4, 1, GATED>(a, s); return true; }
+  if (nchunks <= 8) { launch_fast<X, Y, W, 8, 1, GATED>(a, s); return true; }
+  if (nchunks <= 16) { launch_fast<X, Y, W, 16, 1, GATED>(a, s); return true; }
+  if (nchunks <= 32) { launch_fast<X, Y, W, 32, 1, GATED>(a, s); return true; }
+  if (nchunks <= 64) { launch_fast<X, Y, W, 64, 1, GATED>(a, s); return true; }
+  if (nchunks <= 128) { launch_fast<X, Y, W, 64, 2, GATED>(a, s); return true; }
   if constexpr (!GATED) {
     const int cpl = (nchunks + 63) / 64;
     switch (cpl) {
-      case 3: launch_fast<X, Y, 64, 3, false>(a, s); return true;
-      case 4: launch_fast<X, Y, 64, 4, false>(a, s); return true;
-      case 5: launch_fast<X, Y, 64, 5, false>(a, s); return true;
-      case 6: launch_fast<X, Y, 64, 6, false>(a, s); return true;
-      case 7: launch_fast<X, Y, 64, 7, false>(a, s); return true;
-      case 8: launch_fast<X, Y, 64, 8, false>(a, s); return true;
-      case 9: case 10: launch_fast<X, Y, 64, 10, false>(a, s); return true;
-      case 11: case 12: launch_fast<X, Y, 64, 12, false>(a, s); return true;
+      case 3: launch_fast<X, Y, W, 64, 3, false>(a, s); return true;
+      case 4: launch_fast<X, Y, W, 64, 4, false>(a, s); return true;
+      case 5: launch_fast<X, Y, W, 64, 5, false>(a, s); return true;
+      case 6: launch_fast<X, Y, W, 64, 6, false>(a, s); return true;
+      case 7: launch_fast<X, Y, W, 64, 7, false>(a, s); return true;
+      case 8: launch_fast<X, Y, W, 64, 8, false>(a, s); return true;
+      case 9: case 10: launch_fast<X, Y, W, 64, 10, false>(a, s); return true;
+      case 11: case 12: launch_fast<X, Y, W, 64, 12, false>(a, s); return true;
       case 13: case 14: case 15: case 16:
-        launch_fast<X, Y, 64, 16, false>(a, s); return true;
+        launch_fast<X, Y, W, 64, 16, false>(a, s); return true;
       default: break;
     }
   }
   return false;
 }
 
+// The vectorised kernels take weights in the activation type or in f32;
+// any other weight dtype goes to the generic kernel.
 template <class X, class Y, bool GATED>
 void launch_xy(const NormArgs& a, bool vec_ok, hipStream_t s) {
   const int nchunks = a.n / Vec<X>::N;
-  if (vec_ok && launch_by_shape<X, Y, GATED>(a, nchunks, s)) return;
+  if (vec_ok) {
+    if (!a.w || a.wdt == X::kCode) {
+      if (launch_by_shape<X, Y, X, GATED>(a, nchunks, s)) return;
+    } else if (a.wdt == DT_F32) {
+      if (launch_by_shape<X, Y, F32, GATED>(a, nchunks, s)) return;
+    }
+  }
   launch_generic<X, Y, GATED>(a, s);
 }
 

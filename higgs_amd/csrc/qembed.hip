@@ -67,30 +67,32 @@ __global__ __launch_bounds__(256) void qembed_kernel(QembArgs a) {
   const uint32_t* wrow = a.wq + row * a.wpr;
   const int64_t grow = row * a.gpr;
 
-  uint32_t codes[STEPS];
-  float sv[STEPS], bv[STEPS];
+  // every load of the token goes out first, as raw words (converting a value
+  // where it is loaded would make the compiler wait for it step by step)
+  uint32_t codes[STEPS], sraw[STEPS], braw[STEPS];
+  const uint16_t* sc = reinterpret_cast<const uint16_t*>(a.sc);
+  const uint16_t* bi = reinterpret_cast<const uint16_t*>(a.bi);
+  // (addresses are clamped into the row instead of predicating the loads, so
+  // no select has to wait on a loaded value before the next load issues)
 #pragma unroll
   for (int s = 0; s < STEPS; ++s) {
     const int w = s * 64 + lane;
-    if (valid && w < a.wpr) {
-      codes[s] = wrow[w];
-      const int g = (w * 8) / a.group;
-      sv[s] = load1<S>(a.sc, grow + g);
-      bv[s] = load1<S>(a.bi, grow + g);
-    } else {
-      codes[s] = 0u;
-      sv[s] = bv[s] = 0.0f;
-    }
+    const int wc = w < a.wpr ? w : a.wpr - 1;
+    const int g = (wc * 8) / a.group;
+    codes[s] = wrow[wc];
+    sraw[s] = (uint32_t)sc[grow + g];
+    braw[s] = (uint32_t)bi[grow + g];
   }
 #pragma unroll
   for (int s = 0; s < STEPS; ++s) {
     const int w = s * 64 + lane;
     if (w >= a.wpr) continue;
+    const float sv = S::lo(sraw[s]), bv = S::lo(braw[s]);
     float v[8];
 #pragma unroll
     for (int nib = 0; nib < 8; ++nib) {
       const uint32_t q = (codes[s] >> (4 * nib)) & 0xfu;
-      float x = deq<S>(q, sv[s], bv[s]);
+      float x = deq<S>(q, sv, bv);
       x = a.has_scale ? S::round(x * osc) : x;
       v[nib] = valid ? x : 0.0f;
     }

@@ -69,93 +69,146 @@ __device__ inline void fill_table(const RopeArgs& a, float* cs, float* sn, uint3
   }
 }
 
+constexpr int kRopeBatch = 4;  // head rows a lane group keeps in flight
+
+// Row r of the block's rows (token-major: tk = r / hsum, head = r % hsum).
+struct RopeRow {
+  int64_t xb, yb;
+  int tk;
+  bool isk;
+};
+
+// The q and k tensor descriptors, read once into wave-uniform registers so a
+// row's q/k choice is a register select rather than a per-lane load from the
+// kernel-argument segment (such loads would sit in the same in-order memory
+// counter as the data loads and drain them at every wait).
+struct RopePair {
+  const void* x[2];
+  void* y[2];
+  int64_t xs0[2], xs1[2], xs2[2], ys0[2], ys1[2], ys2[2];
+  int qheads;
+};
+
+__device__ inline RopePair rope_pair(const RopeArgs& a) {
+  RopePair p;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    p.x[i] = a.t[i].x;
+    p.y[i] = a.t[i].y;
+    p.xs0[i] = a.t[i].xs0; p.xs1[i] = a.t[i].xs1; p.xs2[i] = a.t[i].xs2;
+    p.ys0[i] = a.t[i].ys0; p.ys1[i] = a.t[i].ys1; p.ys2[i] = a.t[i].ys2;
+  }
+  p.qheads = a.t[0].heads;
+  return p;
+}
+
+__device__ inline RopeRow rope_row(const RopeArgs& a, const RopePair& p, uint32_t t0, int r) {
+  RopeRow o;
+  o.tk = r / a.hsum;
+  const int h = r - o.tk * a.hsum;
+  o.isk = h >= p.qheads;
+  const int hh = o.isk ? h - p.qheads : h;
+  const uint32_t tok = t0 + o.tk;
+  const uint32_t b = tok / a.L, l = tok - b * a.L;
+  o.xb = (int64_t)b * (o.isk ? p.xs0[1] : p.xs0[0]) + (int64_t)l * (o.isk ? p.xs1[1] : p.xs1[0]) +
+         (int64_t)hh * (o.isk ? p.xs2[1] : p.xs2[0]);
+  o.yb = (int64_t)b * (o.isk ? p.ys0[1] : p.ys0[0]) + (int64_t)l * (o.isk ? p.ys1[1] : p.ys1[0]) +
+         (int64_t)hh * (o.isk ? p.ys2[1] : p.ys2[0]);
+  return o;
+}
+
 template <class X, int LPR, bool NORM>
 __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
   constexpr int V = Vec<X>::N;
+  constexpr int RB = kRopeBatch;
+  constexpr int slots = 256 / LPR;
   extern __shared__ float smem[];
   float* cs = smem;
   float* sn = smem + a.tpb * a.half;
   const uint32_t t0 = blockIdx.x * (uint32_t)a.tpb;
   const int ntok = (int)min((uint32_t)a.tpb, a.tokens - t0);
-  fill_table<X>(a, cs, sn, t0, ntok);
-  __syncthreads();
-
-  const int slots = blockDim.x / LPR;
+  const int rows = ntok * a.hsum;
   const int slot = threadIdx.x / LPR;
   const int j = threadIdx.x % LPR;
   const bool rot = j < a.R;
   const int c0 = rot ? j : 2 * j;
   const int c1 = rot ? j + a.R : 2 * j + 1;
 
-  float wq[2][V], wk[2][V];
+  // norm weights of q and k for this lane's two chunks, packed
+  u32x4 w0q{1u, 1u, 1u, 1u}, w1q = w0q, w0k = w0q, w1k = w0q;
   if constexpr (NORM) {
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const void* nw = a.t[h].nw;
-      float(*w)[V] = h ? wk : wq;
-      if (nw) {
-        load_chunk<X>(nw, c0 * V, w[0]);
-        load_chunk<X>(nw, c1 * V, w[1]);
-      } else {
-#pragma unroll
-        for (int e = 0; e < V; ++e) w[0][e] = w[1][e] = 1.0f;
-      }
-    }
+    if (a.t[0].nw) { w0q = ld16<X>(a.t[0].nw, c0 * V); w1q = ld16<X>(a.t[0].nw, c1 * V); }
+    if (a.t[1].nw) { w0k = ld16<X>(a.t[1].nw, c0 * V); w1k = ld16<X>(a.t[1].nw, c1 * V); }
   }
 
-  const int rows = ntok * a.hsum;
-  for (int rr = slot; rr < rows; rr += slots) {
-    const int tk = rr / a.hsum;
-    const int h = rr - tk * a.hsum;
-    const bool isk = h >= a.t[0].heads;
-    const int hh = isk ? h - a.t[0].heads : h;
-    const uint32_t tok = t0 + tk;
-    const uint32_t b = tok / a.L, l = tok - b * a.L;
-    const void* xp = isk ? a.t[1].x : a.t[0].x;
-    void* yp = isk ? a.t[1].y : a.t[0].y;
-    const int64_t xb = (int64_t)b * (isk ? a.t[1].xs0 : a.t[0].xs0) +
-                       (int64_t)l * (isk ? a.t[1].xs1 : a.t[0].xs1) +
-                       (int64_t)hh * (isk ? a.t[1].xs2 : a.t[0].xs2);
-    const int64_t yb = (int64_t)b * (isk ? a.t[1].ys0 : a.t[0].ys0) +
-                       (int64_t)l * (isk ? a.t[1].ys1 : a.t[0].ys1) +
-                       (int64_t)hh * (isk ? a.t[1].ys2 : a.t[0].ys2);
-    float v0[V], v1[V];
-    load_chunk<X>(xp, xb + c0 * V, v0);
-    load_chunk<X>(xp, xb + c1 * V, v1);
-    if constexpr (NORM) {
-      const bool has = isk ? (a.t[1].nw != nullptr) : (a.t[0].nw != nullptr);
-      if (has) {  // uniform across the row's lane group
-        double ss = 0.0;
+  const RopePair pr = rope_pair(a);
+  u32x4 d0[RB], d1[RB];
+  RopeRow rw[RB];
+  auto load_batch = [&](int base) {
 #pragma unroll
-        for (int e = 0; e < V; ++e) ss = __builtin_fma((double)v0[e], (double)v0[e], ss);
-#pragma unroll
-        for (int e = 0; e < V; ++e) ss = __builtin_fma((double)v1[e], (double)v1[e], ss);
-        ss = group_sum<LPR>(ss);
-        const float r = rms_scale(ss, a.inv_d, a.eps);
-#pragma unroll
-        for (int e = 0; e < V; ++e) {
-          const float w0 = isk ? wk[0][e] : wq[0][e];
-          const float w1 = isk ? wk[1][e] : wq[1][e];
-          v0[e] = X::round(X::round(v0[e] * r) * w0);
-          v1[e] = X::round(X::round(v1[e] * r) * w1);
-        }
-      }
+    for (int k = 0; k < RB; ++k) {
+      // rows past the block's last are clamped to it (loaded, never stored)
+      const int r = base + k * slots;
+      rw[k] = rope_row(a, pr, t0, r < rows ? r : rows - 1);
+      const void* xp = rw[k].isk ? pr.x[1] : pr.x[0];
+      d0[k] = ld16<X>(xp, rw[k].xb + c0 * V);
+      d1[k] = ld16<X>(xp, rw[k].xb + c1 * V);
     }
-    if (rot) {
-      const float* cp = cs + tk * a.half + j * V;
-      const float* sp = sn + tk * a.half + j * V;
+  };
+
+  // the first batch's loads go out before the block spends time on sincos
+  load_batch(slot);
+  fill_table<X>(a, cs, sn, t0, ntok);
+  __syncthreads();
+
+  for (int base = slot;;) {
+#pragma unroll
+    for (int k = 0; k < RB; ++k) {
+      const int r = base + k * slots;
+      if (r >= rows) break;
+      const bool isk = rw[k].isk;
+      float v0[V], v1[V];
 #pragma unroll
       for (int e = 0; e < V; ++e) {
-        const float c = cp[e], s = sp[e];
-        const float x1 = v0[e], x2 = v1[e];
-        const float y1 = X::round(X::round(x1 * c) - X::round(x2 * s));
-        const float y2 = X::round(X::round(x1 * s) + X::round(x2 * c));
-        v0[e] = y1;
-        v1[e] = y2;
+        v0[e] = elem<X>(d0[k], e);
+        v1[e] = elem<X>(d1[k], e);
       }
+      if constexpr (NORM) {
+        const bool has = isk ? (a.t[1].nw != nullptr) : (a.t[0].nw != nullptr);
+        if (has) {  // uniform across the row's lane group
+          double ss = 0.0;
+#pragma unroll
+          for (int e = 0; e < V; ++e) ss = __builtin_fma((double)v0[e], (double)v0[e], ss);
+#pragma unroll
+          for (int e = 0; e < V; ++e) ss = __builtin_fma((double)v1[e], (double)v1[e], ss);
+          ss = group_sum<LPR>(ss);
+          const float rs = rms_scale(ss, a.inv_d, a.eps);
+          const u32x4 wa = isk ? w0k : w0q, wb = isk ? w1k : w1q;
+#pragma unroll
+          for (int e = 0; e < V; ++e) {
+            v0[e] = X::round(X::round(v0[e] * rs) * elem<X>(wa, e));
+            v1[e] = X::round(X::round(v1[e] * rs) * elem<X>(wb, e));
+          }
+        }
+      }
+      if (rot) {
+        const float* cp = cs + rw[k].tk * a.half + j * V;
+        const float* sp = sn + rw[k].tk * a.half + j * V;
+#pragma unroll
+        for (int e = 0; e < V; ++e) {
+          const float c = cp[e], s = sp[e];
+          const float x1 = v0[e], x2 = v1[e];
+          v0[e] = X::round(X::round(x1 * c) - X::round(x2 * s));
+          v1[e] = X::round(X::round(x1 * s) + X::round(x2 * c));
+        }
+      }
+      void* yp = isk ? pr.y[1] : pr.y[0];
+      store_elems<X, V>(yp, rw[k].yb + c0 * V, v0);
+      store_elems<X, V>(yp, rw[k].yb + c1 * V, v1);
     }
-    store_elems<X, V>(yp, yb + c0 * V, v0);
-    store_elems<X, V>(yp, yb + c1 * V, v1);
+    base += slots * RB;
+    if (base >= rows) break;
+    load_batch(base);
   }
 }
 
