@@ -8,45 +8,26 @@
 //
 // SwiGLU arithmetic is MLX's CPU composition, bit for bit:
 //   sig = round_T(sigmoid(g)); s = round_T(g * sig); out = round_T(s * u)
-// with MLX's sigmoid (1/(1+exp(|g|)), complemented for g >= 0) and MLX's
-// polynomial exp, built from IEEE operations only.
+// with MLX's sigmoid (y = 1/(1+exp(|g|)); g < 0 ? y : 1-y) and MLX's
+// polynomial exp, built from IEEE operations only. That exact sigmoid costs
+// ~40 VALU operations per element and would make the kernel compute-bound, so
+// for 16-bit inputs the kernel first evaluates the same formula with the
+// hardware exp2 and reciprocal, and keeps it only when the result cannot round
+// differently: |g| <= 64 (there the fast value is within 3 f32 ulps of the
+// exact one, measured over every 16-bit input) and the value is more than
+// kTieWindow ulps from a rounding tie of T. Everything else takes the exact
+// path. Since a 16-bit input has only 65536 values, the tests check the result
+// for all of them.
+//
 // GeGLU runs in f32 (mlx-rs builds gelu_approximate from f32 scalar arrays,
 // which promote a bf16 input): 0.5*g*(1+tanh(k0*(g + k1*g^3))) is evaluated as
 // the identical g / (1 + exp(-2*k0*(g + k1*g^3))), using the hardware exp2 and
 // reciprocal (relative error ~1e-6), and the product with up is rounded once.
-//
-// Large 16-bit SwiGLU: the exact sigmoid costs ~40 VALU operations per element,
-// which would make the kernel compute-bound. But round_T(g * round_T(sig(g)))
-// depends only on the 16 bits of g, so a 64K-entry table of it (built once per
-// device by the exact code path) is held in LDS (128 KB of gfx950's 160 KB per
-// CU) by one 1024-thread block per CU; each element then costs one LDS lookup,
-// one multiply and one conversion, bit-identical to the direct path.
-#include <mutex>
-
 #include "../../include/higgs_hip.h"
 #include "hgk_common.h"
 #include "hgk_host.h"
 
 namespace hgk {
-
-// s = round_T(g * round_T(sigmoid(g))) for every 16-bit pattern g.
-__device__ uint16_t g_silu_lut_bf16[65536];
-__device__ uint16_t g_silu_lut_f16[65536];
-
-template <class X>
-__device__ inline uint16_t* silu_lut() {
-  if constexpr (X::kCode == DT_BF16) return g_silu_lut_bf16;
-  else return g_silu_lut_f16;
-}
-
-template <class X>
-__global__ __launch_bounds__(256) void silu_lut_init_kernel() {
-  const uint32_t i = blockIdx.x * 256u + threadIdx.x;
-  const float g = X::lo(i);
-  const float sg = X::round(mlx_sigmoid(g));
-  const float s = X::round(g * sg);
-  silu_lut<X>()[i] = (uint16_t)(X::pack(s, 0.0f) & 0xffffu);
-}
 
 struct GluArgs {
   const void* g;
@@ -60,12 +41,67 @@ struct GluArgs {
   int contig;      // all three tensors densely packed
 };
 
+constexpr int kTieWindow = 16;  // f32 ulps; the fast sigmoid errs by <= 3
+
+// True when the f32 value `b` (bits) lies within kTieWindow ulps of a value
+// halfway between two neighbours of T, or where T's rounding is not decided
+// by the low bits alone (f16 subnormal range).
+template <class X>
+__device__ inline bool near_tie(uint32_t b) {
+  if constexpr (X::kCode == DT_BF16) {
+    const int d = (int)(b & 0xffffu) - 0x8000;
+    return d <= kTieWindow && d >= -kTieWindow;
+  } else {
+    const int d = (int)(b & 0x1fffu) - 0x1000;
+    return (d <= kTieWindow && d >= -kTieWindow) || (b & 0x7fffffffu) < 0x38800000u;
+  }
+}
+
+// Fast sigmoid with MLX's branch structure; *slow is set when the result may
+// round differently from the exact one.
+template <class X>
+__device__ inline float sigmoid16_fast(float g, bool* slow) {
+  const float e = __builtin_amdgcn_exp2f(fabsf(g) * 1.4426950408889634f);
+  const float y = __builtin_amdgcn_rcpf(1.0f + e);
+  const float sg = g < 0.0f ? y : 1.0f - y;
+  *slow = !(fabsf(g) <= 64.0f) || near_tie<X>(f2u(sg));  // !(<=) also catches NaN
+  return sg;
+}
+
+// N SwiGLU outputs round_T(round_T(g*round_T(sigmoid(g))) * u) for 16-bit T,
+// bit-identical to the exact MLX composition: all fast sigmoids first, then
+// one (rarely taken) branch that redoes the flagged ones exactly.
+template <class X, int N>
+__device__ inline void swiglu16(const float* g, const float* u, float* o) {
+  float sg[N];
+  bool fl[N];
+  bool any = false;
+#pragma unroll
+  for (int e = 0; e < N; ++e) {
+    sg[e] = sigmoid16_fast<X>(g[e], &fl[e]);
+    any |= fl[e];
+  }
+  if (any) {
+#pragma unroll
+    for (int e = 0; e < N; ++e)
+      if (fl[e]) sg[e] = mlx_sigmoid(g[e]);
+  }
+#pragma unroll
+  for (int e = 0; e < N; ++e) o[e] = X::round(X::round(g[e] * X::round(sg[e])) * u[e]);
+}
+
 template <class X, int ACT>
 __device__ inline float glu1(float g, float u) {
   if constexpr (ACT == HGK_ACT_SILU) {
-    const float sg = X::round(mlx_sigmoid(g));
-    const float s = X::round(g * sg);
-    return X::round(s * u);
+    if constexpr (X::kBytes == 2) {
+      float o;
+      swiglu16<X, 1>(&g, &u, &o);
+      return o;
+    } else {
+      const float sg = X::round(mlx_sigmoid(g));
+      const float s = X::round(g * sg);
+      return X::round(s * u);
+    }
   } else {
     const float k0 = 0.7978845608028654f, k1 = 0.044715f;
     const float g3 = g * g * g;
@@ -108,12 +144,27 @@ __global__ __launch_bounds__(256) void glu_kernel(GluArgs a) {
     gr[k] = ld16<X>(a.g, go);
     ur[k] = ld16<X>(a.u, uo);
   }
+  if constexpr (ACT == HGK_ACT_SILU && X::kBytes == 2) {
+    float gv[U * V], uv[U * V], o[U * V];
 #pragma unroll
-  for (int k = 0; k < U; ++k) {
-    float o[V];
+    for (int k = 0; k < U; ++k)
 #pragma unroll
-    for (int e = 0; e < V; ++e) o[e] = glu1<X, ACT>(elem<X>(gr[k], e), elem<X>(ur[k], e));
-    if (base + 256u * k < a.total) store_elems<Y, V>(a.o, oo[k], o);
+      for (int e = 0; e < V; ++e) {
+        gv[k * V + e] = elem<X>(gr[k], e);
+        uv[k * V + e] = elem<X>(ur[k], e);
+      }
+    swiglu16<X, U * V>(gv, uv, o);
+#pragma unroll
+    for (int k = 0; k < U; ++k)
+      if (base + 256u * k < a.total) store_elems<Y, V>(a.o, oo[k], o + k * V);
+  } else {
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      float o[V];
+#pragma unroll
+      for (int e = 0; e < V; ++e) o[e] = glu1<X, ACT>(elem<X>(gr[k], e), elem<X>(ur[k], e));
+      if (base + 256u * k < a.total) store_elems<Y, V>(a.o, oo[k], o);
+    }
   }
 }
 
@@ -127,110 +178,10 @@ __global__ __launch_bounds__(256) void glu_generic_kernel(GluArgs a, int64_t n, 
   store1<Y>(a.o, row * a.os + c, glu1<X, ACT>(g, u));
 }
 
-constexpr int kLutBlock = 1024;
-constexpr int kLutUnroll = 4;
-
-// Persistent SwiGLU for 16-bit X: one 1024-thread block per CU loads the silu
-// table into LDS once, then strides over the tensor kLutUnroll chunks per
-// thread at a time (all loads of a step issued before any lookup).
-template <class X, class Y, bool CONTIG>
-__global__ __launch_bounds__(kLutBlock) void swiglu_lut_kernel(GluArgs a) {
-  constexpr int V = Vec<X>::N;
-  constexpr int U = kLutUnroll;
-  __shared__ uint16_t lut[65536];
-  const uint32_t per_iter = (uint32_t)kLutBlock * U;
-  const uint32_t stride = gridDim.x * per_iter;
-  u32x4 gr[U], ur[U];
-  int64_t oo[U];
-  auto load_step = [&](uint32_t base) {
-#pragma unroll
-    for (int k = 0; k < U; ++k) {
-      const uint32_t q = base + (uint32_t)kLutBlock * k;
-      const uint32_t qq = q < a.total ? q : a.total - 1;
-      int64_t go, uo;
-      glu_offsets<V, CONTIG>(a, qq, go, uo, oo[k]);
-      gr[k] = ld16<X>(a.g, go);
-      ur[k] = ld16<X>(a.u, uo);
-    }
-  };
-  // the first step's loads go out before the 128 KB table copy
-  uint32_t base = blockIdx.x * per_iter + threadIdx.x;
-  load_step(base);
-  {
-    const u32x4* src = reinterpret_cast<const u32x4*>(silu_lut<X>());
-    u32x4* dst = reinterpret_cast<u32x4*>(lut);
-#pragma unroll
-    for (int i = 0; i < 65536 * 2 / 16 / kLutBlock; ++i)
-      dst[i * kLutBlock + threadIdx.x] = src[i * kLutBlock + threadIdx.x];
-  }
-  __syncthreads();
-  while (base < a.total) {
-#pragma unroll
-    for (int k = 0; k < U; ++k) {
-      float o[V];
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const float s0 = X::lo((uint32_t)lut[gr[k][w] & 0xffffu]);
-        const float s1 = X::lo((uint32_t)lut[gr[k][w] >> 16]);
-        o[2 * w] = s0 * X::lo(ur[k][w]);
-        o[2 * w + 1] = s1 * X::hi(ur[k][w]);
-        if constexpr (Y::kCode != X::kCode) {  // MLX's result is X; widen after rounding
-          o[2 * w] = X::round(o[2 * w]);
-          o[2 * w + 1] = X::round(o[2 * w + 1]);
-        }
-      }
-      if (base + (uint32_t)kLutBlock * k < a.total) store_elems<Y, V>(a.o, oo[k], o);
-    }
-    base += stride;
-    if (base < a.total) load_step(base);
-  }
-}
-
 namespace {
-
-constexpr int kMaxDevices = 64;
-std::mutex g_lut_mu;
-bool g_lut_ready[2][kMaxDevices];
-int g_cu_count[kMaxDevices];
-
-// Build the table for X on the current device once; false when that cannot be
-// done right now (stream under graph capture), in which case the caller takes
-// the direct path.
-template <class X>
-bool ensure_silu_lut(hipStream_t s, int* cus) {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return false;
-  const int which = X::kCode == DT_BF16 ? 0 : 1;
-  std::lock_guard<std::mutex> lk(g_lut_mu);
-  if (!g_cu_count[dev]) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-      return false;
-    g_cu_count[dev] = n;
-  }
-  *cus = g_cu_count[dev];
-  if (g_lut_ready[which][dev]) return true;
-  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-  if (hipStreamIsCapturing(s, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return false;
-  hipLaunchKernelGGL((silu_lut_init_kernel<X>), dim3(65536 / 256), dim3(256), 0, s);
-  if (hipGetLastError() != hipSuccess || hipStreamSynchronize(s) != hipSuccess) return false;
-  g_lut_ready[which][dev] = true;
-  return true;
-}
 
 template <class X, class Y, int ACT>
 void launch(const GluArgs& a, bool vec_ok, int64_t rows, int64_t n, hipStream_t s) {
-  if constexpr (ACT == HGK_ACT_SILU && X::kBytes == 2) {
-    int cus = 0;
-    if (vec_ok && a.total >= (1u << 18) && a.total < (1u << 31) && ensure_silu_lut<X>(s, &cus)) {
-      const uint32_t per_block = (uint32_t)kLutBlock * kLutUnroll;
-      const uint32_t need = (a.total + per_block - 1) / per_block;
-      const unsigned blocks = need < (uint32_t)cus ? need : (unsigned)cus;
-      if (a.contig) hipLaunchKernelGGL((swiglu_lut_kernel<X, Y, true>), dim3(blocks), dim3(kLutBlock), 0, s, a);
-      else hipLaunchKernelGGL((swiglu_lut_kernel<X, Y, false>), dim3(blocks), dim3(kLutBlock), 0, s, a);
-      return;
-    }
-  }
   if (vec_ok) {
     if (a.total >= 256u * 4u * 1024u) {
       const unsigned blocks = (a.total + 1024u - 1u) / 1024u;
@@ -281,7 +232,7 @@ extern "C" int hgk_glu(int act, int dtype, const void* gate, int64_t gate_row_st
   if (rows == 0 || n == 0) return HGK_OK;
   const int V = 16 / dtype_bytes(dtype);
   const int64_t chunks = (n / V) * rows;
-  if (chunks >= ((int64_t)1 << 32) || n * rows >= ((int64_t)1 << 40))
+  if (chunks >= ((int64_t)1 << 31) || n * rows >= ((int64_t)1 << 40))
     return fail(HGK_ERR_UNSUPPORTED, "hgk_glu: problem too large");
   GluArgs a{};
   a.g = gate; a.gs = gate_row_stride; a.u = up; a.us = up_row_stride;

@@ -233,10 +233,27 @@ __device__ inline float group_sum(float v) {
   return v;
 }
 
+// Value of `v` from the partner lane selected by a DPP control (row-local).
+template <int CTRL>
+__device__ inline double dpp_partner(double v) {
+  const uint64_t b = __builtin_bit_cast(uint64_t, v);
+  const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, CTRL, 0xF, 0xF, true);
+  const int hi = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)(b >> 32), CTRL, 0xF, 0xF, true);
+  return __builtin_bit_cast(double, ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
+}
+
+// f64 sum over aligned groups of W lanes. Within a 16-lane row the partners
+// come from DPP (quad_perm xor 1, xor 2, half-row mirror, row mirror: each an
+// involution, so every lane adds the same pair and ends with the same bits);
+// wider groups finish with cross-row shuffles.
 template <int W>
 __device__ inline double group_sum(double v) {
-#pragma unroll
-  for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, W);
+  if constexpr (W >= 2) v += dpp_partner<0xB1>(v);   // quad_perm [1,0,3,2]
+  if constexpr (W >= 4) v += dpp_partner<0x4E>(v);   // quad_perm [2,3,0,1]
+  if constexpr (W >= 8) v += dpp_partner<0x141>(v);  // row_half_mirror
+  if constexpr (W >= 16) v += dpp_partner<0x140>(v); // row_mirror
+  if constexpr (W >= 32) v += __shfl_xor(v, 16, W);
+  if constexpr (W >= 64) v += __shfl_xor(v, 32, W);
   return v;
 }
 

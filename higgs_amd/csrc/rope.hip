@@ -273,13 +273,13 @@ __global__ __launch_bounds__(256) void rope_generic_kernel(RopeArgs a) {
 
 namespace {
 
-int gcd_i(int a, int b) { while (b) { int t = a % b; a = b; b = t; } return a; }
 
 template <class X, int LPR, bool NORM>
 void launch_fast(RopeArgs& a, hipStream_t s) {
+  // as many tokens per block as keep every lane group's rows in one batch of
+  // loads, but enough blocks to fill the chip
   const int slots = 256 / LPR;
-  int tpb = slots / gcd_i(slots, a.hsum);  // lcm(slots, hsum) / hsum
-  tpb = std::max(1, std::min(tpb, kMaxTpb));
+  int tpb = std::max(1, std::min((slots * kRopeBatch) / a.hsum, kMaxTpb));
   while (tpb > 1 && (a.tokens + tpb - 1) / tpb < 1024u) tpb = (tpb + 1) / 2;
   a.tpb = tpb;
   const unsigned blocks = (a.tokens + tpb - 1) / tpb;

@@ -230,6 +230,32 @@ def test_swiglu_bitexact(dev, dt):
     assert np.array_equal(got, ref)
 
 
+def _same_bits_nan_aware(got, ref, dt):
+    from bits import nan_mask
+    gn, rn = nan_mask(got, dt), nan_mask(ref, dt)
+    assert np.array_equal(gn, rn), "NaN positions differ"
+    bad = (got != ref) & ~gn
+    assert not bad.any(), f"{int(bad.sum())} elements differ, first at {np.argwhere(bad)[0]}"
+
+
+@pytest.mark.parametrize("dt", [O.BF16, O.F16])
+def test_swiglu_every_16bit_gate_value(dev, dt):
+    """The 16-bit SwiGLU keeps a fast sigmoid only where it provably rounds like
+    MLX's exact one; check that claim for all 65536 gate bit patterns
+    (subnormals, infinities and NaNs included), through both launch shapes."""
+    codes = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    g = codes.reshape(256, 256)
+    one = O.from_f32(np.ones((256, 256), np.float32), dt)
+    ref = O.glu(O.ACT_SILU, g, one, dt)
+    got = to_host(H.swiglu(to_dev(g, dt, dev), to_dev(one, dt, dev)))
+    _same_bits_nan_aware(got, ref, dt)
+    gt = np.ascontiguousarray(np.tile(codes, 512).reshape(4096, 8192))
+    u = O.from_f32(O.normal(1901 + dt, (4096, 8192)), dt)
+    ref = O.glu(O.ACT_SILU, gt, u, dt)
+    got = to_host(H.swiglu(to_dev(gt, dt, dev), to_dev(u, dt, dev)))
+    _same_bits_nan_aware(got, ref, dt)
+
+
 def test_swiglu_reference_known_answers(dev):
     g = torch.tensor([[0.0, 1.0, -1.0]], device=dev)
     u = torch.tensor([[5.0, 1.0, 2.0]], device=dev)
