@@ -71,6 +71,16 @@ struct F32 {
 // Elements of T per 16-byte chunk.
 template <class T> struct Vec { static constexpr int N = 16 / T::kBytes; };
 
+// Round two f32 values to T in place with one packed conversion.
+template <class T>
+__device__ inline void round2(float& a, float& b) {
+  if constexpr (T::kBytes == 2) {
+    const uint32_t p = T::pack(a, b);
+    a = T::lo(p);
+    b = T::hi(p);
+  }
+}
+
 // ---------------------------------------------------------------- chunk I/O
 template <class T>
 __device__ inline void unpack16(u32x4 r, float* v) {

@@ -99,27 +99,40 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(NormArgs a) {
   ss = group_sum<LPR>(ss);
   const float rr = rms_scale(ss, a.inv_n, a.eps);
 
+  // Roundings to X go in pairs (one packed conversion for two values). The
+  // last rounding of each output is the store's own conversion when Y is X.
+  const bool rx = a.round_x != 0;
 #pragma unroll
   for (int c = 0; c < CPL; ++c) {
     const int ch = j + c * LPR;
     if (ch >= nchunks) continue;
     float o[V];
 #pragma unroll
-    for (int e = 0; e < V; ++e) {
-      float nv = elem<X>(xr[c], e) * rr;
-      nv = a.round_x ? X::round(nv) : nv;
-      const float w0 = has_w ? elem<W>(wr[c], e) : 1.0f;
-      const float we = a.plus_one ? w0 + 1.0f : w0;
-      nv = nv * we;
-      nv = a.round_x ? X::round(nv) : nv;
-      if constexpr (GATED) {
-        const float zz = elem<X>(zr[c], e);
-        const float sg = X::round(mlx_sigmoid(zz));
-        const float act = X::round(zz * sg);
-        nv = act * nv;
-        nv = a.round_x ? X::round(nv) : nv;
+    for (int e = 0; e < V; e += 2) {
+      float n0 = elem<X>(xr[c], e) * rr, n1 = elem<X>(xr[c], e + 1) * rr;
+      if (rx) round2<X>(n0, n1);
+      float w0 = has_w ? elem<W>(wr[c], e) : 1.0f, w1 = has_w ? elem<W>(wr[c], e + 1) : 1.0f;
+      if (a.plus_one) {
+        w0 = w0 + 1.0f;
+        w1 = w1 + 1.0f;
       }
-      o[e] = nv;
+      n0 = n0 * w0;
+      n1 = n1 * w1;
+      if constexpr (GATED) {
+        if (rx) round2<X>(n0, n1);
+        const float z0 = elem<X>(zr[c], e), z1 = elem<X>(zr[c], e + 1);
+        float s0 = mlx_sigmoid(z0), s1 = mlx_sigmoid(z1);
+        round2<X>(s0, s1);
+        float g0 = z0 * s0, g1 = z1 * s1;
+        round2<X>(g0, g1);
+        n0 = g0 * n0;
+        n1 = g1 * n1;
+      }
+      if constexpr (Y::kCode != X::kCode) {
+        if (rx) round2<X>(n0, n1);
+      }
+      o[e] = n0;
+      o[e + 1] = n1;
     }
     if (live) store_elems<Y, V>(a.y, r * a.ys + (int64_t)ch * V, o);
   }

@@ -185,21 +185,39 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
           const float rs = rms_scale(ss, a.inv_d, a.eps);
           const u32x4 wa = isk ? w0k : w0q, wb = isk ? w1k : w1q;
 #pragma unroll
-          for (int e = 0; e < V; ++e) {
-            v0[e] = X::round(X::round(v0[e] * rs) * elem<X>(wa, e));
-            v1[e] = X::round(X::round(v1[e] * rs) * elem<X>(wb, e));
+          for (int e = 0; e < V; e += 2) {  // roundings paired: one conversion per two
+            float p0 = v0[e] * rs, p1 = v0[e + 1] * rs, q0 = v1[e] * rs, q1 = v1[e + 1] * rs;
+            round2<X>(p0, p1);
+            round2<X>(q0, q1);
+            p0 = p0 * elem<X>(wa, e);
+            p1 = p1 * elem<X>(wa, e + 1);
+            q0 = q0 * elem<X>(wb, e);
+            q1 = q1 * elem<X>(wb, e + 1);
+            round2<X>(p0, p1);
+            round2<X>(q0, q1);
+            v0[e] = p0; v0[e + 1] = p1; v1[e] = q0; v1[e + 1] = q1;
           }
         }
       }
       if (rot) {
+        // y1 = round(round(x1*c) - round(x2*s)), y2 = round(round(x1*s) + round(x2*c));
+        // the outer rounding happens in the store's packing conversion
         const float* cp = cs + rw[k].tk * a.half + j * V;
         const float* sp = sn + rw[k].tk * a.half + j * V;
 #pragma unroll
-        for (int e = 0; e < V; ++e) {
-          const float c = cp[e], s = sp[e];
-          const float x1 = v0[e], x2 = v1[e];
-          v0[e] = X::round(X::round(x1 * c) - X::round(x2 * s));
-          v1[e] = X::round(X::round(x1 * s) + X::round(x2 * c));
+        for (int e = 0; e < V; e += 2) {
+          const float c0 = cp[e], s0 = sp[e], c1 = cp[e + 1], s1 = sp[e + 1];
+          const float x10 = v0[e], x20 = v1[e], x11 = v0[e + 1], x21 = v1[e + 1];
+          float a0 = x10 * c0, a1 = x11 * c1, b0 = x20 * s0, b1 = x21 * s1;
+          float d0 = x10 * s0, d1 = x11 * s1, f0 = x20 * c0, f1 = x21 * c1;
+          round2<X>(a0, a1);
+          round2<X>(b0, b1);
+          round2<X>(d0, d1);
+          round2<X>(f0, f1);
+          v0[e] = a0 - b0;
+          v0[e + 1] = a1 - b1;
+          v1[e] = d0 + f0;
+          v1[e + 1] = d1 + f1;
         }
       }
       void* yp = isk ? pr.y[1] : pr.y[0];
