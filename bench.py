@@ -46,18 +46,16 @@ class Kernel:
     back to torch's caching allocator, and graph capture (which empties that
     cache) would unmap it under the launches."""
 
-    def __init__(self, name, nbytes, fn, argsets, tokens=0, keep=()):
+    def __init__(self, name, nbytes, fn, argsets, tokens=0, keep=(), cpu=None):
         self.name, self.bytes, self.fn, self.tokens = name, nbytes, fn, tokens
         self.argsets = [tuple(a) for a in argsets]
         self.keep = keep
+        self.cpu = cpu  # (kind, params) for the oracle's timing of the same op
 
     def launch(self, s):
         st = self.fn(*self.argsets[s])
         if st:
             raise RuntimeError(f"{self.name}: status {st}")
-
-    def restream(self, stream):
-        self.argsets = [a[:-1] + (stream,) for a in self.argsets]
 
 
 class Workload:
@@ -127,21 +125,24 @@ def k_embed(cx, name, sets, tab, V, Hd, n, scale=0.0, group=64):
     nbytes = n * (Hd // 2 + 2 * 2 * (Hd // group) + 4 + Hd * 2)
     args = [(_vp(ids), I32, n, _vp(wq), _vp(sc), _vp(bi), BF16, V, Hd, group, 4, _f(scale),
              _vp(out), Hd, cx.stream) for ids, out in sets]
-    return Kernel(name, nbytes, cx.lib.hgk_quantized_embedding, args, n, keep=(sets, tab))
+    return Kernel(name, nbytes, cx.lib.hgk_quantized_embedding, args, n, keep=(sets, tab),
+                  cpu=("qembed", dict(V=V, H=Hd, n=n, scale=scale, group=group)))
 
 
 def k_rmsnorm(cx, name, sets, w, rows, n, eps, plus_one=0, ydt=BF16):
     nbytes = rows * n * 2 + rows * n * (4 if ydt == F32 else 2) + n * 2
     args = [(_vp(x), BF16, n, _vp(w), BF16, plus_one, _f(eps), _vp(y), ydt, n, rows, n,
              cx.stream) for x, y in sets]
-    return Kernel(name, nbytes, cx.lib.hgk_rms_norm, args, rows, keep=(sets, w))
+    return Kernel(name, nbytes, cx.lib.hgk_rms_norm, args, rows, keep=(sets, w),
+                  cpu=("rms", dict(rows=rows, n=n, eps=eps, plus_one=plus_one, ydt=ydt)))
 
 
 def k_glu(cx, name, sets, rows, n, act):
     nbytes = 3 * rows * n * 2
     args = [(act, BF16, _vp(g), n, _vp(u), n, _vp(o), BF16, n, rows, n, cx.stream)
             for g, u, o in sets]
-    return Kernel(name, nbytes, cx.lib.hgk_glu, args, rows, keep=(sets,))
+    return Kernel(name, nbytes, cx.lib.hgk_glu, args, rows, keep=(sets,),
+                  cpu=("glu", dict(rows=rows, n=n, act=act)))
 
 
 def k_qkrope(cx, name, sets, B, L, Hq, Hk, D, dims, base, freqs=None, wq=None, wk=None,
@@ -164,14 +165,18 @@ def k_qkrope(cx, name, sets, B, L, Hq, Hk, D, dims, base, freqs=None, wq=None, w
              B, L, D, dims, _f(base), _f(1.0), fr, 0,
              None if offsets is None else _vp(offsets), cx.stream) for q, k, qo, ko in sets]
     return Kernel(name, nbytes, cx.lib.hgk_qk_norm_rope, args, B * L,
-                  keep=(sets, wq, wk, offsets, fr, qs, ks, qos, kos))
+                  keep=(sets, wq, wk, offsets, fr, qs, ks, qos, kos),
+                  cpu=("rope", dict(B=B, L=L, Hq=Hq, Hk=Hk, D=D, dims=dims, base=base,
+                                    freqs=freqs, norm=wq is not None, eps=eps,
+                                    offsets=offsets is not None)))
 
 
 def k_gated(cx, name, sets, w, rows, n, eps, zrow, zgroup, zgs):
     nbytes = 3 * rows * n * 2 + n * 2
     args = [(BF16, _vp(y), n, _vp(z), zrow, zgroup, zgs, _vp(w), BF16, _f(eps), _vp(o), BF16,
              n, rows, n, cx.stream) for y, z, o in sets]
-    return Kernel(name, nbytes, cx.lib.hgk_gated_rms_norm, args, rows, keep=(sets, w))
+    return Kernel(name, nbytes, cx.lib.hgk_gated_rms_norm, args, rows, keep=(sets, w),
+                  cpu=("gated", dict(rows=rows, n=n, eps=eps)))
 
 
 def wl_llama_chain(cx):
@@ -212,7 +217,7 @@ def wl_rmsnorm_512(cx):
     cfg = {"workload": "rmsnorm alone", "rows": rows, "hidden": n, "eps": 1e-5,
            "buffer_sets": ns}
     return Workload("rmsnorm_512x2048", cfg, [k_rmsnorm(cx, "rms_norm", sets, w, rows, n, 1e-5)],
-                    ns, rows)
+                    ns, rows, graph=True)
 
 
 def wl_qwen3_prefill(cx):
@@ -349,29 +354,93 @@ class HipEvents:
             self.h.hipEventDestroy(e)
 
 
+def _capture(cx, launches):
+    """One HIP graph holding `launches` (callables taking a stream), captured
+    on a side stream at the default priority."""
+    torch = cx.torch
+    side = torch.cuda.Stream(cx.dev)
+    sh = C.c_void_p(side.cuda_stream)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        for fn in launches:
+            fn(sh)  # eager pass on the capture stream first
+        side.synchronize()
+        with torch.cuda.graph(g, stream=side):
+            for fn in launches:
+                fn(sh)
+    return g
+
+
+def _launcher(k, s):
+    def fn(stream):
+        a = k.argsets[s]
+        if k.fn(*(a[:-1] + (stream,))):
+            raise RuntimeError(f"{k.name}: status != 0")
+    return fn
+
+
+def kernel_times(cx, wl, graph, per_group=20, groups=5):
+    """Average launch duration of each distinct kernel: `per_group` launches
+    of it back to back over the rotating buffer sets, in `groups` groups
+    bracketed by HIP events on the stream the kernels run on.
+
+    Eager (graph=False): launched from the host; this agrees with rocprofv3's
+    per-dispatch durations for kernels longer than the host launch cost
+    (~6 us through ctypes). Graph (graph=True): each group is one captured
+    HIP graph, which hides the host cost but adds a per-node dispatch cost of
+    its own (~3 us per node measured on MI355X), so small kernels read high;
+    rocprofv3's kernel trace gives their device durations."""
+    torch = cx.torch
+    he = HipEvents()
+    rec = he.h.hipEventRecord
+    st = cx.stream
+    seen, per = set(), []
+    for k in wl.kernels:
+        if k.name in seen:
+            continue
+        seen.add(k.name)
+        if graph:
+            g = _capture(cx, [_launcher(k, i % wl.nsets) for i in range(per_group)])
+            go = g.replay
+        else:
+            plan = [k.argsets[i % wl.nsets] for i in range(per_group)]
+
+            def go(plan=plan, fn=k.fn, name=k.name):
+                for a in plan:
+                    if fn(*a):
+                        raise RuntimeError(f"{name}: {cx.lib.hgk_last_error().decode()}")
+        go()  # warm
+        torch.cuda.synchronize()
+        evs = he.create(groups + 1)
+        rec(evs[0], st)
+        for i in range(groups):
+            go()
+            rec(evs[i + 1], st)
+        torch.cuda.synchronize()
+        d = sorted(he.elapsed_ms(evs[i], evs[i + 1]) / per_group for i in range(groups))
+        he.destroy(evs)
+        if graph:
+            del g
+        avg = sum(d) / len(d)
+        per.append({"kernel": k.name, "bytes": k.bytes, "avg_us": avg * 1e3,
+                    "median_us": d[len(d) // 2] * 1e3, "best_us": d[0] * 1e3,
+                    "launches": groups * per_group, "method": "graph" if graph else "eager",
+                    "gbs": k.bytes / (avg * 1e-3) / 1e9,
+                    "frac_of_peak": k.bytes / (avg * 1e-3) / 1e9 / PEAK_HBM_GBS})
+    return per
+
+
 def measure(cx, wl, steps, warmup):
     torch = cx.torch
     he = HipEvents()
     rec = he.h.hipEventRecord
     if wl.graph:
-        # launch-bound sequence: one captured graph per buffer set, replayed
-        side = torch.cuda.Stream(cx.dev)
-        sh = C.c_void_p(side.cuda_stream)
-        for k in wl.kernels:
-            k.restream(sh)
-        graphs = []
-        for si in range(wl.nsets):
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.stream(side):
-                for k in wl.kernels:
-                    k.launch(si)  # eager pass on the capture stream first
-                side.synchronize()
-                with torch.cuda.graph(g, stream=side):
-                    for k in wl.kernels:
-                        k.launch(si)
-            graphs.append(g)
-        for k in wl.kernels:
-            k.restream(cx.stream)
+        # launch-bound sequence: captured graphs replayed back to back; each
+        # graph holds `reps` whole steps so one replay's host cost is shared
+        reps = max(1, 200 // len(wl.kernels))
+        graphs = [_capture(cx, [_launcher(k, (si + r) % wl.nsets)
+                                for r in range(reps) for k in wl.kernels])
+                  for si in range(wl.nsets)]
         for i in range(warmup):
             graphs[i % wl.nsets].replay()
         torch.cuda.synchronize()
@@ -383,9 +452,11 @@ def measure(cx, wl, steps, warmup):
         rec(t1, cx.stream)
         torch.cuda.synchronize()
         wall = time.perf_counter() - w0
-        ms = he.elapsed_ms(t0, t1) / steps
+        ms = he.elapsed_ms(t0, t1) / (steps * reps)
         he.destroy([t0, t1])
-        return {"ms_per_step": ms, "wall_ms_per_step": wall * 1e3 / steps, "kernels": None}
+        del graphs
+        return {"ms_per_step": ms, "wall_ms_per_step": wall * 1e3 / (steps * reps),
+                "steps_per_graph": reps, "kernels": kernel_times(cx, wl, graph=True)}
     for i in range(warmup):
         wl.step(i)
     torch.cuda.synchronize()
@@ -409,29 +480,8 @@ def measure(cx, wl, steps, warmup):
     wall = time.perf_counter() - w0
     ms = he.elapsed_ms(t0, t1) / steps
     he.destroy([t0, t1])
-    # per-kernel launch duration: each kernel back to back over the rotating
-    # buffer sets, in groups bracketed by events on the same stream
-    groups, per_group = 5, max(4, steps // 5)
-    per = []
-    for k in wl.kernels:
-        evs = he.create(groups + 1)
-        kp = [(k.fn, k.argsets[i % wl.nsets], k.name) for i in range(per_group)]
-        run(kp)  # warm
-        torch.cuda.synchronize()
-        rec(evs[0], st)
-        for g in range(groups):
-            run(kp)
-            rec(evs[g + 1], st)
-        torch.cuda.synchronize()
-        d = sorted(he.elapsed_ms(evs[g], evs[g + 1]) / per_group for g in range(groups))
-        he.destroy(evs)
-        avg = sum(d) / len(d)
-        per.append({"kernel": k.name, "bytes": k.bytes, "avg_us": avg * 1e3,
-                    "median_us": d[len(d) // 2] * 1e3, "best_us": d[0] * 1e3,
-                    "launches": groups * per_group,
-                    "gbs": k.bytes / (avg * 1e-3) / 1e9,
-                    "frac_of_peak": k.bytes / (avg * 1e-3) / 1e9 / PEAK_HBM_GBS})
-    return {"ms_per_step": ms, "wall_ms_per_step": wall * 1e3 / steps, "kernels": per}
+    return {"ms_per_step": ms, "wall_ms_per_step": wall * 1e3 / steps,
+            "kernels": kernel_times(cx, wl, graph=False)}
 
 
 # ---------------------------------------------------------------- CPU baseline
@@ -474,6 +524,82 @@ def cpu_sample_llama(budget_s=10.0):
             "tokens_per_s": round(T * reps / el, 1), "np_version": np.__version__}
 
 
+def cpu_op(spec, budget_s=1.0):
+    """The oracle timed on a bounded sample of one op of a workload, with the
+    same algorithmic-byte formula as the GPU kernel. Returns GB/s, rows/s, the
+    sample and the thread count."""
+    import numpy as np
+
+    import oracle as O
+
+    kind, p = spec
+    B16 = O.BF16
+    if kind == "rms":
+        R = min(p["rows"], 256)
+        x = O.from_f32(O.normal(7001, (R, p["n"])), B16)
+        w = O.from_f32(O.normal(7002, (p["n"],), 0.0 if p["plus_one"] else 1.0, 0.02), B16)
+        od = O.F32 if p["ydt"] == F32 else B16
+        fn = lambda: O.rms_norm(x, B16, w, B16, p["eps"], plus_one=bool(p["plus_one"]), out_dt=od)
+        nbytes = R * p["n"] * (2 + (4 if od == O.F32 else 2)) + p["n"] * 2
+        rows, what = R, f"{R} of {p['rows']} rows"
+    elif kind == "glu":
+        R = min(p["rows"], 64)
+        g = O.from_f32(O.normal(7003, (R, p["n"])), B16)
+        u = O.from_f32(O.normal(7004, (R, p["n"])), B16)
+        fn = lambda: O.glu(p["act"], g, u, B16)
+        nbytes = 3 * R * p["n"] * 2
+        rows, what = R, f"{R} of {p['rows']} rows"
+    elif kind == "gated":
+        R = min(p["rows"], 1024)
+        y = O.from_f32(O.normal(7005, (R, p["n"])), B16)
+        z = O.from_f32(O.normal(7006, (R, p["n"])), B16)
+        w = O.from_f32(O.normal(7007, (p["n"],), 1.0, 0.02), B16)
+        fn = lambda: O.gated_rms_norm(y, z, B16, w, B16, p["eps"])
+        nbytes = 3 * R * p["n"] * 2 + p["n"] * 2
+        rows, what = R, f"{R} of {p['rows']} rows"
+    elif kind == "rope":
+        D, dims = p["D"], p["dims"]
+        if p["L"] == 1:
+            Bs, Ls = min(p["B"], 64), 1
+        else:
+            Bs, Ls = 1, min(p["L"], 64)
+        q = O.from_f32(O.normal(7008, (Bs, Ls, p["Hq"], D)), B16)
+        k = O.from_f32(O.normal(7009, (Bs, Ls, p["Hk"], D)), B16)
+        wn = O.from_f32(O.normal(7010, (D,), 1.0, 0.02), B16) if p["norm"] else None
+        inv = (O.rope_inv_freq(0.0, dims, np.asarray(p["freqs"], np.float32))
+               if p["freqs"] is not None else O.rope_inv_freq(p["base"], dims))
+        offs = O.offsets(7011, Bs, 1, 32768) if p["offsets"] else None
+        kw = dict(dims=dims, inv_freq=inv, offsets=offs, norm_w=wn,
+                  w_dt=B16 if wn is not None else None, eps=p["eps"])
+        fn = lambda: (O.norm_rope(q, B16, **kw), O.norm_rope(k, B16, **kw))
+        nbytes = Bs * Ls * (p["Hq"] + p["Hk"]) * D * 4 + (2 * D * 2 if wn is not None else 0)
+        rows, what = Bs * Ls, f"{Bs * Ls} of {p['B'] * p['L']} tokens"
+    elif kind == "qembed":
+        V, H, G = p["V"], p["H"], p["group"]
+        T = min(p["n"], 256)
+        wq = O.u32(7012, (V, H // 8))
+        sc = O.from_f32(O.uniform(7013, (V, H // G), 0.005, 0.02), B16)
+        bi = O.from_f32(O.uniform(7014, (V, H // G), -0.1, 0.1), B16)
+        ids = O.ids(7015, T, V)
+        scale = p["scale"]
+        fn = lambda: O.qembed(ids, wq, sc, bi, B16, group=G, out_scale=scale)
+        nbytes = T * (H // 2 + 4 * (H // G) + 4 + 2 * H)
+        rows, what = T, f"{T} of {p['n']} ids (full {V}x{H} table)"
+    else:
+        raise ValueError(kind)
+    fn()
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s and reps >= 2:
+            break
+    cores = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or os.cpu_count()
+    return {"gbs": nbytes * reps / el / 1e9, "rows_per_s": rows * reps / el, "cores": cores,
+            "sample": what, "reps": reps}
+
+
 # ---------------------------------------------------------------- main
 def traffic_for(kernel_name, workload):
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
@@ -500,6 +626,8 @@ def main(argv=None):
     ap.add_argument("--table", action="store_true", help="also measure every workload")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
+    ap.add_argument("--cpu-op-budget", type=float, default=1.0,
+                    help="seconds of oracle time per op for the --table CPU column")
     ap.add_argument("--calib", action="store_true",
                     help="run a plain 256 MiB copy first (counter calibration)")
     args = ap.parse_args(argv)
@@ -557,17 +685,26 @@ def main(argv=None):
                      "gbs": w2.bytes / (rr["ms_per_step"] * 1e-3) / 1e9,
                      "tokens_per_s": w2.tokens / (rr["ms_per_step"] * 1e-3),
                      "kernels": rr["kernels"]}
+                specs = {k.name: k.cpu for k in w2.kernels}
                 del rr, w2
             else:
                 r = {"workload": name, "ms_per_step": ms, "bytes": wl.bytes, "gbs": gbs,
                      "tokens_per_s": line["tokens_per_s"], "kernels": res["kernels"]}
+                specs = {k.name: k.cpu for k in wl.kernels}
+            if not args.no_cpu:
+                # the oracle on a bounded sample of each op, for the CPU column
+                for kd in r["kernels"] or []:
+                    spec = specs.get(kd["kernel"])
+                    kd["cpu"] = None if spec is None else cpu_op(spec, args.cpu_op_budget)
             rows.append(r)
             print(f"[table] {name}: {r['ms_per_step'] * 1e3:.1f} us/step "
                   f"{r['gbs']:.0f} GB/s ({r['gbs'] / PEAK_HBM_GBS:.1%}) "
                   f"{r['tokens_per_s']:.0f} tok/s", file=sys.stderr, flush=True)
             for k in r["kernels"] or []:
+                cpu = k.get("cpu")
+                cpu_txt = (f"   cpu {cpu['gbs']:.2f} GB/s ({cpu['cores']} threads)" if cpu else "")
                 print(f"[table]    {k['kernel']:<24} {k['avg_us']:9.2f} us  {k['gbs']:7.0f} GB/s "
-                      f"({k['frac_of_peak']:.1%})", file=sys.stderr, flush=True)
+                      f"({k['frac_of_peak']:.1%}){cpu_txt}", file=sys.stderr, flush=True)
         os.makedirs("gpurun_out", exist_ok=True)
         with open(os.path.join("gpurun_out", "bench_table.json"), "w") as f:
             json.dump(rows, f, indent=1)

@@ -3,7 +3,8 @@
     python -m higgs_amd.build          # or: python higgs_amd/build.py
 
 Each ``csrc/*.hip`` is compiled to an object in ``higgs_amd/_build`` (in
-parallel), then linked into ``higgs_amd/libhiggs_hip.so``. hipcc cross-compiles
+parallel), then linked into ``higgs_amd/libhiggs_hip.so``. The C++ host API
+(``host/higgs.cpp``) is then built over it into ``higgs_amd/libhiggs.so``. hipcc cross-compiles
 without a GPU, so this runs anywhere the ROCm toolchain is installed.
 """
 from __future__ import annotations
@@ -19,6 +20,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libhiggs_hip.so")
+HOST = os.path.join(HERE, "host")
+HOST_LIB = os.path.join(HERE, "libhiggs.so")
 ARCH = os.environ.get("HGK_OFFLOAD_ARCH", "gfx950")
 
 # -ffp-contract=off: products and sums are rounded separately, exactly as the
@@ -66,7 +69,28 @@ def build(verbose: bool = True) -> str:
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB}")
+    build_host(verbose)
     return LIB
+
+
+def build_host(verbose: bool = True) -> str:
+    """libhiggs.so: the C++ host API (host/higgs.hpp) over libhiggs_hip.so."""
+    cxx = os.environ.get("CXX") or shutil.which("g++") or "g++"
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    srcs = sorted(glob.glob(os.path.join(HOST, "*.cpp")))
+    tmp = HOST_LIB + ".tmp"
+    cmd = [cxx, "-std=c++17", "-O2", "-fPIC", "-shared", "-Wall", "-Wextra",
+           "-D__HIP_PLATFORM_AMD__", "-I", os.path.join(os.path.dirname(HERE), "include"),
+           "-I", os.path.join(rocm, "include"), *srcs, "-o", tmp,
+           "-L", HERE, "-lhiggs_hip", "-L", os.path.join(rocm, "lib"), "-lamdhip64",
+           "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{os.path.join(rocm, 'lib')}"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"host library build failed:\n{r.stderr}")
+    os.replace(tmp, HOST_LIB)
+    if verbose:
+        print(f"built {HOST_LIB}")
+    return HOST_LIB
 
 
 if __name__ == "__main__":

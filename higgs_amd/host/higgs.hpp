@@ -1,0 +1,243 @@
+// higgs.hpp -- C++ host API over the C ABI of libhiggs_hip.so.
+//
+// The reference (panbanda/higgs, crates/higgs-models) calls these ops through
+// mlx-rs from its layer structs. This header keeps those calls' names,
+// argument meaning and error behaviour, so a layer forward written against
+// mlx-rs reads the same against it:
+//
+//   fast::rms_norm(x, weight, eps)               mlx_rs::fast::rms_norm
+//   nn::RmsNorm{weight, eps}.forward(x)          nn::RmsNorm (transformer.rs:387-392, 407-415)
+//   fast::rope(x, dims, traditional, base, scale, offset, freqs)
+//                                                mlx_rs::fast::rope
+//   apply_rope(x, rope, offset)                  utils.rs:16-26
+//   apply_rope_batched(x, rope, offsets)         the per-request rope loop of
+//                                                Model::forward_batched (transformer.rs:747-802)
+//   qk_norm_rope(q, k, q_norm, k_norm, rope, offset)
+//                                                q_norm/k_norm, transpose, apply_rope
+//                                                (transformer.rs:264-287)
+//   swiglu(gate, x)                              qwen3_next.rs:275-277
+//   nn::silu_mul(gate, up)                       nn::silu(gate) * up (transformer.rs:349-353)
+//   nn::gelu_approximate_mul(gate, up)           nn::gelu_approximate(gate) * up (gemma2.rs:422-427)
+//   gated_rms_norm(y, z, norm)                   swiglu(z, norm(y)) (qwen3_next.rs:1204-1205)
+//   nn::QuantizedEmbedding{...}.forward(ids)     nn::QuantizedEmbedding (transformer.rs:494)
+//                                                and QEmbedding::forward (qwen3_next.rs:248-257)
+//
+// Errors are thrown as higgs::Exception, whose message follows the
+// reference's `Exception::custom` convention (qwen3_next.rs:337-361): the
+// op name, the library's message, then the operands' shapes and dtypes.
+//
+// Every op enqueues on the calling thread's current stream
+// (Stream::task_local_or_default, after qwen3_next.rs:307) and never
+// synchronises; only the host readback helpers (to_f32, to_bits, item) wait.
+// Results are allocated stream-ordered (hipMallocAsync) and released with
+// hipFreeAsync on the stream they were allocated on.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <memory>
+#include <optional>
+#include <stdexcept>
+#include <string>
+#include <utility>
+#include <vector>
+
+#include "higgs_hip.h"
+
+namespace higgs {
+
+// mlx_rs::Dtype names for the types this path uses.
+enum class Dtype : int {
+  Float32 = HGK_F32,
+  Bfloat16 = HGK_BF16,
+  Float16 = HGK_F16,
+  Uint32 = HGK_U32,
+  Int32 = HGK_I32,
+};
+std::size_t size_of(Dtype dt);
+const char* name_of(Dtype dt);      // "Float32", "Bfloat16", ... (Rust Debug form)
+bool is_floating(Dtype dt);
+Dtype promote(Dtype a, Dtype b);    // MLX float promotion (equal -> same, else Float32)
+
+using Shape = std::vector<int64_t>;
+std::string format_shape(const Shape& s);  // "[512, 2048]"
+
+class Exception : public std::runtime_error {
+ public:
+  Exception(int status, const std::string& msg) : std::runtime_error(msg), status_(status) {}
+  // Exception::custom(msg) of mlx-rs: an argument error with a message.
+  static Exception custom(const std::string& msg) { return Exception(HGK_ERR_ARG, msg); }
+  int status() const { return status_; }
+
+ private:
+  int status_;
+};
+
+// A HIP stream handle. Default-constructed = the null stream. `create()`
+// makes an owning stream at the default priority.
+class Stream {
+ public:
+  Stream() = default;
+  explicit Stream(hipStream_t s) : s_(s) {}
+  static Stream create();
+  // The calling thread's current stream (set with StreamScope), else the
+  // null stream.
+  static Stream task_local_or_default();
+  hipStream_t get() const { return s_; }
+  void synchronize() const;
+
+ private:
+  hipStream_t s_ = nullptr;
+  std::shared_ptr<void> owner_;
+};
+
+// Makes `s` the calling thread's current stream for the scope's lifetime.
+class StreamScope {
+ public:
+  explicit StreamScope(const Stream& s);
+  ~StreamScope();
+  StreamScope(const StreamScope&) = delete;
+  StreamScope& operator=(const StreamScope&) = delete;
+
+ private:
+  Stream prev_;
+};
+
+namespace detail {
+struct Buffer;
+}
+
+// A device array: shape, element strides and dtype over a shared device
+// buffer. Views (transpose, slice, reshape of contiguous data) share the
+// buffer; ops write fresh row-major results.
+class Array {
+ public:
+  Array() = default;
+
+  static Array empty(const Shape& shape, Dtype dt);
+  // Host values rounded (to nearest even) to `dt` and uploaded.
+  static Array from_slice(const float* data, std::size_t n, const Shape& shape,
+                          Dtype dt = Dtype::Float32);
+  static Array from_slice(const std::vector<float>& v, const Shape& shape,
+                          Dtype dt = Dtype::Float32) {
+    return from_slice(v.data(), v.size(), shape, dt);
+  }
+  static Array from_slice(const int32_t* data, std::size_t n, const Shape& shape);
+  static Array from_slice(const std::vector<int32_t>& v, const Shape& shape) {
+    return from_slice(v.data(), v.size(), shape);
+  }
+  static Array from_slice(const uint32_t* data, std::size_t n, const Shape& shape);
+  static Array from_slice(const std::vector<uint32_t>& v, const Shape& shape) {
+    return from_slice(v.data(), v.size(), shape);
+  }
+  // Raw 16-bit codes (bf16 or f16 bit patterns) uploaded unchanged.
+  static Array from_bits(const uint16_t* bits, std::size_t n, const Shape& shape, Dtype dt);
+
+  const Shape& shape() const { return shape_; }
+  int64_t dim(int axis) const;  // negative axes count from the end
+  const Shape& strides() const { return strides_; }
+  int ndim() const { return static_cast<int>(shape_.size()); }
+  int64_t size() const;
+  Dtype dtype() const { return dtype_; }
+  std::size_t itemsize() const { return size_of(dtype_); }
+  bool is_contiguous() const;
+  // Device address of element [0, ..., 0].
+  void* data() const;
+
+  // Views.
+  Array transpose(const std::vector<int>& axes) const;
+  Array slice(int axis, int64_t start, int64_t stop) const;
+  Array reshape(const Shape& shape) const;  // contiguous arrays only
+
+  // Host readback (waits for the current stream). Elements come back in
+  // row-major order of the logical shape, whatever the strides.
+  std::vector<float> to_f32() const;
+  std::vector<uint16_t> to_bits() const;  // 16-bit dtypes only
+  std::vector<uint32_t> to_u32() const;   // 32-bit dtypes, raw words
+  float item() const;                      // size-1 arrays
+
+  // "[512, 2048]/Bfloat16", the operand form used in error messages.
+  std::string describe() const;
+
+ private:
+  std::shared_ptr<detail::Buffer> buf_;
+  int64_t offset_ = 0;  // elements
+  Shape shape_, strides_;
+  Dtype dtype_ = Dtype::Float32;
+  void gather_host(void* out) const;
+};
+
+// Inverse frequencies and llama3 frequency tables, as fast::rope derives them.
+std::vector<float> rope_inv_freq(float base, int dims, const std::vector<float>* freqs = nullptr);
+std::vector<float> llama3_rope_freqs(float base, int dims, float factor, float low_freq_factor,
+                                     float high_freq_factor, float original_max_position);
+
+namespace fast {
+// y = weight * round(x * rsqrt(mean(x^2) + eps)) over the last axis. The
+// result dtype is the promotion of x's and weight's.
+Array rms_norm(const Array& x, const Array& weight, float eps);
+// x is [..., L, D] with positions along axis -2 (leading axes flattened).
+// Exactly one of `base` and `freqs` is given.
+Array rope(const Array& x, int dims, bool traditional, std::optional<float> base, float scale,
+           int offset, const std::vector<float>* freqs = nullptr);
+// As rope for x [B, H, L, D], with offsets (int32 [B], device) giving each
+// sequence its own start position.
+Array rope_batched(const Array& x, int dims, bool traditional, std::optional<float> base,
+                   float scale, const Array& offsets, const std::vector<float>* freqs = nullptr);
+}  // namespace fast
+
+namespace nn {
+// nn::RmsNorm. `plus_one` applies Gemma's (1 + weight) in f32, which the
+// reference bakes into the weights at load time (gemma2.rs:799-826); the
+// result is then Float32, as it is there.
+struct RmsNorm {
+  Array weight;
+  float eps = 1e-5f;
+  bool plus_one = false;
+  Array forward(const Array& x) const;
+};
+
+// nn::Rope's fields (dimensions, traditional, base, scale) plus an optional
+// explicit frequency table (the freqs argument of fast::rope,
+// deepseek_v2.rs:222-225; llama3 scaling uses it).
+struct Rope {
+  int dimensions = 0;
+  bool traditional = false;
+  std::optional<float> base = 10000.0f;
+  float scale = 1.0f;
+  std::vector<float> freqs;  // empty: derive from base
+  Array forward(const Array& x, int offset) const;
+};
+
+// nn::QuantizedEmbedding over the MLX affine format: weight Uint32
+// [V, H*bits/32], scales and biases [V, H/group_size] (Bfloat16 or Float16).
+struct QuantizedEmbedding {
+  Array weight, scales, biases;
+  int group_size = 64;
+  int bits = 4;
+  int64_t hidden() const;
+  Array forward(const Array& ids) const;
+  // forward followed by h * round(scale) (Gemma's sqrt(H) embedding scale,
+  // gemma2.rs:587-600) in the same pass.
+  Array forward_scaled(const Array& ids, float scale) const;
+};
+
+Array silu_mul(const Array& gate, const Array& up);
+Array gelu_approximate_mul(const Array& gate, const Array& up);
+}  // namespace nn
+
+Array apply_rope(const Array& x, const nn::Rope& rope, int offset);
+Array apply_rope_batched(const Array& x, const nn::Rope& rope, const Array& offsets);
+Array swiglu(const Array& gate, const Array& x);
+// swiglu(z, norm.forward(y)); z may be a strided view (read in place).
+Array gated_rms_norm(const Array& y, const Array& z, const nn::RmsNorm& norm);
+// Per-head RMSNorm over head_dim, then RoPE, for q [B, L, Hq, D] and
+// k [B, L, Hk, D] in the projection layout (any strides, unit D stride).
+// Returns (q, k) as [B, H, L, D]. `offsets` (int32 [B]) overrides `offset`.
+std::pair<Array, Array> qk_norm_rope(const Array& q, const Array& k, const nn::RmsNorm* q_norm,
+                                     const nn::RmsNorm* k_norm, const nn::Rope& rope,
+                                     int offset, const Array* offsets = nullptr);
+
+}  // namespace higgs

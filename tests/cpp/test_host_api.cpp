@@ -1,0 +1,553 @@
+// Parity tests of the C++ host API (higgs_amd/host/higgs.hpp) on the GPU,
+// written in the shape of the reference's own Rust tests: build inputs with
+// Array::from_slice, call the layer-level function, read results back and
+// assert. Expected values come from the oracle (oracle/liboracle.so, the CPU
+// restatement of MLX's CPU-device ops) on the same seeded inputs, or from the
+// reference tests' own constants (qwen3_next.rs:1689-1697, 1927-1961).
+//
+//   test_host_api            run every test, print one line each, exit 1 on failure
+//   test_host_api --list     print the test names (needs no GPU)
+//   test_host_api NAME...    run the named tests only
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <functional>
+#include <string>
+#include <vector>
+
+#include "higgs.hpp"
+
+extern "C" {
+#include "oracle.h"
+}
+
+using higgs::Array;
+using higgs::Dtype;
+using higgs::Shape;
+
+namespace {
+
+struct Case {
+  const char* name;
+  std::function<void()> fn;
+};
+std::vector<Case>& registry() {
+  static std::vector<Case> r;
+  return r;
+}
+struct Register {
+  Register(const char* n, std::function<void()> f) { registry().push_back({n, std::move(f)}); }
+};
+
+#define TEST(name)                                 \
+  static void name();                              \
+  static Register reg_##name(#name, name);         \
+  static void name()
+
+struct Failure {
+  std::string msg;
+};
+
+#define ASSERT(cond, ...)                                                            \
+  do {                                                                               \
+    if (!(cond)) {                                                                   \
+      char buf_[512];                                                                \
+      std::snprintf(buf_, sizeof buf_, __VA_ARGS__);                                 \
+      throw Failure{std::string(__FILE__ ":") + std::to_string(__LINE__) + ": " +   \
+                    #cond + ": " + buf_};                                            \
+    }                                                                                \
+  } while (0)
+
+// ---- seeded inputs (the oracle's generators) ----
+std::vector<float> normal(uint64_t key, int64_t n, float mean = 0.0f, float sd = 1.0f) {
+  std::vector<float> v(n);
+  or_fill_normal(key, mean, sd, v.data(), n);
+  return v;
+}
+std::vector<float> uniform(uint64_t key, int64_t n, float lo, float hi) {
+  std::vector<float> v(n);
+  or_fill_uniform(key, lo, hi, v.data(), n);
+  return v;
+}
+// f32 values as the 16-bit codes of dtype dt (round to nearest even)
+std::vector<uint16_t> bits_of(const std::vector<float>& v, int dt) {
+  std::vector<uint16_t> b(v.size());
+  or_convert_from_f32(dt, v.data(), b.data(), static_cast<int64_t>(v.size()));
+  return b;
+}
+Array dev16(const std::vector<uint16_t>& b, const Shape& s, Dtype dt) {
+  return Array::from_bits(b.data(), b.size(), s, dt);
+}
+int64_t count_mismatch(const std::vector<uint16_t>& a, const std::vector<uint16_t>& b,
+                       int64_t* first) {
+  int64_t bad = 0;
+  *first = -1;
+  for (std::size_t i = 0; i < a.size(); ++i)
+    if (a[i] != b[i]) {
+      if (*first < 0) *first = static_cast<int64_t>(i);
+      ++bad;
+    }
+  return bad;
+}
+
+#define ASSERT_BITS_EQ(got, want)                                                          \
+  do {                                                                                     \
+    ASSERT((got).size() == (want).size(), "size %zu vs %zu", (got).size(), (want).size()); \
+    int64_t f_;                                                                            \
+    const int64_t bad_ = count_mismatch((got), (want), &f_);                               \
+    ASSERT(bad_ == 0, "%lld of %zu differ; first at %lld: 0x%04x vs 0x%04x",               \
+           (long long)bad_, (got).size(), (long long)f_, f_ >= 0 ? (got)[f_] : 0,          \
+           f_ >= 0 ? (want)[f_] : 0);                                                      \
+  } while (0)
+
+// ulp distance between two bf16/f16 codes of the same sign class
+int ulp16(uint16_t a, uint16_t b) {
+  auto key = [](uint16_t v) { return (v & 0x8000) ? -static_cast<int>(v & 0x7fff) : static_cast<int>(v); };
+  return std::abs(key(a) - key(b));
+}
+
+// ---------------------------------------------------------------- reference tests
+// qwen3_next.rs:1689-1697
+TEST(test_swiglu) {
+  const float g[] = {1.0f, -1.0f, 0.5f};
+  const float x[] = {2.0f, 3.0f, 4.0f};
+  Array gate = Array::from_slice(g, 3, {1, 3});
+  Array xx = Array::from_slice(x, 3, {1, 3});
+  Array result = higgs::swiglu(gate, xx);
+  ASSERT(result.shape() == Shape({1, 3}), "shape %s", higgs::format_shape(result.shape()).c_str());
+  // silu(1.0) * 2.0 = 0.7311 * 2.0 ~= 1.462
+  const float first = result.slice(1, 0, 1).item();
+  ASSERT(first > 1.0f, "first = %g", first);
+}
+
+// qwen3_next.rs:1927-1961
+TEST(test_swiglu_numeric_correctness) {
+  auto one = [](float g, float x) {
+    return higgs::swiglu(Array::from_slice(&g, 1, {1, 1}), Array::from_slice(&x, 1, {1, 1})).item();
+  };
+  const float v1 = one(0.0f, 5.0f);
+  ASSERT(std::fabs(v1 - 0.0f) < 1e-6f, "silu(0)*5 should be 0, got %g", v1);
+  const float v2 = one(1.0f, 1.0f);
+  ASSERT(std::fabs(v2 - 0.7310586f) < 1e-4f, "silu(1)*1 should be ~0.7311, got %g", v2);
+  const float v3 = one(-1.0f, 2.0f);
+  ASSERT(std::fabs(v3 - (-0.5378828f)) < 1e-4f, "silu(-1)*2 should be ~-0.5379, got %g", v3);
+}
+
+// ---------------------------------------------------------------- host plumbing
+TEST(test_from_slice_rounds_like_the_oracle) {
+  std::vector<float> v = normal(11, 4096, 0.0f, 100.0f);
+  const float specials[] = {0.0f, -0.0f, 1.0f, 65504.0f, 65519.99f, 65520.0f, 1e-8f, -6.1e-5f,
+                            5.96e-8f, 2.98e-8f, 1.00390625f, 1.01171875f, INFINITY, -INFINITY,
+                            3.0e38f, 1e-40f};
+  v.insert(v.end(), std::begin(specials), std::end(specials));
+  for (int dt : {OR_BF16, OR_F16}) {
+    const Dtype d = dt == OR_BF16 ? Dtype::Bfloat16 : Dtype::Float16;
+    Array a = Array::from_slice(v, {static_cast<int64_t>(v.size())}, d);
+    auto got = a.to_bits();
+    auto want = bits_of(v, dt);
+    ASSERT_BITS_EQ(got, want);
+    std::vector<float> back(v.size());
+    or_convert_to_f32(dt, want.data(), back.data(), static_cast<int64_t>(v.size()));
+    auto f = a.to_f32();
+    for (std::size_t i = 0; i < v.size(); ++i)
+      ASSERT(std::memcmp(&f[i], &back[i], 4) == 0, "to_f32 mismatch at %zu", i);
+  }
+}
+
+TEST(test_views_read_back_in_logical_order) {
+  std::vector<float> v(2 * 3 * 4);
+  for (std::size_t i = 0; i < v.size(); ++i) v[i] = static_cast<float>(i);
+  Array a = Array::from_slice(v, {2, 3, 4});
+  auto t = a.transpose({2, 0, 1}).to_f32();  // [4, 2, 3]
+  for (int k = 0; k < 4; ++k)
+    for (int i = 0; i < 2; ++i)
+      for (int j = 0; j < 3; ++j)
+        ASSERT(t[(k * 2 + i) * 3 + j] == v[(i * 3 + j) * 4 + k], "transpose at %d,%d,%d", k, i, j);
+  auto s = a.slice(2, 1, 3).reshape({2, 3, 2, 1}).to_f32();
+  ASSERT(s.size() == 12 && s[0] == 1.0f && s[1] == 2.0f && s[2] == 5.0f, "slice/reshape view");
+  bool threw = false;
+  try {
+    a.transpose({1, 0, 2}).reshape({24});
+  } catch (const higgs::Exception&) {
+    threw = true;
+  }
+  ASSERT(threw, "a reshape that needs a copy must throw");
+}
+
+// ---------------------------------------------------------------- RMSNorm
+// nn::RmsNorm on the RMSNorm-alone workload: bf16 [512, 2048], eps 1e-5.
+TEST(test_rms_norm_matches_oracle_bf16) {
+  const int64_t R = 512, N = 2048;
+  auto xb = bits_of(normal(1000, R * N), OR_BF16);
+  auto wb = bits_of(normal(1001, N, 1.0f, 0.02f), OR_BF16);
+  higgs::nn::RmsNorm norm{dev16(wb, {N}, Dtype::Bfloat16), 1e-5f};
+  Array y = norm.forward(dev16(xb, {R, N}, Dtype::Bfloat16));
+  ASSERT(y.dtype() == Dtype::Bfloat16, "dtype %s", higgs::name_of(y.dtype()));
+  std::vector<uint16_t> want(R * N);
+  ASSERT(or_rms_norm(xb.data(), OR_BF16, N, wb.data(), OR_BF16, 0, 1e-5f, want.data(), OR_BF16, N,
+                     R, N) == 0, "oracle");
+  auto got = y.to_bits();
+  ASSERT_BITS_EQ(got, want);
+  // fast::rms_norm is the same call
+  auto got2 = higgs::fast::rms_norm(dev16(xb, {R, N}, Dtype::Bfloat16), norm.weight, 1e-5f).to_bits();
+  ASSERT_BITS_EQ(got2, want);
+}
+
+// Gemma's (1 + w) norm: weights shifted in f32 at load time (gemma2.rs:799-826),
+// so the result is Float32.
+TEST(test_rms_norm_gemma_plus_one_is_float32) {
+  const int64_t R = 64, N = 3584;
+  auto xb = bits_of(normal(2000, R * N), OR_BF16);
+  auto wb = bits_of(normal(2001, N, 0.0f, 0.02f), OR_BF16);
+  higgs::nn::RmsNorm norm{dev16(wb, {N}, Dtype::Bfloat16), 1e-6f, true};
+  Array y = norm.forward(dev16(xb, {4, 16, N}, Dtype::Bfloat16));
+  ASSERT(y.dtype() == Dtype::Float32 && y.shape() == Shape({4, 16, N}), "%s", y.describe().c_str());
+  std::vector<float> want(R * N);
+  ASSERT(or_rms_norm(xb.data(), OR_BF16, N, wb.data(), OR_BF16, 1, 1e-6f, want.data(), OR_F32, N, R,
+                     N) == 0, "oracle");
+  auto got = y.to_f32();
+  for (int64_t i = 0; i < R * N; ++i)
+    ASSERT(std::memcmp(&got[i], &want[i], 4) == 0, "at %lld: %.9g vs %.9g", (long long)i, got[i], want[i]);
+}
+
+// Rows read through a row stride (a column slice of a wider buffer).
+TEST(test_rms_norm_strided_rows_f16) {
+  const int64_t R = 96, W = 1536, N = 1024;
+  auto xb = bits_of(normal(3000, R * W), OR_F16);
+  auto wb = bits_of(normal(3001, N, 1.0f, 0.02f), OR_F16);
+  Array x = dev16(xb, {R, W}, Dtype::Float16).slice(1, 256, 256 + N);
+  Array y = higgs::fast::rms_norm(x, dev16(wb, {N}, Dtype::Float16), 1e-6f);
+  std::vector<uint16_t> want(R * N);
+  ASSERT(or_rms_norm(xb.data() + 256, OR_F16, W, wb.data(), OR_F16, 0, 1e-6f, want.data(), OR_F16, N,
+                     R, N) == 0, "oracle");
+  auto got = y.to_bits();
+  ASSERT_BITS_EQ(got, want);
+}
+
+// ---------------------------------------------------------------- RoPE
+// Oracle RoPE of x [B, H, L, D] (contiguous) into the same layout.
+std::vector<uint16_t> oracle_rope(const std::vector<uint16_t>& xb, int64_t B, int64_t H, int64_t L,
+                                  int64_t D, int dims, const std::vector<float>& inv, int offset,
+                                  const int32_t* offsets, const uint16_t* norm_w = nullptr) {
+  std::vector<uint16_t> y(xb.size());
+  const int64_t s[3] = {H * L * D, D, L * D};
+  const int rc = or_norm_rope(OR_BF16, xb.data(), s, y.data(), s, B, L, H, D, norm_w, OR_BF16, 1e-6f,
+                              dims, inv.data(), 1.0f, offset, offsets);
+  if (rc) throw Failure{"oracle rope failed"};
+  return y;
+}
+
+// apply_rope (utils.rs:16-26) on the post-transpose [B, H, L, D] layout.
+TEST(test_apply_rope_default_bf16) {
+  const int64_t B = 2, H = 4, L = 16, D = 64;
+  auto xb = bits_of(normal(4000, B * H * L * D), OR_BF16);
+  higgs::nn::Rope rope;
+  rope.dimensions = 64;
+  rope.base = 10000.0f;
+  Array y = higgs::apply_rope(dev16(xb, {B, H, L, D}, Dtype::Bfloat16), rope, 5);
+  std::vector<float> inv(32);
+  or_rope_inv_freq(10000.0f, 64, nullptr, inv.data());
+  auto want = oracle_rope(xb, B, H, L, D, 64, inv, 5, nullptr);
+  auto got = y.to_bits();
+  ASSERT_BITS_EQ(got, want);
+  // nn::Rope::forward and fast::rope are the same computation
+  auto got2 = rope.forward(dev16(xb, {B, H, L, D}, Dtype::Bfloat16), 5).to_bits();
+  ASSERT_BITS_EQ(got2, want);
+}
+
+// llama3-scaled frequencies passed as fast::rope's freqs (deepseek_v2.rs:222-225).
+TEST(test_apply_rope_llama3_freqs) {
+  const int64_t B = 1, H = 8, L = 64, D = 64;
+  auto freqs = higgs::llama3_rope_freqs(500000.0f, 64, 32.0f, 1.0f, 4.0f, 8192.0f);
+  std::vector<float> want_f(32);
+  or_llama3_freqs(500000.0f, 64, 32.0f, 1.0f, 4.0f, 8192.0f, want_f.data());
+  for (int i = 0; i < 32; ++i)
+    ASSERT(std::memcmp(&freqs[i], &want_f[i], 4) == 0, "freq %d: %.9g vs %.9g", i, freqs[i], want_f[i]);
+  auto xb = bits_of(normal(4100, B * H * L * D), OR_BF16);
+  higgs::nn::Rope rope;
+  rope.dimensions = 64;
+  rope.freqs = freqs;
+  Array y = higgs::apply_rope(dev16(xb, {B, H, L, D}, Dtype::Bfloat16), rope, 1000);
+  std::vector<float> inv(32);
+  or_rope_inv_freq(0.0f, 64, want_f.data(), inv.data());
+  auto want = oracle_rope(xb, B, H, L, D, 64, inv, 1000, nullptr);
+  auto got = y.to_bits();
+  ASSERT_BITS_EQ(got, want);
+}
+
+// Partial rotary (qwen3_next.rs:680-703): dims [64, 256) pass through bit-exactly.
+TEST(test_apply_rope_partial_passes_tail_through) {
+  const int64_t B = 3, H = 16, L = 1, D = 256;
+  auto xb = bits_of(normal(4200, B * H * L * D), OR_BF16);
+  higgs::nn::Rope rope;
+  rope.dimensions = 64;
+  rope.base = 1e7f;
+  auto got = higgs::apply_rope(dev16(xb, {B, H, L, D}, Dtype::Bfloat16), rope, 12345).to_bits();
+  for (int64_t r = 0; r < B * H * L; ++r)
+    for (int64_t d = 64; d < D; ++d)
+      ASSERT(got[r * D + d] == xb[r * D + d], "tail changed at row %lld dim %lld", (long long)r, (long long)d);
+  std::vector<float> inv(32);
+  or_rope_inv_freq(1e7f, 64, nullptr, inv.data());
+  auto want = oracle_rope(xb, B, H, L, D, 64, inv, 12345, nullptr);
+  ASSERT_BITS_EQ(got, want);
+}
+
+// Per-sequence offsets replace forward_batched's per-request rope loop
+// (transformer.rs:747-802): one batched call equals the loop, bit for bit.
+TEST(test_apply_rope_batched_equals_per_request_loop) {
+  const int64_t B = 5, H = 2, L = 1, D = 256;
+  auto xb = bits_of(normal(4300, B * H * L * D), OR_BF16);
+  const std::vector<int32_t> offs = {1, 100, 32768, 7, 4095};
+  higgs::nn::Rope rope;
+  rope.dimensions = 64;
+  rope.base = 1e7f;
+  Array x = dev16(xb, {B, H, L, D}, Dtype::Bfloat16);
+  auto batched = higgs::apply_rope_batched(x, rope, Array::from_slice(offs, {B})).to_bits();
+  for (int64_t b = 0; b < B; ++b) {
+    auto one = higgs::apply_rope(x.slice(0, b, b + 1), rope, offs[b]).to_bits();
+    for (int64_t i = 0; i < H * L * D; ++i)
+      ASSERT(batched[b * H * L * D + i] == one[i], "sequence %lld element %lld", (long long)b, (long long)i);
+  }
+  std::vector<float> inv(32);
+  or_rope_inv_freq(1e7f, 64, nullptr, inv.data());
+  auto want = oracle_rope(xb, B, H, L, D, 64, inv, 0, offs.data());
+  ASSERT_BITS_EQ(batched, want);
+}
+
+// q_norm / k_norm, transpose and apply_rope (transformer.rs:264-287) in one
+// call: q and k in the projection layout [B, L, H, D], results [B, H, L, D].
+TEST(test_qk_norm_rope_matches_oracle) {
+  const int64_t B = 2, L = 8, Hq = 8, Hk = 2, D = 128;
+  auto qb = bits_of(normal(5000, B * L * Hq * D), OR_BF16);
+  auto kb = bits_of(normal(5001, B * L * Hk * D), OR_BF16);
+  auto qwb = bits_of(normal(5002, D, 1.0f, 0.02f), OR_BF16);
+  auto kwb = bits_of(normal(5003, D, 1.0f, 0.02f), OR_BF16);
+  higgs::nn::RmsNorm qn{dev16(qwb, {D}, Dtype::Bfloat16), 1e-6f};
+  higgs::nn::RmsNorm kn{dev16(kwb, {D}, Dtype::Bfloat16), 1e-6f};
+  higgs::nn::Rope rope;
+  rope.dimensions = 128;
+  rope.base = 1e6f;
+  auto qk = higgs::qk_norm_rope(dev16(qb, {B, L, Hq, D}, Dtype::Bfloat16),
+                                dev16(kb, {B, L, Hk, D}, Dtype::Bfloat16), &qn, &kn, rope, 3);
+  ASSERT(qk.first.shape() == Shape({B, Hq, L, D}), "q out %s", qk.first.describe().c_str());
+  std::vector<float> inv(64);
+  or_rope_inv_freq(1e6f, 128, nullptr, inv.data());
+  for (int t = 0; t < 2; ++t) {
+    const int64_t H = t ? Hk : Hq;
+    const auto& in = t ? kb : qb;
+    std::vector<uint16_t> want(in.size());
+    const int64_t xs[3] = {L * H * D, H * D, D};
+    const int64_t ys[3] = {H * L * D, D, L * D};
+    ASSERT(or_norm_rope(OR_BF16, in.data(), xs, want.data(), ys, B, L, H, D, t ? kwb.data() : qwb.data(),
+                        OR_BF16, 1e-6f, 128, inv.data(), 1.0f, 3, nullptr) == 0, "oracle");
+    auto got = (t ? qk.second : qk.first).to_bits();
+    ASSERT_BITS_EQ(got, want);
+  }
+}
+
+// ---------------------------------------------------------------- gated norm
+// GatedDeltaNet's norm: swiglu(z, norm(y)) with z read in place from the
+// in_proj_qkvz output (qwen3_next.rs:1204-1205, 1214-1265).
+TEST(test_gated_rms_norm_reads_z_in_place) {
+  const int64_t S = 8, NK = 16, VPK = 2, DV = 128, BLK = 768;
+  auto yb = bits_of(normal(6000, S * NK * VPK * DV), OR_BF16);
+  auto qkvz = bits_of(normal(6001, S * NK * BLK), OR_BF16);
+  auto wb = bits_of(normal(6002, DV, 1.0f, 0.02f), OR_BF16);
+  Array z = dev16(qkvz, {S, NK, BLK}, Dtype::Bfloat16).slice(2, 512, 768).reshape({S, NK, VPK, DV});
+  higgs::nn::RmsNorm norm{dev16(wb, {DV}, Dtype::Bfloat16), 1e-6f};
+  Array out = higgs::gated_rms_norm(dev16(yb, {S, NK * VPK, DV}, Dtype::Bfloat16), z, norm);
+  // the oracle takes z as plain rows
+  std::vector<uint16_t> zc;
+  for (int64_t s = 0; s < S; ++s)
+    for (int64_t k = 0; k < NK; ++k)
+      zc.insert(zc.end(), qkvz.begin() + (s * NK + k) * BLK + 512, qkvz.begin() + (s * NK + k + 1) * BLK);
+  const int64_t R = S * NK * VPK;
+  std::vector<uint16_t> want(R * DV);
+  ASSERT(or_gated_rms_norm(OR_BF16, yb.data(), DV, zc.data(), DV, wb.data(), OR_BF16, 1e-6f, want.data(),
+                           OR_BF16, DV, R, DV) == 0, "oracle");
+  auto got = out.to_bits();
+  ASSERT_BITS_EQ(got, want);
+}
+
+// ---------------------------------------------------------------- GLU
+TEST(test_silu_mul_and_gelu_approximate_mul) {
+  const int64_t R = 64, N = 1536;
+  auto gb = bits_of(normal(7000, R * N, 0.0f, 3.0f), OR_BF16);
+  auto ub = bits_of(normal(7001, R * N), OR_BF16);
+  Array g = dev16(gb, {R, N}, Dtype::Bfloat16), u = dev16(ub, {R, N}, Dtype::Bfloat16);
+  std::vector<uint16_t> want(R * N);
+  ASSERT(or_glu(OR_ACT_SILU, OR_BF16, gb.data(), N, ub.data(), N, want.data(), OR_BF16, N, R, N) == 0, "oracle");
+  auto silu = higgs::nn::silu_mul(g, u).to_bits();
+  ASSERT_BITS_EQ(silu, want);
+  ASSERT(or_glu(OR_ACT_GELU_TANH, OR_BF16, gb.data(), N, ub.data(), N, want.data(), OR_BF16, N, R, N) == 0,
+         "oracle");
+  // bf16 bar: within 1 ulp, or within atol 1e-3 next to zero where ulps
+  // shrink without bound (rtol 1e-2 / atol 1e-3)
+  auto gelu = higgs::nn::gelu_approximate_mul(g, u).to_bits();
+  std::vector<float> gf(want.size()), wf(want.size());
+  or_convert_to_f32(OR_BF16, gelu.data(), gf.data(), static_cast<int64_t>(gf.size()));
+  or_convert_to_f32(OR_BF16, want.data(), wf.data(), static_cast<int64_t>(wf.size()));
+  int64_t far = 0, exact = 0;
+  for (std::size_t i = 0; i < want.size(); ++i) {
+    const float d = std::fabs(gf[i] - wf[i]);
+    exact += gelu[i] == want[i];
+    if (ulp16(gelu[i], want[i]) > 1 && d > 1e-3f) ++far;
+    ASSERT(d <= 1e-3f + 1e-2f * std::fabs(wf[i]), "GeGLU at %zu: %g vs %g", i, gf[i], wf[i]);
+  }
+  ASSERT(far == 0, "%lld GeGLU values are beyond 1 bf16 ulp and atol 1e-3", (long long)far);
+  ASSERT(exact * 10 >= static_cast<int64_t>(want.size()) * 9, "only %lld of %zu GeGLU values exact",
+         (long long)exact, want.size());
+}
+
+// phi3's fused gate_up projection (phi3.rs:261-265): two halves read in place.
+TEST(test_swiglu_fused_gate_up_halves) {
+  const int64_t R = 32, I = 2048;
+  auto gu = bits_of(normal(7100, R * 2 * I), OR_BF16);
+  Array a = dev16(gu, {R, 2 * I}, Dtype::Bfloat16);
+  auto got = higgs::swiglu(a.slice(1, 0, I), a.slice(1, I, 2 * I)).to_bits();
+  std::vector<uint16_t> want(R * I);
+  ASSERT(or_glu(OR_ACT_SILU, OR_BF16, gu.data(), 2 * I, gu.data() + I, 2 * I, want.data(), OR_BF16, I, R,
+                I) == 0, "oracle");
+  ASSERT_BITS_EQ(got, want);
+}
+
+// ---------------------------------------------------------------- embedding
+// nn::QuantizedEmbedding at the Llama-3.2-1B table size (vocab 128256, hidden
+// 2048, group 64), bit-exact, with the first and last ids included.
+TEST(test_quantized_embedding_llama_table) {
+  const int64_t V = 128256, H = 2048, G = 64, T = 512;
+  std::vector<uint32_t> wq(V * H / 8);
+  or_fill_u32(8000, wq.data(), static_cast<int64_t>(wq.size()));
+  auto sb = bits_of(uniform(8001, V * H / G, 0.005f, 0.02f), OR_BF16);
+  auto bb = bits_of(uniform(8002, V * H / G, -0.1f, 0.1f), OR_BF16);
+  std::vector<uint32_t> ids(T);
+  or_fill_ids(8003, static_cast<uint32_t>(V), ids.data(), T);
+  ids[0] = 0;
+  ids[1] = static_cast<uint32_t>(V - 1);
+  higgs::nn::QuantizedEmbedding emb{Array::from_slice(wq, {V, H / 8}), dev16(sb, {V, H / G}, Dtype::Bfloat16),
+                                    dev16(bb, {V, H / G}, Dtype::Bfloat16), 64, 4};
+  Array idv = Array::from_slice(ids, {4, T / 4});
+  Array h = emb.forward(idv);
+  ASSERT(h.shape() == Shape({4, T / 4, H}) && h.dtype() == Dtype::Bfloat16, "%s", h.describe().c_str());
+  std::vector<uint16_t> want(T * H);
+  ASSERT(or_qembed(ids.data(), OR_U32, T, wq.data(), sb.data(), bb.data(), OR_BF16, V, H, 64, 4, 0.0f,
+                   want.data()) == 0, "oracle");
+  auto got = h.to_bits();
+  ASSERT_BITS_EQ(got, want);
+  // Gemma's embedding scale fused into the gather (gemma2.rs:587-600)
+  const float scale = std::sqrt(3584.0f);
+  auto got_s = emb.forward_scaled(idv, scale).to_bits();
+  ASSERT(or_qembed(ids.data(), OR_U32, T, wq.data(), sb.data(), bb.data(), OR_BF16, V, H, 64, 4, scale,
+                   want.data()) == 0, "oracle");
+  ASSERT_BITS_EQ(got_s, want);
+}
+
+// ---------------------------------------------------------------- empty inputs
+TEST(test_empty_inputs_give_empty_results) {
+  higgs::nn::RmsNorm norm{Array::from_slice(std::vector<float>(64, 1.0f), {64}, Dtype::Bfloat16), 1e-5f};
+  Array x = Array::empty({0, 64}, Dtype::Bfloat16);
+  ASSERT(norm.forward(x).shape() == Shape({0, 64}), "rms_norm");
+  ASSERT(higgs::swiglu(x, x).size() == 0, "swiglu");
+  higgs::nn::Rope rope;
+  rope.dimensions = 64;
+  ASSERT(higgs::apply_rope(Array::empty({2, 4, 0, 64}, Dtype::Bfloat16), rope, 0).size() == 0, "rope");
+}
+
+// ---------------------------------------------------------------- errors
+// Failures surface as an Exception naming the op, the library's reason and
+// the operands, after the reference's Exception::custom messages
+// (qwen3_next.rs:337-361).
+TEST(test_errors_name_the_op_and_operands) {
+  Array x = Array::from_slice(std::vector<float>(32, 1.0f), {4, 8}, Dtype::Bfloat16);
+  Array w = Array::from_slice(std::vector<float>(7, 1.0f), {7}, Dtype::Bfloat16);
+  try {
+    higgs::fast::rms_norm(x, w, 1e-5f);
+    ASSERT(false, "rms_norm with a mismatched weight returned");
+  } catch (const higgs::Exception& e) {
+    const std::string m = e.what();
+    ASSERT(e.status() == HGK_ERR_ARG, "status %d", e.status());
+    ASSERT(m.find("rms_norm failed:") == 0, "message: %s", m.c_str());
+    ASSERT(m.find("[x=[4, 8]/Bfloat16 w=[7]/Bfloat16]") != std::string::npos, "message: %s", m.c_str());
+  }
+  higgs::nn::Rope rope;
+  rope.dimensions = 8;
+  rope.traditional = true;
+  Array x4 = Array::from_slice(std::vector<float>(64, 1.0f), {1, 2, 4, 8}, Dtype::Bfloat16);
+  try {
+    higgs::apply_rope(x4, rope, 0);
+    ASSERT(false, "traditional rope returned");
+  } catch (const higgs::Exception& e) {
+    ASSERT(e.status() == HGK_ERR_UNSUPPORTED, "status %d: %s", e.status(), e.what());
+  }
+  try {
+    std::vector<float> f(4, 1.0f);
+    higgs::fast::rope(x4, 8, false, 10000.0f, 1.0f, 0, &f);
+    ASSERT(false, "rope with both base and freqs returned");
+  } catch (const higgs::Exception& e) {
+    ASSERT(e.status() == HGK_ERR_ARG, "status %d", e.status());
+  }
+  try {
+    Array ids = Array::from_slice(std::vector<float>(4, 0.0f), {4});
+    higgs::nn::QuantizedEmbedding emb{Array::empty({16, 8}, Dtype::Uint32), Array::empty({16, 1}, Dtype::Bfloat16),
+                                      Array::empty({16, 1}, Dtype::Bfloat16), 64, 4};
+    emb.forward(ids);
+    ASSERT(false, "Float32 ids returned");
+  } catch (const higgs::Exception& e) {
+    ASSERT(std::string(e.what()).find("ids must be Int32 or Uint32") != std::string::npos, "%s", e.what());
+  }
+}
+
+// ---------------------------------------------------------------- streams
+// Ops follow the thread's current stream; results do not depend on it.
+TEST(test_ops_run_on_the_scoped_stream) {
+  const int64_t R = 256, N = 2048;
+  auto xb = bits_of(normal(9000, R * N), OR_BF16);
+  auto wb = bits_of(normal(9001, N, 1.0f, 0.02f), OR_BF16);
+  auto base = higgs::fast::rms_norm(dev16(xb, {R, N}, Dtype::Bfloat16), dev16(wb, {N}, Dtype::Bfloat16), 1e-5f)
+                  .to_bits();
+  higgs::Stream s = higgs::Stream::create();
+  std::vector<uint16_t> other;
+  {
+    higgs::StreamScope scope(s);
+    ASSERT(higgs::Stream::task_local_or_default().get() == s.get(), "scope did not set the stream");
+    Array y = higgs::fast::rms_norm(dev16(xb, {R, N}, Dtype::Bfloat16), dev16(wb, {N}, Dtype::Bfloat16), 1e-5f);
+    other = y.to_bits();
+  }
+  ASSERT(higgs::Stream::task_local_or_default().get() == nullptr, "scope did not restore the stream");
+  ASSERT_BITS_EQ(other, base);
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+  if (argc > 1 && std::strcmp(argv[1], "--list") == 0) {
+    for (const auto& c : registry()) std::printf("%s\n", c.name);
+    return 0;
+  }
+  int run = 0, failed = 0;
+  for (const auto& c : registry()) {
+    if (argc > 1) {
+      bool want = false;
+      for (int i = 1; i < argc; ++i) want |= std::strcmp(argv[i], c.name) == 0;
+      if (!want) continue;
+    }
+    ++run;
+    std::printf("%s ... ", c.name);
+    std::fflush(stdout);
+    try {
+      c.fn();
+      std::printf("ok\n");
+    } catch (const Failure& f) {
+      ++failed;
+      std::printf("FAILED\n  %s\n", f.msg.c_str());
+    } catch (const std::exception& e) {
+      ++failed;
+      std::printf("FAILED\n  exception: %s\n", e.what());
+    }
+    std::fflush(stdout);
+  }
+  std::printf("%d run, %d failed\n", run, failed);
+  return failed || run == 0 ? 1 : 0;
+}
