@@ -38,6 +38,11 @@ PROTOTYPES = {
                                   _vp, _int, _i64, _i64, _i64, _vp]),
     "hgk_quantized_embedding": (_int, [_vp, _int, _i64, _vp, _vp, _vp, _int, _i64, _i64,
                                        _int, _int, _f32, _vp, _i64, _vp]),
+    "hgk_add_rms_norm": (_int, [_int, _vp, _i64, _vp, _i64, _vp, _int, _int, _f32, _vp, _i64,
+                                _vp, _int, _i64, _i64, _i64, _vp]),
+    "hgk_quantized_embedding_rms_norm": (_int, [_vp, _int, _i64, _vp, _vp, _vp, _int, _i64,
+                                                _i64, _int, _int, _f32, _vp, _i64, _vp, _int,
+                                                _int, _f32, _vp, _int, _i64, _vp]),
 }
 
 

@@ -1,5 +1,5 @@
-// norm.hip -- RMSNorm, Gemma (1+w) RMSNorm, per-head q/k RMSNorm and the
-// Qwen3-Next gated RMSNorm on gfx950.
+// norm.hip -- RMSNorm, Gemma (1+w) RMSNorm, per-head q/k RMSNorm, the
+// Qwen3-Next gated RMSNorm and the fused residual add + RMSNorm on gfx950.
 //
 // Layout: rows of n contiguous elements, arbitrary row stride. A group of LPR
 // lanes owns one row (LPR = 64 for hidden-size rows, fewer for head_dim rows,
@@ -12,16 +12,21 @@
 //   r = 1 / sqrt(f32(sum(x*x)) * f32(1/n) + eps)   (sum accumulated in f64)
 //   n = round_T(x * r);  y = round_T(n * w')        (T = promote(x, w'))
 // and, gated, out = round_T(round_T(z * round_T(sigmoid(z))) * y).
+// The residual form first forms h = round_X(x + r) (MLX's add), writes h and
+// normalises it: the block boundary `h = x.add(residual); norm(h)` of
+// transformer.rs:413-415 in one pass.
 #include "../../include/higgs_hip.h"
 #include "hgk_common.h"
 #include "hgk_host.h"
 
 namespace hgk {
 
+enum NormMode { kPlain = 0, kGated = 1, kResid = 2 };
+
 struct NormArgs {
   const void* x;
   int64_t xs;
-  const void* z;  // gated only: row r at (r / zg) * zgs + (r % zg) * zs
+  const void* z;  // gated: z; residual: r. Row r at (r / zg) * zgs + (r % zg) * zs
   int64_t zs;
   int64_t zg;
   int64_t zgs;
@@ -33,6 +38,8 @@ struct NormArgs {
   float inv_n;
   void* y;
   int64_t ys;
+  void* h;  // residual form: h = x + r (may be null)
+  int64_t hs;
   int64_t rows;
   int n;
 };
@@ -45,8 +52,9 @@ __device__ inline int64_t z_row_offset(const NormArgs& a, int64_t r) {
 // X activation, Y output, W weight storage type (X's type or f32). Every load
 // of the row (x, weights, z) is issued before the reduction; all stay packed
 // in registers until the element is consumed.
-template <class X, class Y, class W, int LPR, int CPL, bool GATED>
+template <class X, class Y, class W, int LPR, int CPL, int MODE>
 __global__ __launch_bounds__(256) void rms_norm_kernel(NormArgs a) {
+  constexpr bool GATED = MODE == kGated, RESID = MODE == kResid, TWO = GATED || RESID;
   constexpr int V = Vec<X>::N;
   constexpr int RPW = 64 / LPR;
   constexpr int WW = V * W::kBytes / 4;  // 32-bit words of weights per chunk
@@ -64,14 +72,14 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(NormArgs a) {
   // the next load can issue.
   u32x4 xr[CPL];
   uint32_t wr[CPL][WW];
-  u32x4 zr[GATED ? CPL : 1];
-  const int64_t zoff = GATED ? z_row_offset(a, r) : 0;
+  u32x4 zr[TWO ? CPL : 1];
+  const int64_t zoff = TWO ? z_row_offset(a, r) : 0;
 #pragma unroll
   for (int c = 0; c < CPL; ++c) {
     const int ch = j + c * LPR;
     const int chc = ch < nchunks ? ch : nchunks - 1;
     xr[c] = ld16<X>(a.x, r * a.xs + (int64_t)chc * V);
-    if constexpr (GATED) zr[c] = ld16<X>(a.z, zoff + (int64_t)chc * V);
+    if constexpr (TWO) zr[c] = ld16<X>(a.z, zoff + (int64_t)chc * V);
   }
   if (has_w) {
 #pragma unroll
@@ -84,6 +92,25 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(NormArgs a) {
 #pragma unroll
         for (int k = 0; k < 4; ++k) wr[c][4 * q + k] = t[k];
       }
+    }
+  }
+  if constexpr (RESID) {
+    // h = round_X(x + r), one packed conversion per pair; h replaces x
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        if constexpr (X::kBytes == 2) {
+          xr[c][k] = X::pack(X::lo(xr[c][k]) + X::lo(zr[c][k]), X::hi(xr[c][k]) + X::hi(zr[c][k]));
+        } else {
+          xr[c][k] = f2u(u2f(xr[c][k]) + u2f(zr[c][k]));
+        }
+      }
+      const int ch = j + c * LPR;
+      if (a.h && live && ch < nchunks)
+        __builtin_nontemporal_store(
+            xr[c], reinterpret_cast<u32x4*>(reinterpret_cast<char*>(a.h) +
+                                            (r * a.hs + (int64_t)ch * V) * X::kBytes));
     }
   }
   double ss = 0.0;
@@ -139,20 +166,31 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(NormArgs a) {
 }
 
 // Any n, any alignment: one wave per row, element-strided, two passes over x.
-template <class X, class Y, bool GATED>
+template <class X, class Y, int MODE>
 __global__ __launch_bounds__(256) void rms_norm_generic_kernel(NormArgs a) {
+  constexpr bool GATED = MODE == kGated, RESID = MODE == kResid;
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (row >= a.rows) return;  // whole wave leaves together
+  // the row's input value: x, or round_X(x + r) in the residual form
+  auto in = [&](int i) {
+    const float xv = load1<X>(a.x, row * a.xs + i);
+    if constexpr (RESID) return X::round(xv + load1<X>(a.z, z_row_offset(a, row) + i));
+    else return xv;
+  };
   double ss = 0.0;
   for (int i = lane; i < a.n; i += 64) {
-    const double xv = (double)load1<X>(a.x, row * a.xs + i);
+    const double xv = (double)in(i);
     ss = __builtin_fma(xv, xv, ss);
   }
   ss = group_sum<64>(ss);
   const float rr = rms_scale(ss, a.inv_n, a.eps);
   for (int i = lane; i < a.n; i += 64) {
-    float nv = load1<X>(a.x, row * a.xs + i) * rr;
+    const float hv = in(i);
+    if constexpr (RESID) {
+      if (a.h) store1<X>(a.h, row * a.hs + i, hv);
+    }
+    float nv = hv * rr;
     nv = a.round_x ? X::round(nv) : nv;
     float we = a.w ? load1_dt(a.w, a.wdt, i) : 1.0f;
     we = a.plus_one ? we + 1.0f : we;
@@ -171,46 +209,47 @@ __global__ __launch_bounds__(256) void rms_norm_generic_kernel(NormArgs a) {
 
 namespace {
 
-template <class X, class Y, class W, int LPR, int CPL, bool GATED>
+template <class X, class Y, class W, int LPR, int CPL, int MODE>
 void launch_fast(const NormArgs& a, hipStream_t s) {
   constexpr int RPW = 64 / LPR;
   const int64_t waves = (a.rows + RPW - 1) / RPW;
   const int wpb = waves >= 4096 ? 4 : 1;  // small problems: spread over CUs
   const int64_t blocks = (waves + wpb - 1) / wpb;
-  hipLaunchKernelGGL((rms_norm_kernel<X, Y, W, LPR, CPL, GATED>), dim3((unsigned)blocks),
+  hipLaunchKernelGGL((rms_norm_kernel<X, Y, W, LPR, CPL, MODE>), dim3((unsigned)blocks),
                      dim3(64 * wpb), 0, s, a);
 }
 
-template <class X, class Y, bool GATED>
+template <class X, class Y, int MODE>
 void launch_generic(const NormArgs& a, hipStream_t s) {
   const int wpb = a.rows >= 4096 ? 4 : 1;
   const int64_t blocks = (a.rows + wpb - 1) / wpb;
-  hipLaunchKernelGGL((rms_norm_generic_kernel<X, Y, GATED>), dim3((unsigned)blocks),
+  hipLaunchKernelGGL((rms_norm_generic_kernel<X, Y, MODE>), dim3((unsigned)blocks),
                      dim3(64 * wpb), 0, s, a);
 }
 
 // Pick (LPR, CPL) for a row of `nchunks` 16-byte chunks; false -> generic.
-template <class X, class Y, class W, bool GATED>
+// The gated form (head_dim rows) stops at 128 chunks.
+template <class X, class Y, class W, int MODE>
 bool launch_by_shape(const NormArgs& a, int nchunks, hipStream_t s) {
-  if (nchunks <= 4) { launch_fast<X, Y, W, 4, 1, GATED>(a, s); return true; }
-  if (nchunks <= 8) { launch_fast<X, Y, W, 8, 1, GATED>(a, s); return true; }
-  if (nchunks <= 16) { launch_fast<X, Y, W, 16, 1, GATED>(a, s); return true; }
-  if (nchunks <= 32) { launch_fast<X, Y, W, 32, 1, GATED>(a, s); return true; }
-  if (nchunks <= 64) { launch_fast<X, Y, W, 64, 1, GATED>(a, s); return true; }
-  if (nchunks <= 128) { launch_fast<X, Y, W, 64, 2, GATED>(a, s); return true; }
-  if constexpr (!GATED) {
+  if (nchunks <= 4) { launch_fast<X, Y, W, 4, 1, MODE>(a, s); return true; }
+  if (nchunks <= 8) { launch_fast<X, Y, W, 8, 1, MODE>(a, s); return true; }
+  if (nchunks <= 16) { launch_fast<X, Y, W, 16, 1, MODE>(a, s); return true; }
+  if (nchunks <= 32) { launch_fast<X, Y, W, 32, 1, MODE>(a, s); return true; }
+  if (nchunks <= 64) { launch_fast<X, Y, W, 64, 1, MODE>(a, s); return true; }
+  if (nchunks <= 128) { launch_fast<X, Y, W, 64, 2, MODE>(a, s); return true; }
+  if constexpr (MODE != kGated) {
     const int cpl = (nchunks + 63) / 64;
     switch (cpl) {
-      case 3: launch_fast<X, Y, W, 64, 3, false>(a, s); return true;
-      case 4: launch_fast<X, Y, W, 64, 4, false>(a, s); return true;
-      case 5: launch_fast<X, Y, W, 64, 5, false>(a, s); return true;
-      case 6: launch_fast<X, Y, W, 64, 6, false>(a, s); return true;
-      case 7: launch_fast<X, Y, W, 64, 7, false>(a, s); return true;
-      case 8: launch_fast<X, Y, W, 64, 8, false>(a, s); return true;
-      case 9: case 10: launch_fast<X, Y, W, 64, 10, false>(a, s); return true;
-      case 11: case 12: launch_fast<X, Y, W, 64, 12, false>(a, s); return true;
+      case 3: launch_fast<X, Y, W, 64, 3, MODE>(a, s); return true;
+      case 4: launch_fast<X, Y, W, 64, 4, MODE>(a, s); return true;
+      case 5: launch_fast<X, Y, W, 64, 5, MODE>(a, s); return true;
+      case 6: launch_fast<X, Y, W, 64, 6, MODE>(a, s); return true;
+      case 7: launch_fast<X, Y, W, 64, 7, MODE>(a, s); return true;
+      case 8: launch_fast<X, Y, W, 64, 8, MODE>(a, s); return true;
+      case 9: case 10: launch_fast<X, Y, W, 64, 10, MODE>(a, s); return true;
+      case 11: case 12: launch_fast<X, Y, W, 64, 12, MODE>(a, s); return true;
       case 13: case 14: case 15: case 16:
-        launch_fast<X, Y, W, 64, 16, false>(a, s); return true;
+        launch_fast<X, Y, W, 64, 16, MODE>(a, s); return true;
       default: break;
     }
   }
@@ -219,32 +258,35 @@ bool launch_by_shape(const NormArgs& a, int nchunks, hipStream_t s) {
 
 // The vectorised kernels take weights in the activation type or in f32;
 // any other weight dtype goes to the generic kernel.
-template <class X, class Y, bool GATED>
+template <class X, class Y, int MODE>
 void launch_xy(const NormArgs& a, bool vec_ok, hipStream_t s) {
   const int nchunks = a.n / Vec<X>::N;
   if (vec_ok) {
     if (!a.w || a.wdt == X::kCode) {
-      if (launch_by_shape<X, Y, X, GATED>(a, nchunks, s)) return;
+      if (launch_by_shape<X, Y, X, MODE>(a, nchunks, s)) return;
     } else if (a.wdt == DT_F32) {
-      if (launch_by_shape<X, Y, F32, GATED>(a, nchunks, s)) return;
+      if (launch_by_shape<X, Y, F32, MODE>(a, nchunks, s)) return;
     }
   }
-  launch_generic<X, Y, GATED>(a, s);
+  launch_generic<X, Y, MODE>(a, s);
 }
 
-template <bool GATED>
+constexpr const char* mode_fn(int mode) {
+  return mode == kGated ? "hgk_gated_rms_norm" : (mode == kResid ? "hgk_add_rms_norm" : "hgk_rms_norm");
+}
+
+template <int MODE>
 int dispatch(const NormArgs& a, int xdt, int ydt, bool vec_ok, hipStream_t s) {
-  if (xdt == DT_BF16 && ydt == DT_BF16) launch_xy<BF16, BF16, GATED>(a, vec_ok, s);
-  else if (xdt == DT_BF16 && ydt == DT_F32) launch_xy<BF16, F32, GATED>(a, vec_ok, s);
-  else if (xdt == DT_F16 && ydt == DT_F16) launch_xy<F16, F16, GATED>(a, vec_ok, s);
-  else if (xdt == DT_F16 && ydt == DT_F32) launch_xy<F16, F32, GATED>(a, vec_ok, s);
-  else if (xdt == DT_F32 && ydt == DT_F32) launch_xy<F32, F32, GATED>(a, vec_ok, s);
+  if (xdt == DT_BF16 && ydt == DT_BF16) launch_xy<BF16, BF16, MODE>(a, vec_ok, s);
+  else if (xdt == DT_BF16 && ydt == DT_F32) launch_xy<BF16, F32, MODE>(a, vec_ok, s);
+  else if (xdt == DT_F16 && ydt == DT_F16) launch_xy<F16, F16, MODE>(a, vec_ok, s);
+  else if (xdt == DT_F16 && ydt == DT_F32) launch_xy<F16, F32, MODE>(a, vec_ok, s);
+  else if (xdt == DT_F32 && ydt == DT_F32) launch_xy<F32, F32, MODE>(a, vec_ok, s);
   else
     return fail(HGK_ERR_UNSUPPORTED, "%s: output dtype %s for input %s is not implemented "
                 "(output must be the input dtype or f32)",
-                GATED ? "hgk_gated_rms_norm" : "hgk_rms_norm", dtype_name(ydt),
-                dtype_name(xdt));
-  return launch_status(GATED ? "hgk_gated_rms_norm" : "hgk_rms_norm");
+                mode_fn(MODE), dtype_name(ydt), dtype_name(xdt));
+  return launch_status(mode_fn(MODE));
 }
 
 int check_common(const char* fn, const void* x, int xdt, int64_t xs, const void* w, int wdt,
@@ -292,7 +334,7 @@ extern "C" int hgk_rms_norm(const void* x, int x_dtype, int64_t x_row_stride, co
   const bool vec_ok = aligned16(x) && aligned16(y) && (!w || aligned16(w)) && n % vx == 0 &&
                       x_row_stride % vx == 0 && (y_row_stride * dtype_bytes(y_dtype)) % 16 == 0 &&
                       (n * dtype_bytes(y_dtype)) % 16 == 0;
-  return dispatch<false>(a, x_dtype, y_dtype, vec_ok, as_stream(stream));
+  return dispatch<kPlain>(a, x_dtype, y_dtype, vec_ok, as_stream(stream));
 }
 
 extern "C" int hgk_gated_rms_norm(int dtype, const void* x, int64_t x_row_stride, const void* z,
@@ -327,5 +369,41 @@ extern "C" int hgk_gated_rms_norm(int dtype, const void* x, int64_t x_row_stride
                       z_group_stride % vx == 0 &&
                       (out_row_stride * dtype_bytes(out_dtype)) % 16 == 0 &&
                       (n * dtype_bytes(out_dtype)) % 16 == 0;
-  return dispatch<true>(a, dtype, out_dtype, vec_ok, as_stream(stream));
+  return dispatch<kGated>(a, dtype, out_dtype, vec_ok, as_stream(stream));
+}
+
+extern "C" int hgk_add_rms_norm(int dtype, const void* x, int64_t x_row_stride, const void* r,
+                                int64_t r_row_stride, const void* w, int w_dtype, int w_plus_one,
+                                float eps, void* h, int64_t h_row_stride, void* y, int y_dtype,
+                                int64_t y_row_stride, int64_t rows, int64_t n, void* stream) {
+  clear_error();
+  const char* fn = "hgk_add_rms_norm";
+  int st = check_common(fn, x, dtype, x_row_stride, w, w_dtype, y, y_dtype, y_row_stride, rows,
+                        n, eps);
+  if (st) return st;
+  if (!r) return fail(HGK_ERR_ARG, "%s: null residual r", fn);
+  if (w_plus_one && !w) return fail(HGK_ERR_ARG, "%s: w_plus_one needs a weight", fn);
+  if (rows > 1 && (r_row_stride < n || (h && h_row_stride < n)))
+    return fail(HGK_ERR_ARG, "%s: r/h row strides (%lld, %lld) smaller than n=%lld", fn,
+                (long long)r_row_stride, (long long)h_row_stride, (long long)n);
+  if (rows == 0 || n == 0) return HGK_OK;
+  const int w_eff = w ? (w_plus_one ? DT_F32 : w_dtype) : dtype;
+  const int t_out = promote(dtype, w_eff);
+  if (t_out != dtype && t_out != DT_F32)
+    return fail(HGK_ERR_UNSUPPORTED, "%s: computation type %s not implemented", fn,
+                dtype_name(t_out));
+  NormArgs a{};
+  // r's rows as groups of one row: row i at i * r_row_stride
+  a.x = x; a.xs = x_row_stride; a.z = r; a.zs = r_row_stride; a.zg = 1; a.zgs = r_row_stride;
+  a.w = w; a.wdt = w_dtype; a.plus_one = w_plus_one ? 1 : 0;
+  a.round_x = (t_out == dtype) ? 1 : 0;
+  a.eps = eps; a.inv_n = (float)(1.0 / (double)n);
+  a.y = y; a.ys = y_row_stride; a.h = h; a.hs = h_row_stride; a.rows = rows; a.n = (int)n;
+  const int vx = 16 / dtype_bytes(dtype);
+  const bool vec_ok = aligned16(x) && aligned16(r) && aligned16(y) && (!h || aligned16(h)) &&
+                      (!w || aligned16(w)) && n % vx == 0 && x_row_stride % vx == 0 &&
+                      r_row_stride % vx == 0 && (!h || h_row_stride % vx == 0) &&
+                      (y_row_stride * dtype_bytes(y_dtype)) % 16 == 0 &&
+                      (n * dtype_bytes(y_dtype)) % 16 == 0;
+  return dispatch<kResid>(a, dtype, y_dtype, vec_ok, as_stream(stream));
 }

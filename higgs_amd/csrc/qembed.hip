@@ -13,6 +13,12 @@
 // Arithmetic (MLX dequantize, S = scales dtype):
 //   v = round_S(round_S(q * s) + b);  optionally v = round_S(v * round_S(scale))
 // which is exact to reproduce: no transcendental functions are involved.
+//
+// The fused form also applies the first layer's input RMSNorm to the row it
+// has just built (the wave holds the whole row in registers), writing the
+// embedding h (the residual stream) and y = rms_norm(h) in one pass: the
+// `embed_tokens.forward(ids)` then `input_layernorm.forward(&h)` pair of
+// transformer.rs:494 and 407.
 #include "../../include/higgs_hip.h"
 #include "hgk_common.h"
 #include "hgk_host.h"
@@ -32,9 +38,18 @@ struct QembArgs {
   int group;
   float scale;
   int has_scale;
-  void* out;
+  void* out;  // h (may be null in the fused form)
   int64_t os;
   int64_t hidden;
+  // fused RMSNorm (qembed_norm_kernel only)
+  const void* nw;
+  int nwdt;
+  int plus_one;
+  int round_x;
+  float eps;
+  float inv_n;
+  void* y;
+  int64_t ys;
 };
 
 __device__ inline int64_t load_id(const QembArgs& a, int64_t t) {
@@ -117,6 +132,137 @@ __global__ __launch_bounds__(256) void qembed_generic_kernel(QembArgs a) {
   store1<S>(a.out, t * a.os + k, x);
 }
 
+// Gather + dequantize + RMSNorm: one wave per token, as qembed_kernel. The
+// row's values are kept packed in S (they are exactly S values) while the f64
+// sum of squares is reduced across the wave; the norm weights (W = S or f32)
+// are loaded with the codes. Computation type T = promote(S, w'), as in
+// rms_norm_kernel; Y is S or f32.
+template <class S, int STEPS, class W, class Y>
+__global__ __launch_bounds__(256) void qembed_norm_kernel(QembArgs a) {
+  constexpr int WW = 8 * W::kBytes / 4;  // 32-bit words of weights per packed word
+  const int lane = threadIdx.x & 63;
+  const int64_t t = (int64_t)blockIdx.x * (blockDim.x >> 6) +
+                    __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (t >= a.n) return;  // whole wave leaves together
+  const int64_t id = load_id(a, t);
+  const bool valid = id >= 0 && id < a.vocab;
+  const int64_t row = valid ? id : 0;
+  const float osc = S::round(a.scale);
+  const uint32_t* wrow = a.wq + row * a.wpr;
+  const int64_t grow = row * a.gpr;
+  const uint16_t* sc = reinterpret_cast<const uint16_t*>(a.sc);
+  const uint16_t* bi = reinterpret_cast<const uint16_t*>(a.bi);
+
+  uint32_t codes[STEPS], sraw[STEPS], braw[STEPS], wr[STEPS][WW];
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s) {
+    const int w = s * 64 + lane;
+    const int wc = w < a.wpr ? w : a.wpr - 1;
+    const int g = (wc * 8) / a.group;
+    codes[s] = wrow[wc];
+    sraw[s] = (uint32_t)sc[grow + g];
+    braw[s] = (uint32_t)bi[grow + g];
+#pragma unroll
+    for (int q = 0; q < WW / 4; ++q) {
+      const u32x4 tw = ld16<W>(a.nw, (int64_t)wc * 8 + q * Vec<W>::N);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) wr[s][4 * q + k] = tw[k];
+    }
+  }
+  // dequantize; h values are S values, kept packed two per word
+  uint32_t hp[STEPS][4];
+  double ss = 0.0;
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s) {
+    const float sv = S::lo(sraw[s]), bv = S::lo(braw[s]);
+    const bool own = s * 64 + lane < a.wpr;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      float v[2];
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const uint32_t q = (codes[s] >> (4 * (2 * k + e))) & 0xfu;
+        float x = deq<S>(q, sv, bv);
+        x = a.has_scale ? S::round(x * osc) : x;
+        v[e] = (valid && own) ? x : 0.0f;
+        ss = __builtin_fma((double)v[e], (double)v[e], ss);
+      }
+      hp[s][k] = S::pack(v[0], v[1]);
+    }
+  }
+  ss = group_sum<64>(ss);
+  const float rr = rms_scale(ss, a.inv_n, a.eps);
+  const bool rx = a.round_x != 0;
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s) {
+    const int w = s * 64 + lane;
+    if (w >= a.wpr) continue;
+    if (a.out) {
+      u32x4 hv;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) hv[k] = hp[s][k];
+      __builtin_nontemporal_store(
+          hv, reinterpret_cast<u32x4*>(reinterpret_cast<char*>(a.out) +
+                                       (t * a.os + (int64_t)w * 8) * S::kBytes));
+    }
+    float o[8];
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+      float n0 = S::lo(hp[s][e / 2]) * rr, n1 = S::hi(hp[s][e / 2]) * rr;
+      if (rx) round2<S>(n0, n1);
+      float w0 = elem<W>(wr[s], e), w1 = elem<W>(wr[s], e + 1);
+      if (a.plus_one) {
+        w0 = w0 + 1.0f;
+        w1 = w1 + 1.0f;
+      }
+      n0 = n0 * w0;
+      n1 = n1 * w1;
+      if constexpr (Y::kCode != S::kCode) {
+        if (rx) round2<S>(n0, n1);
+      }
+      o[e] = n0;
+      o[e + 1] = n1;
+    }
+    store_elems<Y, 8>(a.y, t * a.ys + (int64_t)w * 8, o);
+  }
+}
+
+// Fused form, any layout: one wave per token, two passes (the second
+// dequantizes again), element-strided.
+template <class S, class Y>
+__global__ __launch_bounds__(256) void qembed_norm_generic_kernel(QembArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (t >= a.n) return;  // whole wave leaves together
+  const int64_t id = load_id(a, t);
+  const bool valid = id >= 0 && id < a.vocab;
+  auto value = [&](int64_t k) {
+    if (!valid) return 0.0f;
+    const uint32_t q = (a.wq[id * a.wpr + k / 8] >> (4 * (k % 8))) & 0xfu;
+    const int64_t g = id * a.gpr + k / a.group;
+    float x = deq<S>(q, load1<S>(a.sc, g), load1<S>(a.bi, g));
+    return a.has_scale ? S::round(x * S::round(a.scale)) : x;
+  };
+  double ss = 0.0;
+  for (int64_t k = lane; k < a.hidden; k += 64) {
+    const double v = (double)value(k);
+    ss = __builtin_fma(v, v, ss);
+  }
+  ss = group_sum<64>(ss);
+  const float rr = rms_scale(ss, a.inv_n, a.eps);
+  for (int64_t k = lane; k < a.hidden; k += 64) {
+    const float hv = value(k);
+    if (a.out) store1<S>(a.out, t * a.os + k, hv);
+    float nv = hv * rr;
+    nv = a.round_x ? S::round(nv) : nv;
+    float we = load1_dt(a.nw, a.nwdt, k);
+    we = a.plus_one ? we + 1.0f : we;
+    nv = nv * we;
+    nv = a.round_x ? S::round(nv) : nv;
+    store1<Y>(a.y, t * a.ys + k, nv);
+  }
+}
+
 namespace {
 
 template <class S>
@@ -178,5 +324,96 @@ extern "C" int hgk_quantized_embedding(const void* ids, int ids_dtype, int64_t n
                       hidden % 8 == 0 && out_row_stride % 8 == 0;
   if (scales_dtype == DT_BF16) launch<BF16>(a, vec_ok, as_stream(stream));
   else launch<F16>(a, vec_ok, as_stream(stream));
+  return launch_status(fn);
+}
+
+namespace hgk {
+namespace {
+
+template <class S, class W, class Y>
+bool launch_norm_fast(const QembArgs& a, hipStream_t s) {
+  const int steps = (a.wpr + 63) / 64;
+  const int wpb = a.n >= 1024 ? 4 : 1;
+  const dim3 g((unsigned)((a.n + wpb - 1) / wpb)), b(64 * wpb);
+  if (steps <= 1) hipLaunchKernelGGL((qembed_norm_kernel<S, 1, W, Y>), g, b, 0, s, a);
+  else if (steps <= 2) hipLaunchKernelGGL((qembed_norm_kernel<S, 2, W, Y>), g, b, 0, s, a);
+  else if (steps <= 4) hipLaunchKernelGGL((qembed_norm_kernel<S, 4, W, Y>), g, b, 0, s, a);
+  else if (steps <= 7) hipLaunchKernelGGL((qembed_norm_kernel<S, 7, W, Y>), g, b, 0, s, a);
+  else if (steps <= 8) hipLaunchKernelGGL((qembed_norm_kernel<S, 8, W, Y>), g, b, 0, s, a);
+  else if (steps <= 16) hipLaunchKernelGGL((qembed_norm_kernel<S, 16, W, Y>), g, b, 0, s, a);
+  else return false;
+  return true;
+}
+
+template <class S, class Y>
+void launch_norm(const QembArgs& a, bool vec_ok, hipStream_t s) {
+  if (vec_ok) {
+    if (a.nwdt == S::kCode && launch_norm_fast<S, S, Y>(a, s)) return;
+    if (a.nwdt == DT_F32 && launch_norm_fast<S, F32, Y>(a, s)) return;
+  }
+  const int wpb = a.n >= 1024 ? 4 : 1;
+  hipLaunchKernelGGL((qembed_norm_generic_kernel<S, Y>), dim3((unsigned)((a.n + wpb - 1) / wpb)),
+                     dim3(64 * wpb), 0, s, a);
+}
+
+}  // namespace
+}  // namespace hgk
+
+extern "C" int hgk_quantized_embedding_rms_norm(
+    const void* ids, int ids_dtype, int64_t n_ids, const uint32_t* w_q, const void* scales,
+    const void* biases, int scales_dtype, int64_t vocab, int64_t hidden, int group_size, int bits,
+    float out_scale, void* h, int64_t h_row_stride, const void* norm_w, int norm_w_dtype,
+    int w_plus_one, float eps, void* y, int y_dtype, int64_t y_row_stride, void* stream) {
+  clear_error();
+  const char* fn = "hgk_quantized_embedding_rms_norm";
+  if (bits != 4) return fail(HGK_ERR_UNSUPPORTED, "%s: bits=%d (only 4 is implemented)", fn, bits);
+  if (group_size != 32 && group_size != 64 && group_size != 128)
+    return fail(HGK_ERR_UNSUPPORTED, "%s: group_size=%d (32, 64 or 128)", fn, group_size);
+  if (ids_dtype != DT_I32 && ids_dtype != DT_U32)
+    return fail(HGK_ERR_ARG, "%s: ids dtype must be int32 or uint32", fn);
+  if (scales_dtype != DT_BF16 && scales_dtype != DT_F16)
+    return fail(HGK_ERR_UNSUPPORTED, "%s: scales dtype must be bf16 or f16", fn);
+  if (n_ids < 0 || vocab <= 0 || hidden <= 0)
+    return fail(HGK_ERR_ARG, "%s: bad shape n=%lld vocab=%lld hidden=%lld", fn, (long long)n_ids,
+                (long long)vocab, (long long)hidden);
+  if (hidden % group_size)
+    return fail(HGK_ERR_ARG, "%s: hidden=%lld not a multiple of group_size=%d", fn,
+                (long long)hidden, group_size);
+  if (n_ids > 1 && ((h && h_row_stride < hidden) || y_row_stride < hidden))
+    return fail(HGK_ERR_ARG, "%s: h/y row stride < hidden", fn);
+  if (!ids || !w_q || !scales || !biases || !norm_w || !y)
+    return fail(HGK_ERR_ARG, "%s: null pointer", fn);
+  if (!is_float_dtype(norm_w_dtype) || !is_float_dtype(y_dtype))
+    return fail(HGK_ERR_ARG, "%s: norm weight / y dtype must be f32, bf16 or f16", fn);
+  if (!(eps >= 0.0f)) return fail(HGK_ERR_ARG, "%s: eps must be >= 0", fn);
+  if (hidden > (1 << 24) || n_ids * hidden >= ((int64_t)1 << 40))
+    return fail(HGK_ERR_UNSUPPORTED, "%s: problem too large", fn);
+  const int w_eff = w_plus_one ? DT_F32 : norm_w_dtype;
+  const int t_out = promote(scales_dtype, w_eff);
+  if (t_out != scales_dtype && t_out != DT_F32)
+    return fail(HGK_ERR_UNSUPPORTED, "%s: computation type %s not implemented", fn,
+                dtype_name(t_out));
+  if (y_dtype != scales_dtype && y_dtype != DT_F32)
+    return fail(HGK_ERR_UNSUPPORTED, "%s: y dtype must be the scales dtype or f32", fn);
+  if (n_ids == 0) return HGK_OK;
+  QembArgs a{};
+  a.ids = ids; a.ids_i32 = ids_dtype == DT_I32; a.n = n_ids; a.wq = w_q; a.sc = scales;
+  a.bi = biases; a.vocab = vocab; a.wpr = (int)(hidden / 8); a.gpr = (int)(hidden / group_size);
+  a.group = group_size; a.scale = out_scale; a.has_scale = out_scale != 0.0f;
+  a.out = h; a.os = h_row_stride; a.hidden = hidden;
+  a.nw = norm_w; a.nwdt = norm_w_dtype; a.plus_one = w_plus_one ? 1 : 0;
+  a.round_x = t_out == scales_dtype ? 1 : 0; a.eps = eps; a.inv_n = (float)(1.0 / (double)hidden);
+  a.y = y; a.ys = y_row_stride;
+  const bool vec_ok = (reinterpret_cast<uintptr_t>(w_q) & 3u) == 0 && hidden % 8 == 0 &&
+                      (!h || (aligned16(h) && h_row_stride % 8 == 0)) && aligned16(y) &&
+                      (y_row_stride * dtype_bytes(y_dtype)) % 16 == 0 && aligned16(norm_w);
+  const hipStream_t st = as_stream(stream);
+  if (scales_dtype == DT_BF16) {
+    if (y_dtype == DT_BF16) launch_norm<BF16, BF16>(a, vec_ok, st);
+    else launch_norm<BF16, F32>(a, vec_ok, st);
+  } else {
+    if (y_dtype == DT_F16) launch_norm<F16, F16>(a, vec_ok, st);
+    else launch_norm<F16, F32>(a, vec_ok, st);
+  }
   return launch_status(fn);
 }

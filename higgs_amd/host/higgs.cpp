@@ -486,6 +486,28 @@ Array nn::RmsNorm::forward(const Array& x) const {
   return rms_norm_impl("rms_norm", x, &weight, eps, plus_one);
 }
 
+std::pair<Array, Array> add_rms_norm(const Array& x, const Array& r, const nn::RmsNorm& norm) {
+  const char* op = "add_rms_norm";
+  Operands ops = {{"x", &x}, {"r", &r}, {"w", &norm.weight}};
+  if (x.shape() != r.shape() || x.dtype() != r.dtype())
+    fail(op, "x and r must match in shape and dtype", ops);
+  const Rows xr = rows_of(x, op, ops);
+  const Rows rr = rows_of(r, op, ops);
+  if (norm.weight.ndim() != 1 || norm.weight.dim(0) != xr.n)
+    fail(op, "weight must be 1-D with the size of x's last axis", ops);
+  const Dtype wd = norm.weight.dtype();
+  const Dtype od = promote(x.dtype(), norm.plus_one ? Dtype::Float32 : wd);
+  Array h = Array::empty(x.shape(), x.dtype());
+  Array y = Array::empty(x.shape(), od);
+  if (x.size() == 0) return {h, y};
+  check(hgk_add_rms_norm(static_cast<int>(x.dtype()), x.data(), xr.row_stride, r.data(),
+                         rr.row_stride, norm.weight.data(), static_cast<int>(wd),
+                         norm.plus_one ? 1 : 0, norm.eps, h.data(), xr.n, y.data(),
+                         static_cast<int>(od), xr.n, xr.rows, xr.n, stream_arg()),
+        op, ops);
+  return {h, y};
+}
+
 Array gated_rms_norm(const Array& y, const Array& z, const nn::RmsNorm& norm) {
   const char* op = "gated_rms_norm";
   Operands ops = {{"y", &y}, {"z", &z}, {"w", &norm.weight}};
@@ -684,8 +706,7 @@ int64_t nn::QuantizedEmbedding::hidden() const {
   return weight.dim(1) * 32 / bits;
 }
 
-static Array qembed_impl(const nn::QuantizedEmbedding& e, const Array& ids, float scale) {
-  const char* op = "quantized_embedding";
+static void qembed_check(const char* op, const nn::QuantizedEmbedding& e, const Array& ids) {
   Operands ops = {{"ids", &ids}, {"w", &e.weight}, {"scales", &e.scales}, {"biases", &e.biases}};
   if (e.weight.ndim() != 2 || e.weight.dtype() != Dtype::Uint32 || !e.weight.is_contiguous())
     fail(op, "weight must be contiguous Uint32 [vocab, hidden*bits/32]", ops);
@@ -698,6 +719,13 @@ static Array qembed_impl(const nn::QuantizedEmbedding& e, const Array& ids, floa
   if (e.scales.ndim() != 2 || e.scales.dim(0) != V || e.group_size <= 0 ||
       e.scales.dim(1) * e.group_size != H || !e.scales.is_contiguous() || !e.biases.is_contiguous())
     fail(op, "scales/biases must be contiguous [vocab, hidden/group_size]", ops);
+}
+
+static Array qembed_impl(const nn::QuantizedEmbedding& e, const Array& ids, float scale) {
+  const char* op = "quantized_embedding";
+  Operands ops = {{"ids", &ids}, {"w", &e.weight}, {"scales", &e.scales}, {"biases", &e.biases}};
+  qembed_check(op, e, ids);
+  const int64_t V = e.weight.dim(0), H = e.hidden();
   Shape os = ids.shape();
   os.push_back(H);
   Array out = Array::empty(os, e.scales.dtype());
@@ -708,6 +736,32 @@ static Array qembed_impl(const nn::QuantizedEmbedding& e, const Array& ids, floa
                                 e.group_size, e.bits, scale, out.data(), H, stream_arg()),
         op, ops);
   return out;
+}
+
+std::pair<Array, Array> nn::QuantizedEmbedding::forward_rms_norm(const Array& ids,
+                                                                 const RmsNorm& norm,
+                                                                 float scale) const {
+  const char* op = "quantized_embedding_rms_norm";
+  Operands ops = {{"ids", &ids}, {"w", &weight}, {"scales", &scales}, {"biases", &biases},
+                  {"norm", &norm.weight}};
+  qembed_check(op, *this, ids);
+  const int64_t V = weight.dim(0), H = hidden();
+  if (norm.weight.ndim() != 1 || norm.weight.dim(0) != H || !norm.weight.is_contiguous())
+    fail(op, "norm weight must be contiguous with hidden elements", ops);
+  const Dtype od = promote(scales.dtype(), norm.plus_one ? Dtype::Float32 : norm.weight.dtype());
+  Shape os = ids.shape();
+  os.push_back(H);
+  Array h = Array::empty(os, scales.dtype());
+  Array y = Array::empty(os, od);
+  if (ids.size() == 0) return {h, y};
+  check(hgk_quantized_embedding_rms_norm(
+            ids.data(), static_cast<int>(ids.dtype()), ids.size(),
+            static_cast<const uint32_t*>(weight.data()), scales.data(), biases.data(),
+            static_cast<int>(scales.dtype()), V, H, group_size, bits, scale, h.data(), H,
+            norm.weight.data(), static_cast<int>(norm.weight.dtype()), norm.plus_one ? 1 : 0,
+            norm.eps, y.data(), static_cast<int>(od), H, stream_arg()),
+        op, ops);
+  return {h, y};
 }
 
 Array nn::QuantizedEmbedding::forward(const Array& ids) const { return qembed_impl(*this, ids, 0.0f); }

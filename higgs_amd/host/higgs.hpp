@@ -19,6 +19,7 @@
 //   nn::silu_mul(gate, up)                       nn::silu(gate) * up (transformer.rs:349-353)
 //   nn::gelu_approximate_mul(gate, up)           nn::gelu_approximate(gate) * up (gemma2.rs:422-427)
 //   gated_rms_norm(y, z, norm)                   swiglu(z, norm(y)) (qwen3_next.rs:1204-1205)
+//   add_rms_norm(x, r, norm)                     h = x.add(r); norm(h) (transformer.rs:413-415)
 //   nn::QuantizedEmbedding{...}.forward(ids)     nn::QuantizedEmbedding (transformer.rs:494)
 //                                                and QEmbedding::forward (qwen3_next.rs:248-257)
 //
@@ -149,7 +150,9 @@ class Array {
   // Views.
   Array transpose(const std::vector<int>& axes) const;
   Array slice(int axis, int64_t start, int64_t stop) const;
-  Array reshape(const Shape& shape) const;  // contiguous arrays only
+  // A view when the new shape only splits or merges row-major runs of axes
+  // (always for contiguous arrays); throws where a copy would be needed.
+  Array reshape(const Shape& shape) const;
 
   // Host readback (waits for the current stream). Elements come back in
   // row-major order of the logical shape, whatever the strides.
@@ -222,6 +225,10 @@ struct QuantizedEmbedding {
   // forward followed by h * round(scale) (Gemma's sqrt(H) embedding scale,
   // gemma2.rs:587-600) in the same pass.
   Array forward_scaled(const Array& ids, float scale) const;
+  // forward_scaled(ids, scale) (scale 0: none) followed by the first block's
+  // input norm (transformer.rs:494, 407) in one pass: returns (h, norm(h)).
+  std::pair<Array, Array> forward_rms_norm(const Array& ids, const RmsNorm& norm,
+                                           float scale = 0.0f) const;
 };
 
 Array silu_mul(const Array& gate, const Array& up);
@@ -231,6 +238,9 @@ Array gelu_approximate_mul(const Array& gate, const Array& up);
 Array apply_rope(const Array& x, const nn::Rope& rope, int offset);
 Array apply_rope_batched(const Array& x, const nn::Rope& rope, const Array& offsets);
 Array swiglu(const Array& gate, const Array& x);
+// The block boundary `h = x.add(r); norm.forward(&h)` (transformer.rs:413-415)
+// in one pass: returns (h, norm(h)).
+std::pair<Array, Array> add_rms_norm(const Array& x, const Array& r, const nn::RmsNorm& norm);
 // swiglu(z, norm.forward(y)); z may be a strided view (read in place).
 Array gated_rms_norm(const Array& y, const Array& z, const nn::RmsNorm& norm);
 // Per-head RMSNorm over head_dim, then RoPE, for q [B, L, Hq, D] and

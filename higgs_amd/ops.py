@@ -12,7 +12,11 @@ Each function keeps the reference call's name and argument meaning:
     silu_mul(gate, up)                       nn::silu(gate) * up (transformer.rs:349-353)
     gelu_approximate_mul(gate, up)           nn::gelu_approximate(gate) * up (gemma2.rs:422-427)
     gated_rms_norm(x, z, weight, eps)        swiglu(z, norm(x)) (qwen3_next.rs:1204-1205)
+    add_rms_norm(x, r, weight, eps)          h = x.add(r); norm(h) (transformer.rs:413-415)
     QuantizedEmbedding(...).forward(ids)     nn::QuantizedEmbedding / QEmbedding::forward
+    QuantizedEmbedding(...).forward_rms_norm(ids, w, eps)
+                                             embed_tokens + the first input_layernorm
+                                             (transformer.rs:494, 407)
 
 Errors surface as HgkError (the reference returns Err(Exception::custom(..))).
 Every op enqueues on torch's current CUDA/HIP stream and never synchronises.
@@ -90,6 +94,36 @@ def rms_norm(x: torch.Tensor, weight: Optional[torch.Tensor], eps: float, *,
     check(lib().hgk_rms_norm(_ptr(x), xd, xs, _ptr(weight), wd, int(plus_one), eps,
                              _ptr(out), od, ys, rows, n, _stream(x.device)))
     return out
+
+
+def add_rms_norm(x: torch.Tensor, r: torch.Tensor, weight: Optional[torch.Tensor], eps: float,
+                 *, plus_one: bool = False, out_dtype: Optional[torch.dtype] = None,
+                 h_out: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
+                 write_h: bool = True):
+    """The block boundary `h = x.add(residual); norm.forward(&h)`
+    (transformer.rs:413-415; qwen3_next.rs:1539-1540) in one pass: returns
+    (h, y). Pass ``h_out=x`` to update the residual stream in place;
+    ``write_h=False`` skips h (returns None for it)."""
+    xd = dtype_code(x.dtype)
+    if r.dtype != x.dtype or r.shape != x.shape:
+        raise HgkError(1, "x and r must match in shape and dtype")
+    wd = dtype_code(weight.dtype) if weight is not None else xd
+    w_eff = (F32 if plus_one else wd) if weight is not None else xd
+    od = dtype_code(out_dtype) if out_dtype is not None else _promote(xd, w_eff)
+    rows, n, xs = _rows2d(x)
+    _, _, rs = _rows2d(r)
+    if weight is not None and (weight.dim() != 1 or weight.shape[0] != n):
+        raise HgkError(1, f"weight shape {tuple(weight.shape)} does not match ({n},)")
+    if write_h and h_out is None:
+        h_out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    hs = _rows2d(h_out)[2] if h_out is not None else 0
+    if out is None:
+        out = torch.empty(x.shape, dtype=_TORCH[od], device=x.device)
+    _, _, ys = _rows2d(out)
+    check(lib().hgk_add_rms_norm(xd, _ptr(x), xs, _ptr(r), rs, _ptr(weight), wd, int(plus_one),
+                                 eps, _ptr(h_out), hs, _ptr(out), od, ys, rows, n,
+                                 _stream(x.device)))
+    return h_out, out
 
 
 def _z_layout(z: torch.Tensor, rows: int, n: int):
@@ -302,6 +336,30 @@ class QuantizedEmbedding:
         return out.reshape(*ids.shape, self.hidden)
 
     __call__ = forward
+
+    def forward_rms_norm(self, ids: torch.Tensor, weight: torch.Tensor, eps: float, *,
+                         plus_one: bool = False, out_scale: float = 0.0,
+                         out_dtype: Optional[torch.dtype] = None, write_h: bool = True):
+        """forward(ids) followed by the first block's input RMSNorm, in one
+        pass: returns (h, y), both [*ids.shape, hidden]; h is None when
+        ``write_h`` is False."""
+        idd = dtype_code(ids.dtype)
+        sd = dtype_code(self.scales.dtype)
+        wd = dtype_code(weight.dtype)
+        w_eff = F32 if plus_one else wd
+        od = dtype_code(out_dtype) if out_dtype is not None else _promote(sd, w_eff)
+        flat = ids.reshape(-1).contiguous()
+        T = flat.numel()
+        h = (torch.empty((T, self.hidden), dtype=_TORCH[sd], device=ids.device)
+             if write_h else None)
+        y = torch.empty((T, self.hidden), dtype=_TORCH[od], device=ids.device)
+        check(lib().hgk_quantized_embedding_rms_norm(
+            _ptr(flat), idd, T, _ptr(self.weight), _ptr(self.scales), _ptr(self.biases), sd,
+            self.vocab, self.hidden, self.group_size, self.bits, out_scale, _ptr(h),
+            self.hidden, _ptr(weight), wd, int(plus_one), eps, _ptr(y), od, self.hidden,
+            _stream(ids.device)))
+        shape = (*ids.shape, self.hidden)
+        return (None if h is None else h.reshape(shape)), y.reshape(shape)
 
 
 def gemma_embed_scale(hidden: int) -> float:

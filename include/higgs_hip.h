@@ -73,6 +73,26 @@ int hgk_rms_norm(const void* x, int x_dtype, int64_t x_row_stride,
                  int64_t rows, int64_t n, void* stream);
 
 /*
+ * Residual add fused with the RMSNorm that follows it:
+ *   h = round_T(x + r)              (MLX add, T = the activation dtype)
+ *   y = w' * round(h * rsqrt(mean(h^2) + eps))   (as hgk_rms_norm)
+ * writing both h (the new residual stream) and y. Replaces the block
+ * boundary `let h = x.add(residual)?; post_attention_layernorm.forward(&h)`
+ * (crates/higgs-models/src/transformer.rs:413-415; qwen3_next.rs:1539-1540)
+ * and the next block's `input_layernorm.forward(x)` after `h.add(mlp_out)`
+ * (transformer.rs:407, 417). x, r and h share `dtype`; w, w_plus_one, eps and
+ * y_dtype mean what they mean for hgk_rms_norm. h may be NULL (y only), and
+ * h may be x or r itself (an in-place residual update); y must not overlap
+ * x, r or h.
+ */
+int hgk_add_rms_norm(int dtype, const void* x, int64_t x_row_stride,
+                     const void* r, int64_t r_row_stride,
+                     const void* w, int w_dtype, int w_plus_one, float eps,
+                     void* h, int64_t h_row_stride,
+                     void* y, int y_dtype, int64_t y_row_stride,
+                     int64_t rows, int64_t n, void* stream);
+
+/*
  * Host helper: the dims/2 inverse frequencies fast::rope uses,
  *   inv[i] = freqs ? 1/freqs[i] : exp(-i * log(base) / (dims/2)).
  * Mirrors the frequency derivation inside mlx_rs::fast::rope
@@ -184,6 +204,27 @@ int hgk_quantized_embedding(const void* ids, int ids_dtype, int64_t n_ids,
                             int64_t vocab, int64_t hidden, int group_size, int bits,
                             float out_scale, void* out, int64_t out_row_stride,
                             void* stream);
+
+/*
+ * The embedding gather fused with the first layer's input RMSNorm: writes
+ * h = hgk_quantized_embedding(...) (the residual stream) and
+ * y = rms_norm(h, norm_w, eps) in one pass over the gathered rows. Replaces
+ * `let h = self.embed_tokens.forward(inputs)?` followed by the first block's
+ * `self.input_layernorm.forward(x)?` (crates/higgs-models/src/transformer.rs:494,
+ * 407; gemma2.rs:587-600 then 491 with the Gemma scale in out_scale and
+ * w_plus_one = 1). The table arguments mean what they mean for
+ * hgk_quantized_embedding; norm_w, w_plus_one, eps and y_dtype what they mean
+ * for hgk_rms_norm (y_dtype: the scales dtype or f32). h may be NULL.
+ * Invalid ids give zero rows in h and in y.
+ */
+int hgk_quantized_embedding_rms_norm(const void* ids, int ids_dtype, int64_t n_ids,
+                                     const uint32_t* w_q, const void* scales,
+                                     const void* biases, int scales_dtype,
+                                     int64_t vocab, int64_t hidden, int group_size, int bits,
+                                     float out_scale, void* h, int64_t h_row_stride,
+                                     const void* norm_w, int norm_w_dtype, int w_plus_one,
+                                     float eps, void* y, int y_dtype, int64_t y_row_stride,
+                                     void* stream);
 
 #ifdef __cplusplus
 }

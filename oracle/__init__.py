@@ -60,6 +60,7 @@ def lib():
             "or_convert_to_f32": (None, [_i32, _vp, _vp, _i64]),
             "or_rms_norm": (_i32, [_vp, _i32, _i64, _vp, _i32, _i32, _f32,
                                    _vp, _i32, _i64, _i64, _i64]),
+            "or_add": (_i32, [_i32, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64]),
             "or_rope_inv_freq": (None, [_f32, _i32, _vp, _vp]),
             "or_llama3_freqs": (None, [_f32, _i32, _f32, _f32, _f32, _f32, _vp]),
             "or_norm_rope": (_i32, [_i32, _vp, _vp, _vp, _vp, _i64, _i64, _i64,
@@ -160,6 +161,35 @@ def rms_norm(x, x_dt, w, w_dt, eps, *, plus_one=False, out_dt=None):
                              w_dt, int(plus_one), eps, _p(y), out_dt, n, rows, n),
            "rms_norm")
     return y
+
+
+def add(a, b, dt):
+    """MLX add of two [rows, n] storage arrays (rows may be strided views)."""
+    rows, n = a.shape
+    assert b.shape == a.shape and a.strides[1] == a.itemsize and b.strides[1] == b.itemsize
+    out = np.empty((rows, n), storage_dtype(dt))
+    _check(lib().or_add(dt, C.c_void_p(a.__array_interface__["data"][0]), a.strides[0] // a.itemsize,
+                        C.c_void_p(b.__array_interface__["data"][0]), b.strides[0] // b.itemsize,
+                        _p(out), n, rows, n), "add")
+    return out
+
+
+def add_rms_norm(x, r, dt, w, w_dt, eps, *, plus_one=False, out_dt=None):
+    """The block boundary `h = x.add(residual); norm(h)` (transformer.rs:413-415;
+    qwen3_next.rs:1539-1540): returns (h, y) with h = MLX add on dt and
+    y = rms_norm(h)."""
+    h = add(x, r, dt)
+    return h, rms_norm(h, dt, w, w_dt, eps, plus_one=plus_one, out_dt=out_dt)
+
+
+def qembed_rms_norm(ids_arr, wq, scales, biases, s_dt, w, w_dt, eps, *, group=64, bits=4,
+                    out_scale=0.0, plus_one=False, out_dt=None):
+    """`embed_tokens.forward(ids)` then the first block's
+    `input_layernorm.forward(&h)` (transformer.rs:494, 407; gemma2.rs:587-600,
+    491): returns (h, y) for ids flattened to [T]."""
+    h = qembed(np.ascontiguousarray(ids_arr).reshape(-1), wq, scales, biases, s_dt,
+               group=group, bits=bits, out_scale=out_scale)
+    return h, rms_norm(h, s_dt, w, w_dt, eps, plus_one=plus_one, out_dt=out_dt)
 
 
 def rope_inv_freq(base, dims, freqs=None) -> np.ndarray:

@@ -255,6 +255,20 @@ int or_rms_norm(const void* x, int x_dt, int64_t x_rs, const void* w, int w_dt,
   return 0;
 }
 
+/* MLX's elementwise add on dtype dt: both operands widened to f32, one f32
+ * add, one rounding to dt (the `x.add(residual)` of transformer.rs:413 and
+ * 417; gemma2.rs:498, 504; qwen3_next.rs:1539, 1544). Rows of n elements with
+ * separate row strides; out may be a or b itself. */
+int or_add(int dt, const void* a, int64_t a_rs, const void* b, int64_t b_rs,
+           void* out, int64_t o_rs, int64_t rows, int64_t n) {
+  if (!a || !b || !out || rows < 0 || n < 0 || !is_float_dt(dt)) return 1;
+#pragma omp parallel for schedule(static)
+  for (int64_t r = 0; r < rows; ++r)
+    for (int64_t i = 0; i < n; ++i)
+      st(out, dt, r * o_rs + i, rnd(ld(a, dt, r * a_rs + i) + ld(b, dt, r * b_rs + i), dt));
+  return 0;
+}
+
 /* ------------------------------------------------------------------ */
 /* RoPE                                                                */
 /* ------------------------------------------------------------------ */

@@ -20,6 +20,10 @@
  *                      transformer.rs:264-269) followed by fast::rope
  *                      (utils.rs:16-26; transformer.rs:747-802 per-request
  *                      offsets; qwen3_next.rs:754-756 partial rotary).
+ *   or_add             MLX's add (the residual `x.add(r)`, transformer.rs:413,
+ *                      417); with or_rms_norm it restates the fused residual
+ *                      add + RMSNorm of the block boundary (transformer.rs:
+ *                      413-415, 417 then 407).
  *   or_rope_inv_freq   the inverse frequencies fast::rope derives from `base`
  *                      (or 1/freqs when explicit frequencies are given,
  *                      deepseek_v2.rs:222-225).
@@ -74,6 +78,10 @@ int or_rms_norm(const void* x, int x_dt, int64_t x_row_stride,
                 const void* w, int w_dt, int plus_one, float eps,
                 void* y, int y_dt, int64_t y_row_stride,
                 int64_t rows, int64_t n);
+
+/* MLX add on dt (f32 sum rounded once); out may alias a or b. */
+int or_add(int dt, const void* a, int64_t a_rs, const void* b, int64_t b_rs,
+           void* out, int64_t o_rs, int64_t rows, int64_t n);
 
 void or_rope_inv_freq(float base, int dims, const float* freqs, float* inv_out);
 void or_llama3_freqs(float base, int dims, float factor, float low_freq_factor,

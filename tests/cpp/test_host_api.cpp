@@ -444,6 +444,62 @@ TEST(test_quantized_embedding_llama_table) {
   ASSERT_BITS_EQ(got_s, want);
 }
 
+// ---------------------------------------------------------------- fused forms
+// The block boundary `h = x.add(r); post_attention_layernorm(h)`
+// (transformer.rs:413-415) in one call, three blocks in a row.
+TEST(test_add_rms_norm_block_boundaries) {
+  const int64_t R = 256, N = 2048;
+  auto hb = bits_of(normal(9100, R * N), OR_BF16);
+  auto wb = bits_of(normal(9101, N, 1.0f, 0.02f), OR_BF16);
+  higgs::nn::RmsNorm norm{dev16(wb, {N}, Dtype::Bfloat16), 1e-5f};
+  Array h = dev16(hb, {R, N}, Dtype::Bfloat16);
+  for (int blk = 0; blk < 3; ++blk) {
+    auto rb = bits_of(normal(9110 + blk, R * N, 0.0f, 0.5f), OR_BF16);
+    auto hy = higgs::add_rms_norm(h, dev16(rb, {R, N}, Dtype::Bfloat16), norm);
+    std::vector<uint16_t> want_h(R * N), want_y(R * N);
+    ASSERT(or_add(OR_BF16, hb.data(), N, rb.data(), N, want_h.data(), N, R, N) == 0, "oracle add");
+    ASSERT(or_rms_norm(want_h.data(), OR_BF16, N, wb.data(), OR_BF16, 0, 1e-5f, want_y.data(), OR_BF16,
+                       N, R, N) == 0, "oracle norm");
+    auto got_h = hy.first.to_bits();
+    auto got_y = hy.second.to_bits();
+    ASSERT_BITS_EQ(got_h, want_h);
+    ASSERT_BITS_EQ(got_y, want_y);
+    h = hy.first;
+    hb = want_h;
+  }
+}
+
+// embed_tokens.forward(ids) then the first input_layernorm (transformer.rs:494,
+// 407) in one call; Gemma's scale and (1 + w) norm (gemma2.rs:587-600, 491).
+TEST(test_quantized_embedding_forward_rms_norm) {
+  const int64_t V = 4096, H = 3584, G = 64, T = 300;
+  std::vector<uint32_t> wq(V * H / 8);
+  or_fill_u32(9200, wq.data(), static_cast<int64_t>(wq.size()));
+  auto sb = bits_of(uniform(9201, V * H / G, 0.005f, 0.02f), OR_BF16);
+  auto bb = bits_of(uniform(9202, V * H / G, -0.1f, 0.1f), OR_BF16);
+  auto wb = bits_of(normal(9203, H, 0.0f, 0.02f), OR_BF16);
+  std::vector<uint32_t> ids(T);
+  or_fill_ids(9204, static_cast<uint32_t>(V), ids.data(), T);
+  higgs::nn::QuantizedEmbedding emb{Array::from_slice(wq, {V, H / 8}), dev16(sb, {V, H / G}, Dtype::Bfloat16),
+                                    dev16(bb, {V, H / G}, Dtype::Bfloat16), 64, 4};
+  higgs::nn::RmsNorm norm{dev16(wb, {H}, Dtype::Bfloat16), 1e-6f, true};
+  const float scale = std::sqrt(3584.0f);
+  auto hy = emb.forward_rms_norm(Array::from_slice(ids, {T}), norm, scale);
+  ASSERT(hy.second.dtype() == Dtype::Float32, "%s", hy.second.describe().c_str());
+  std::vector<uint16_t> want_h(T * H);
+  std::vector<float> want_y(T * H);
+  ASSERT(or_qembed(ids.data(), OR_U32, T, wq.data(), sb.data(), bb.data(), OR_BF16, V, H, 64, 4, scale,
+                   want_h.data()) == 0, "oracle embed");
+  ASSERT(or_rms_norm(want_h.data(), OR_BF16, H, wb.data(), OR_BF16, 1, 1e-6f, want_y.data(), OR_F32, H, T,
+                     H) == 0, "oracle norm");
+  auto got_h = hy.first.to_bits();
+  ASSERT_BITS_EQ(got_h, want_h);
+  auto got_y = hy.second.to_f32();
+  for (int64_t i = 0; i < T * H; ++i)
+    ASSERT(std::memcmp(&got_y[i], &want_y[i], 4) == 0, "y at %lld: %.9g vs %.9g", (long long)i,
+           got_y[i], want_y[i]);
+}
+
 // ---------------------------------------------------------------- empty inputs
 TEST(test_empty_inputs_give_empty_results) {
   higgs::nn::RmsNorm norm{Array::from_slice(std::vector<float>(64, 1.0f), {64}, Dtype::Bfloat16), 1e-5f};

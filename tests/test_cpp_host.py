@@ -22,7 +22,8 @@ EXPECTED = {
     "test_gated_rms_norm_reads_z_in_place", "test_silu_mul_and_gelu_approximate_mul",
     "test_swiglu_fused_gate_up_halves", "test_quantized_embedding_llama_table",
     "test_empty_inputs_give_empty_results", "test_errors_name_the_op_and_operands",
-    "test_ops_run_on_the_scoped_stream",
+    "test_ops_run_on_the_scoped_stream", "test_add_rms_norm_block_boundaries",
+    "test_quantized_embedding_forward_rms_norm",
 }
 
 
@@ -47,13 +48,15 @@ def test_host_library_exports_the_mlx_shaped_api():
                 "higgs::nn::RmsNorm::forward(", "higgs::nn::Rope::forward(",
                 "higgs::nn::QuantizedEmbedding::forward(", "higgs::nn::silu_mul(",
                 "higgs::nn::gelu_approximate_mul(", "higgs::apply_rope(", "higgs::swiglu(",
-                "higgs::gated_rms_norm(", "higgs::qk_norm_rope(", "higgs::Array::from_slice("):
+                "higgs::gated_rms_norm(", "higgs::qk_norm_rope(", "higgs::Array::from_slice(",
+                "higgs::add_rms_norm(", "higgs::nn::QuantizedEmbedding::forward_rms_norm("):
         assert sym in out, sym
     # the host library reaches the kernels only through the C ABI
     dyn = subprocess.run(["nm", "-D", "--undefined-only", HOST_LIB], capture_output=True,
                          text=True, check=True).stdout
     for fn in ("hgk_rms_norm", "hgk_rope", "hgk_qk_norm_rope", "hgk_glu", "hgk_gated_rms_norm",
-               "hgk_quantized_embedding", "hgk_last_error"):
+               "hgk_quantized_embedding", "hgk_last_error", "hgk_add_rms_norm",
+               "hgk_quantized_embedding_rms_norm"):
         assert fn in dyn, fn
 
 

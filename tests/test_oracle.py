@@ -390,3 +390,84 @@ def test_rng_is_deterministic_and_well_formed():
     assert i.max() < 128256 and i.min() >= 0
     o = O.offsets(1004, 10_000, 1, 32768)
     assert o.min() >= 1 and o.max() <= 32768
+
+
+# ------------------------------------------------------------------ residual add (+ norm)
+def test_add_matches_torch_bf16_numpy_f16_and_f32():
+    """MLX's add on bf16/f16 widens to f32, adds once and rounds once. torch's
+    bf16 add and numpy's float16 add are independent implementations of the
+    same IEEE operation; f32 is plain IEEE addition."""
+    a = O.normal(2101, (64, 256)) * np.float32(40.0)
+    b = O.normal(2102, (64, 256)) * np.float32(40.0)
+    # exact bf16 ties: a + b lands halfway between two bf16 values
+    a[0, :8] = np.float32(1.0)
+    b[0, :8] = np.float32(2.0 ** -8) * np.arange(1, 9, dtype=np.float32)
+    a[1, :4] = [60000.0, -60000.0, 1.0, -3.0]
+    b[1, :4] = [60000.0, -60000.0, -1.0, 3.0]
+    xa, xb = O.from_f32(a, O.BF16), O.from_f32(b, O.BF16)
+    ref = (from_bf16_bits(xa) + from_bf16_bits(xb)).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(O.add(xa, xb, O.BF16), ref)
+    ha, hb = O.from_f32(a, O.F16), O.from_f32(b, O.F16)
+    with np.errstate(over="ignore"):
+        ref16 = (ha.view(np.float16) + hb.view(np.float16)).view(np.uint16)
+    assert np.array_equal(O.add(ha, hb, O.F16), ref16)  # incl. 60000+60000 -> inf
+    assert np.array_equal(O.add(a, b, O.F32), a + b)
+    # strided rows and an in-place form
+    wide = O.from_f32(O.normal(2103, (16, 96)), O.BF16)
+    got = O.add(wide[:, :48], wide[:, 48:], O.BF16)
+    ref = (from_bf16_bits(wide[:, :48]) + from_bf16_bits(wide[:, 48:])).view(torch.int16)
+    assert np.array_equal(got, ref.numpy().view(np.uint16))
+
+
+def test_add_rms_norm_closed_forms():
+    """r = 0 leaves h = x and y = rms_norm(x); r = -x gives h = +0 and y = 0
+    (the zero row's scale is 1/sqrt(eps), times 0)."""
+    x = O.from_f32(O.normal(2111, (32, 512)), O.BF16)
+    w = O.from_f32(O.normal(2112, (512,), 1.0, 0.02), O.BF16)
+    zero = O.from_f32(np.zeros((32, 512), np.float32), O.BF16)
+    h, y = O.add_rms_norm(x, zero, O.BF16, w, O.BF16, 1e-5)
+    assert np.array_equal(h, x)
+    assert np.array_equal(y, O.rms_norm(x, O.BF16, w, O.BF16, 1e-5))
+    neg = x ^ np.uint16(0x8000)
+    h, y = O.add_rms_norm(x, neg, O.BF16, w, O.BF16, 1e-5)
+    assert not h.any() and not (y & np.uint16(0x7FFF)).any()
+
+
+def test_add_rms_norm_matches_torch_composition():
+    """h from torch's bf16 add; y against a float64 RMSNorm of that h within
+    the bf16 bar (the f64 path rounds differently only in the last place)."""
+    x = O.from_f32(O.normal(2121, (48, 2048)), O.BF16)
+    r = O.from_f32(O.normal(2122, (48, 2048)), O.BF16)
+    w = O.from_f32(O.normal(2123, (2048,), 1.0, 0.02), O.BF16)
+    h, y = O.add_rms_norm(x, r, O.BF16, w, O.BF16, 1e-5)
+    th = from_bf16_bits(x) + from_bf16_bits(r)
+    assert np.array_equal(h, th.view(torch.int16).numpy().view(np.uint16))
+    hd = th.double()
+    ref = hd * torch.rsqrt((hd * hd).mean(-1, keepdim=True) + 1e-5) * from_bf16_bits(w).double()
+    assert_close(y, bf16_bits_torch(ref.float().numpy()), O.BF16, max_ulp=2,
+                 what="add_rms_norm vs f64")
+
+
+def test_qembed_rms_norm_constant_row_closed_form():
+    """Codes all 3 with scale 1 and bias 0 give h = 3 exactly; the norm of a
+    constant row c is c / sqrt(c^2 + eps), which rounds to 1.0 in bf16 at
+    eps = 1e-5, so y is exactly the weight row."""
+    V, Hd = 16, 256
+    wq = np.full((V, Hd // 8), 0x33333333, np.uint32)
+    one = O.from_f32(np.ones((V, Hd // 64), np.float32), O.BF16)
+    zero = O.from_f32(np.zeros((V, Hd // 64), np.float32), O.BF16)
+    w = O.from_f32(O.normal(2131, (Hd,), 1.0, 0.02), O.BF16)
+    ids = np.array([0, 5, 15], np.uint32)
+    h, y = O.qembed_rms_norm(ids, wq, one, zero, O.BF16, w, O.BF16, 1e-5)
+    assert np.array_equal(O.to_f32(h, O.BF16), np.full((3, Hd), 3.0, np.float32))
+    assert np.array_equal(y, np.broadcast_to(w, (3, Hd)))
+    # and in general it is the gather followed by the norm, invalid ids -> zero rows
+    wq = O.u32(2132, (V, Hd // 8))
+    s = O.from_f32(O.uniform(2133, (V, Hd // 64), 0.005, 0.02), O.BF16)
+    b = O.from_f32(O.uniform(2134, (V, Hd // 64), -0.1, 0.1), O.BF16)
+    ids = np.array([1, -1, 20, 3], np.int32)
+    h, y = O.qembed_rms_norm(ids, wq, s, b, O.BF16, w, O.BF16, 1e-6, out_scale=16.0)
+    hq = O.qembed(ids, wq, s, b, O.BF16, out_scale=16.0)
+    assert np.array_equal(h, hq)
+    assert np.array_equal(y, O.rms_norm(hq, O.BF16, w, O.BF16, 1e-6))
+    assert not y[2].any()
