@@ -137,6 +137,29 @@ def k_rmsnorm(cx, name, sets, w, rows, n, eps, plus_one=0, ydt=BF16):
                   cpu=("rms", dict(rows=rows, n=n, eps=eps, plus_one=plus_one, ydt=ydt)))
 
 
+def k_embed_norm(cx, name, sets, tab, w, V, Hd, n, eps, scale=0.0, group=64, plus_one=0,
+                 ydt=BF16):
+    """Embedding gather + the first RMSNorm in one kernel: writes h and y."""
+    wq, sc, bi = tab
+    nbytes = n * (Hd // 2 + 2 * 2 * (Hd // group) + 4 + Hd * 2 + Hd * (4 if ydt == F32 else 2))
+    nbytes += Hd * 2
+    args = [(_vp(ids), I32, n, _vp(wq), _vp(sc), _vp(bi), BF16, V, Hd, group, 4, _f(scale),
+             _vp(h), Hd, _vp(w), BF16, plus_one, _f(eps), _vp(y), ydt, Hd, cx.stream)
+            for ids, h, y in sets]
+    return Kernel(name, nbytes, cx.lib.hgk_quantized_embedding_rms_norm, args, n,
+                  keep=(sets, tab, w),
+                  cpu=("qembed_rms", dict(V=V, H=Hd, n=n, scale=scale, group=group, eps=eps)))
+
+
+def k_add_rmsnorm(cx, name, sets, w, rows, n, eps):
+    """Residual add + RMSNorm: reads x and r, writes h and y."""
+    nbytes = 4 * rows * n * 2 + n * 2
+    args = [(BF16, _vp(x), n, _vp(r), n, _vp(w), BF16, 0, _f(eps), _vp(h), n, _vp(y), BF16, n,
+             rows, n, cx.stream) for x, r, h, y in sets]
+    return Kernel(name, nbytes, cx.lib.hgk_add_rms_norm, args, rows, keep=(sets, w),
+                  cpu=("add_rms", dict(rows=rows, n=n, eps=eps)))
+
+
 def k_glu(cx, name, sets, rows, n, act):
     nbytes = 3 * rows * n * 2
     args = [(act, BF16, _vp(g), n, _vp(u), n, _vp(o), BF16, n, rows, n, cx.stream)
@@ -205,6 +228,54 @@ def wl_llama_chain(cx):
            "head_dim": 64, "rope": "llama3 factor 32, theta 5e5", "quant": "4-bit g64",
            "buffer_sets": ns}
     return Workload("llama32_1b_chain", cfg, ks, ns, T, cpu_sample=cpu_sample_llama)
+
+
+def wl_llama_chain_fused(cx):
+    """The Llama-3.2-1B chain with the embedding gather and the first RMSNorm
+    in one kernel (gather+norm -> llama3 RoPE -> SwiGLU over 4096 tokens)."""
+    torch = cx.torch
+    V, Hd, T, B, L, I = 128256, 2048, 4096, 4, 1024, 8192
+    tab = cx.qtable(V, Hd)
+    from higgs_amd.ops import llama3_rope_freqs
+    freqs = llama3_rope_freqs(500000.0, 64, 32.0, 1.0, 4.0, 8192.0)
+    w = cx.randn((Hd,), torch.bfloat16, 1.0, 0.02)
+    set_bytes = T * Hd * 2 * 2 + B * L * 40 * 64 * 2 * 2 + T * I * 2 * 3
+    ns = nsets_for(set_bytes)
+    emb = [(cx.ids(T, V), cx.empty((T, Hd), torch.bfloat16), cx.empty((T, Hd), torch.bfloat16))
+           for _ in range(ns)]
+    rp = [(cx.randn((B, L, 32, 64), torch.bfloat16), cx.randn((B, L, 8, 64), torch.bfloat16),
+           cx.empty((B, 32, L, 64), torch.bfloat16), cx.empty((B, 8, L, 64), torch.bfloat16))
+          for _ in range(ns)]
+    gl = [(cx.randn((T, I), torch.bfloat16), cx.randn((T, I), torch.bfloat16),
+           cx.empty((T, I), torch.bfloat16)) for _ in range(ns)]
+    ks = [k_embed_norm(cx, "qembed_rms_norm", emb, tab, w, V, Hd, T, 1e-5),
+          k_qkrope(cx, "rope_llama3", rp, B, L, 32, 8, 64, 64, 500000.0, freqs=freqs),
+          k_glu(cx, "swiglu", gl, T, I, SILU)]
+    cfg = {"workload": "llama3.2-1b layer-op chain, embedding+norm fused", "tokens": T,
+           "batch": B, "seq_len": L, "hidden": Hd, "vocab": V, "intermediate": I,
+           "buffer_sets": ns}
+    return Workload("llama32_1b_chain_fused", cfg, ks, ns, T)
+
+
+def wl_block_boundary(cx):
+    """Residual add + RMSNorm at the Llama-3.2-1B (4096 x 2048) and Qwen3-8B
+    (16384 x 4096) prefill shapes."""
+    torch = cx.torch
+    ks, tot = [], 0
+    for name, rows, n, eps in (("add_rms_norm_llama", 4096, 2048, 1e-5),
+                               ("add_rms_norm_qwen3", 16384, 4096, 1e-6)):
+        ns = nsets_for(rows * n * 8, 2 << 30)
+        w = cx.randn((n,), torch.bfloat16, 1.0, 0.02)
+        sets = [(cx.randn((rows, n), torch.bfloat16), cx.randn((rows, n), torch.bfloat16),
+                 cx.empty((rows, n), torch.bfloat16), cx.empty((rows, n), torch.bfloat16))
+                for _ in range(ns)]
+        ks.append(k_add_rmsnorm(cx, name, sets, w, rows, n, eps))
+        tot = max(tot, ns)
+    for k in ks:  # equal set counts so one step index serves both
+        k.argsets = [k.argsets[i % len(k.argsets)] for i in range(tot)]
+    cfg = {"workload": "residual add + rmsnorm (block boundary)", "shapes": "4096x2048, 16384x4096",
+           "buffer_sets": tot}
+    return Workload("block_boundary_add_rms_norm", cfg, ks, tot, 4096 + 16384)
 
 
 def wl_rmsnorm_512(cx):
@@ -317,6 +388,8 @@ WORKLOADS = {
     "qwen3_8b_prefill": wl_qwen3_prefill,
     "gemma2_9b_prefill": wl_gemma2,
     "qwen3_next_decode": wl_qwen3_next_decode,
+    "llama32_1b_chain_fused": wl_llama_chain_fused,
+    "block_boundary_add_rms_norm": wl_block_boundary,
 }
 
 
@@ -584,6 +657,26 @@ def cpu_op(spec, budget_s=1.0):
         scale = p["scale"]
         fn = lambda: O.qembed(ids, wq, sc, bi, B16, group=G, out_scale=scale)
         nbytes = T * (H // 2 + 4 * (H // G) + 4 + 2 * H)
+        rows, what = T, f"{T} of {p['n']} ids (full {V}x{H} table)"
+    elif kind == "add_rms":
+        R = min(p["rows"], 256)
+        x = O.from_f32(O.normal(7016, (R, p["n"])), B16)
+        r = O.from_f32(O.normal(7017, (R, p["n"])), B16)
+        w = O.from_f32(O.normal(7018, (p["n"],), 1.0, 0.02), B16)
+        fn = lambda: O.add_rms_norm(x, r, B16, w, B16, p["eps"])
+        nbytes = 4 * R * p["n"] * 2 + p["n"] * 2
+        rows, what = R, f"{R} of {p['rows']} rows"
+    elif kind == "qembed_rms":
+        V, H, G = p["V"], p["H"], p["group"]
+        T = min(p["n"], 256)
+        wq = O.u32(7019, (V, H // 8))
+        sc = O.from_f32(O.uniform(7020, (V, H // G), 0.005, 0.02), B16)
+        bi = O.from_f32(O.uniform(7021, (V, H // G), -0.1, 0.1), B16)
+        w = O.from_f32(O.normal(7022, (H,), 1.0, 0.02), B16)
+        ids = O.ids(7023, T, V)
+        fn = lambda: O.qembed_rms_norm(ids, wq, sc, bi, B16, w, B16, p["eps"], group=G,
+                                       out_scale=p["scale"])
+        nbytes = T * (H // 2 + 4 * (H // G) + 4 + 4 * H) + 2 * H
         rows, what = T, f"{T} of {p['n']} ids (full {V}x{H} table)"
     else:
         raise ValueError(kind)
