@@ -43,6 +43,17 @@ PROTOTYPES = {
     "hgk_quantized_embedding_rms_norm": (_int, [_vp, _int, _i64, _vp, _vp, _vp, _int, _i64,
                                                 _i64, _int, _int, _f32, _vp, _i64, _vp, _int,
                                                 _int, _f32, _vp, _int, _i64, _vp]),
+    "hgk_st_open": (_int, [C.c_char_p, C.POINTER(_vp)]),
+    "hgk_st_close": (None, [_vp]),
+    "hgk_st_count": (_i64, [_vp]),
+    "hgk_st_find": (_int, [_vp, C.c_char_p, C.POINTER(_i64)]),
+    "hgk_st_tensor": (_int, [_vp, _i64, C.POINTER(C.c_char_p), C.POINTER(C.c_char_p),
+                             C.POINTER(_int), C.POINTER(_int), C.POINTER(_i64),
+                             C.POINTER(_i64)]),
+    "hgk_st_copy_to_host": (_int, [_vp, _i64, _vp, _i64]),
+    "hgk_st_upload": (_int, [_vp, _i64, _vp, _i64, _vp]),
+    "hgk_st_collect_files": (_int, [C.c_char_p, C.c_char_p, _i64, C.POINTER(_i64)]),
+    "hgk_remap_quantized_key": (_int, [C.c_char_p, C.c_char_p, _i64]),
 }
 
 

@@ -769,4 +769,103 @@ Array nn::QuantizedEmbedding::forward_scaled(const Array& ids, float scale) cons
   return qembed_impl(*this, ids, scale);
 }
 
+
+// ------------------------------------------------------------------ checkpoints
+namespace io {
+
+std::vector<std::string> collect_safetensors_files(const std::string& model_dir) {
+  int64_t need = 0;
+  check(hgk_st_collect_files(model_dir.c_str(), nullptr, 0, &need), "collect_safetensors_files", {});
+  std::string buf((size_t)need, '\0');
+  check(hgk_st_collect_files(model_dir.c_str(), &buf[0], need, &need), "collect_safetensors_files", {});
+  std::vector<std::string> out;
+  size_t pos = 0;
+  for (size_t nl; (nl = buf.find('\n', pos)) != std::string::npos; pos = nl + 1)
+    out.push_back(buf.substr(pos, nl - pos));
+  return out;
+}
+
+std::optional<std::string> remap_quantized_key(const std::string& key) {
+  std::string buf(key.size() + 16, '\0');
+  const int st = hgk_remap_quantized_key(key.c_str(), &buf[0], (int64_t)buf.size());
+  if (st == HGK_ERR_UNSUPPORTED) return std::nullopt;
+  check(st, "remap_quantized_key", {});
+  return std::string(buf.c_str());
+}
+
+SafetensorsFile::SafetensorsFile(const std::string& path) : path_(path) {
+  check(hgk_st_open(path.c_str(), &f_), "load_safetensors", {});
+}
+
+SafetensorsFile::~SafetensorsFile() { hgk_st_close(f_); }
+
+std::vector<std::string> SafetensorsFile::keys() const {
+  std::vector<std::string> out;
+  const int64_t n = hgk_st_count(f_);
+  for (int64_t i = 0; i < n; ++i) {
+    const char* name = nullptr;
+    check(hgk_st_tensor(f_, i, &name, nullptr, nullptr, nullptr, nullptr, nullptr), "load_safetensors", {});
+    out.emplace_back(name);
+  }
+  return out;
+}
+
+int64_t SafetensorsFile::index(const std::string& name) const {
+  int64_t i = -1;
+  check(hgk_st_find(f_, name.c_str(), &i), "load_safetensors", {});
+  return i;
+}
+
+bool SafetensorsFile::contains(const std::string& name) const {
+  int64_t i = -1;
+  return hgk_st_find(f_, name.c_str(), &i) == HGK_OK;
+}
+
+Shape SafetensorsFile::shape(const std::string& name) const {
+  int nd = 0;
+  int64_t sh[8];
+  check(hgk_st_tensor(f_, index(name), nullptr, nullptr, nullptr, &nd, sh, nullptr), "load_safetensors", {});
+  return Shape(sh, sh + nd);
+}
+
+std::string SafetensorsFile::dtype_name(const std::string& name) const {
+  const char* dn = nullptr;
+  check(hgk_st_tensor(f_, index(name), nullptr, &dn, nullptr, nullptr, nullptr, nullptr), "load_safetensors", {});
+  return dn;
+}
+
+Array SafetensorsFile::load(const std::string& name) const {
+  const int64_t i = index(name);
+  int dt = -1, nd = 0;
+  int64_t sh[8], nbytes = 0;
+  const char* dn = nullptr;
+  check(hgk_st_tensor(f_, i, nullptr, &dn, &dt, &nd, sh, &nbytes), "load_safetensors", {});
+  if (dt < 0)
+    throw Exception(HGK_ERR_UNSUPPORTED, "load_safetensors failed: '" + name + "' is " + dn +
+                                             ", which no kernel here takes [" + path_ + "]");
+  Array a = Array::empty(Shape(sh, sh + nd), static_cast<Dtype>(dt));
+  check(hgk_st_upload(f_, i, a.data(), nbytes, stream_arg()), "load_safetensors", {});
+  return a;
+}
+
+size_t load_quantized_safetensors_weights(std::map<std::string, Array>& params,
+                                          const std::string& model_dir, bool quantized) {
+  size_t loaded = 0;
+  for (const auto& path : collect_safetensors_files(model_dir)) {
+    SafetensorsFile f(path);
+    for (const auto& key : f.keys()) {
+      auto it = params.find(key);
+      if (it == params.end() && quantized) {
+        const auto rk = remap_quantized_key(key);
+        if (rk) it = params.find(*rk);
+      }
+      if (it == params.end()) continue;
+      it->second = f.load(key);
+      ++loaded;
+    }
+  }
+  return loaded;
+}
+
+}  // namespace io
 }  // namespace higgs

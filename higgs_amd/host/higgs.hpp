@@ -22,6 +22,9 @@
 //   add_rms_norm(x, r, norm)                     h = x.add(r); norm(h) (transformer.rs:413-415)
 //   nn::QuantizedEmbedding{...}.forward(ids)     nn::QuantizedEmbedding (transformer.rs:494)
 //                                                and QEmbedding::forward (qwen3_next.rs:248-257)
+//   io::load_quantized_safetensors_weights(params, dir, quantized)
+//                                                lib.rs:600-632 (with collect_safetensors_files
+//                                                and remap_quantized_key, lib.rs:682-723)
 //
 // Errors are thrown as higgs::Exception, whose message follows the
 // reference's `Exception::custom` convention (qwen3_next.rs:337-361): the
@@ -38,6 +41,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <map>
 #include <memory>
 #include <optional>
 #include <stdexcept>
@@ -234,6 +238,42 @@ struct QuantizedEmbedding {
 Array silu_mul(const Array& gate, const Array& up);
 Array gelu_approximate_mul(const Array& gate, const Array& up);
 }  // namespace nn
+
+// Checkpoint loading (crates/higgs-models/src/lib.rs:574-723): safetensors
+// files in the MLX 4-bit layout, read through the library's reader.
+namespace io {
+// The checkpoint's files: the shards named by model.safetensors.index.json,
+// else model.safetensors; throws (a "MissingWeight" message) when neither exists.
+std::vector<std::string> collect_safetensors_files(const std::string& model_dir);
+// `x.weight` -> `x.inner.weight` (and .scales, .biases, .bias); nullopt otherwise.
+std::optional<std::string> remap_quantized_key(const std::string& key);
+
+class SafetensorsFile {
+ public:
+  explicit SafetensorsFile(const std::string& path);
+  ~SafetensorsFile();
+  SafetensorsFile(const SafetensorsFile&) = delete;
+  SafetensorsFile& operator=(const SafetensorsFile&) = delete;
+  std::vector<std::string> keys() const;  // header order
+  bool contains(const std::string& name) const;
+  Shape shape(const std::string& name) const;
+  std::string dtype_name(const std::string& name) const;  // "BF16", "U32", ...
+  // The tensor on the device (current stream; complete on return). Only the
+  // dtypes of Dtype load this way.
+  Array load(const std::string& name) const;
+
+ private:
+  hgk_st_file* f_ = nullptr;
+  std::string path_;
+  int64_t index(const std::string& name) const;
+};
+
+// load_quantized_safetensors_weights: every checkpoint key that names an
+// entry of `params` (directly, or after remap_quantized_key when `quantized`)
+// replaces that entry. Returns how many were loaded.
+size_t load_quantized_safetensors_weights(std::map<std::string, Array>& params,
+                                          const std::string& model_dir, bool quantized);
+}  // namespace io
 
 Array apply_rope(const Array& x, const nn::Rope& rope, int offset);
 Array apply_rope_batched(const Array& x, const nn::Rope& rope, const Array& offsets);

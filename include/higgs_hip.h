@@ -226,6 +226,48 @@ int hgk_quantized_embedding_rms_norm(const void* ids, int ids_dtype, int64_t n_i
                                      float eps, void* y, int y_dtype, int64_t y_row_stride,
                                      void* stream);
 
+/* ------------------------------------------------------------------------
+ * Checkpoint files: the safetensors files MLX 4-bit checkpoints ship in
+ * (u32-packed `.weight`, bf16/f16 `.scales`/`.biases`, bf16 norm weights).
+ * Replaces Array::load_safetensors as used by load_quantized_safetensors_weights
+ * (crates/higgs-models/src/lib.rs:600-632) and collect_safetensors_files
+ * (lib.rs:682-705). Host-side only: nothing here launches a kernel.
+ * ------------------------------------------------------------------------ */
+typedef struct hgk_st_file hgk_st_file; /* an open, memory-mapped file */
+
+/* Open and validate a safetensors file (header JSON, dtypes, shapes, and
+ * data offsets that tile the byte buffer exactly). */
+int hgk_st_open(const char* path, hgk_st_file** out);
+void hgk_st_close(hgk_st_file* f);
+/* Number of tensors in the file (-1 for a null file). */
+int64_t hgk_st_count(const hgk_st_file* f);
+/* Index of the tensor called `name`; HGK_ERR_ARG if there is none. */
+int hgk_st_find(const hgk_st_file* f, const char* name, int64_t* index);
+/* Tensor `index` in header order: name, the file's dtype string ("BF16",
+ * "U32", ...), its hgk dtype code (-1 for a type the kernels do not take),
+ * rank (<= 8), shape and byte size. The strings live as long as the file.
+ * Any output pointer may be NULL. */
+int hgk_st_tensor(const hgk_st_file* f, int64_t index, const char** name,
+                  const char** dtype_name, int* dtype, int* ndim, int64_t shape[8],
+                  int64_t* nbytes);
+/* Copy tensor `index`'s bytes into host memory. */
+int hgk_st_copy_to_host(const hgk_st_file* f, int64_t index, void* dst, int64_t dst_bytes);
+/* Copy tensor `index`'s bytes to device memory on `stream`, through pinned
+ * staging buffers; the copy has completed when the call returns. */
+int hgk_st_upload(const hgk_st_file* f, int64_t index, void* dst, int64_t dst_bytes,
+                  void* stream);
+/* The checkpoint's files: the distinct shard files named by
+ * model.safetensors.index.json (sorted), else model.safetensors, else
+ * HGK_ERR_ARG with a "MissingWeight" message (lib.rs:682-705). Writes the
+ * paths, each followed by a newline, NUL-terminated, into out (cap bytes);
+ * the size needed is stored in *needed (out may be NULL to query it). */
+int hgk_st_collect_files(const char* model_dir, char* out, int64_t cap, int64_t* needed);
+/* The reference's remap_quantized_key (lib.rs:709-723): `x.weight` ->
+ * `x.inner.weight`, and likewise `.scales`, `.biases`, `.bias`. Returns 0 and
+ * writes the new key, or HGK_ERR_UNSUPPORTED (2) with an empty string when
+ * the key has no quantized form. */
+int hgk_remap_quantized_key(const char* key, char* out, int64_t cap);
+
 #ifdef __cplusplus
 }
 #endif

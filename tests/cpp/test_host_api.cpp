@@ -14,8 +14,11 @@
 #include <cstdlib>
 #include <cstring>
 #include <functional>
+#include <map>
 #include <string>
 #include <vector>
+
+#include <unistd.h>
 
 #include "higgs.hpp"
 
@@ -498,6 +501,109 @@ TEST(test_quantized_embedding_forward_rms_norm) {
   for (int64_t i = 0; i < T * H; ++i)
     ASSERT(std::memcmp(&got_y[i], &want_y[i], 4) == 0, "y at %lld: %.9g vs %.9g", (long long)i,
            got_y[i], want_y[i]);
+}
+
+// ---------------------------------------------------------------- checkpoints
+// A safetensors file written byte by byte: an 8-byte little-endian header
+// length, the JSON header, then the tensors' bytes in header order.
+struct StTensorSpec {
+  std::string name, dtype;
+  Shape shape;
+  std::vector<unsigned char> bytes;
+};
+template <class T>
+StTensorSpec st_tensor(const std::string& name, const std::string& dtype, const Shape& shape,
+                       const std::vector<T>& v) {
+  StTensorSpec t{name, dtype, shape, {}};
+  t.bytes.resize(v.size() * sizeof(T));
+  std::memcpy(t.bytes.data(), v.data(), t.bytes.size());
+  return t;
+}
+void write_safetensors(const std::string& path, const std::vector<StTensorSpec>& ts) {
+  std::string h = "{\"__metadata__\":{\"format\":\"mlx\"}";
+  size_t off = 0;
+  for (const auto& t : ts) {
+    h += ",\"" + t.name + "\":{\"dtype\":\"" + t.dtype + "\",\"shape\":[";
+    for (size_t i = 0; i < t.shape.size(); ++i) h += (i ? "," : "") + std::to_string(t.shape[i]);
+    h += "],\"data_offsets\":[" + std::to_string(off) + "," + std::to_string(off + t.bytes.size()) + "]}";
+    off += t.bytes.size();
+  }
+  h += "}";
+  FILE* f = std::fopen(path.c_str(), "wb");
+  if (!f) throw Failure{"cannot write " + path};
+  const uint64_t n = h.size();
+  unsigned char len[8];
+  for (int i = 0; i < 8; ++i) len[i] = (unsigned char)(n >> (8 * i));
+  std::fwrite(len, 1, 8, f);
+  std::fwrite(h.data(), 1, h.size(), f);
+  for (const auto& t : ts) std::fwrite(t.bytes.data(), 1, t.bytes.size(), f);
+  std::fclose(f);
+}
+
+// load_quantized_safetensors_weights (lib.rs:600-632) over a sharded MLX
+// checkpoint: flat keys land on the `.inner.` parameter names, and the loaded
+// tensors drive the embedding + first norm bit-exactly.
+TEST(test_load_quantized_checkpoint_drives_embedding_and_norm) {
+  const int64_t V = 2048, H = 1024, G = 64, T = 200;
+  char tmpl[] = "/tmp/higgs_ckpt_XXXXXX";
+  const char* dir = mkdtemp(tmpl);
+  ASSERT(dir != nullptr, "mkdtemp");
+  std::vector<uint32_t> wq(V * H / 8);
+  or_fill_u32(9300, wq.data(), static_cast<int64_t>(wq.size()));
+  auto sb = bits_of(uniform(9301, V * H / G, 0.005f, 0.02f), OR_BF16);
+  auto bb = bits_of(uniform(9302, V * H / G, -0.1f, 0.1f), OR_BF16);
+  auto lb = bits_of(normal(9303, H, 1.0f, 0.02f), OR_BF16);
+  const std::string d = dir;
+  write_safetensors(d + "/model-00001-of-00002.safetensors",
+                    {st_tensor("model.embed_tokens.weight", "U32", {V, H / 8}, wq),
+                     st_tensor("model.embed_tokens.scales", "BF16", {V, H / G}, sb),
+                     st_tensor("model.embed_tokens.biases", "BF16", {V, H / G}, bb)});
+  write_safetensors(d + "/model-00002-of-00002.safetensors",
+                    {st_tensor("model.layers.0.input_layernorm.weight", "BF16", {H}, lb)});
+  FILE* idx = std::fopen((d + "/model.safetensors.index.json").c_str(), "w");
+  std::fprintf(idx, "{\"metadata\": {}, \"weight_map\": {"
+                    "\"model.embed_tokens.weight\": \"model-00001-of-00002.safetensors\", "
+                    "\"model.embed_tokens.scales\": \"model-00001-of-00002.safetensors\", "
+                    "\"model.embed_tokens.biases\": \"model-00001-of-00002.safetensors\", "
+                    "\"model.layers.0.input_layernorm.weight\": \"model-00002-of-00002.safetensors\"}}");
+  std::fclose(idx);
+
+  auto files = higgs::io::collect_safetensors_files(d);
+  ASSERT(files.size() == 2, "%zu files", files.size());
+  std::map<std::string, Array> params = {{"model.embed_tokens.inner.weight", Array()},
+                                         {"model.embed_tokens.inner.scales", Array()},
+                                         {"model.embed_tokens.inner.biases", Array()},
+                                         {"model.layers.0.input_layernorm.weight", Array()}};
+  const size_t n = higgs::io::load_quantized_safetensors_weights(params, d, true);
+  ASSERT(n == 4, "loaded %zu", n);
+  higgs::nn::QuantizedEmbedding emb{params["model.embed_tokens.inner.weight"],
+                                    params["model.embed_tokens.inner.scales"],
+                                    params["model.embed_tokens.inner.biases"], 64, 4};
+  higgs::nn::RmsNorm norm{params["model.layers.0.input_layernorm.weight"], 1e-5f};
+  std::vector<uint32_t> ids(T);
+  or_fill_ids(9304, static_cast<uint32_t>(V), ids.data(), T);
+  auto hy = emb.forward_rms_norm(Array::from_slice(ids, {T}), norm);
+  std::vector<uint16_t> want_h(T * H), want_y(T * H);
+  ASSERT(or_qembed(ids.data(), OR_U32, T, wq.data(), sb.data(), bb.data(), OR_BF16, V, H, 64, 4, 0.0f,
+                   want_h.data()) == 0, "oracle embed");
+  ASSERT(or_rms_norm(want_h.data(), OR_BF16, H, lb.data(), OR_BF16, 0, 1e-5f, want_y.data(), OR_BF16, H, T,
+                     H) == 0, "oracle norm");
+  auto got_h = hy.first.to_bits();
+  auto got_y = hy.second.to_bits();
+  ASSERT_BITS_EQ(got_h, want_h);
+  ASSERT_BITS_EQ(got_y, want_y);
+  ASSERT(higgs::io::remap_quantized_key("model.norm.weight").value_or("") == "model.norm.inner.weight", "remap");
+  ASSERT(!higgs::io::remap_quantized_key("lm_head").has_value(), "remap none");
+  bool threw = false;
+  try {
+    higgs::io::collect_safetensors_files(d + "/nope");
+  } catch (const higgs::Exception& e) {
+    threw = std::string(e.what()).find("MissingWeight") != std::string::npos;
+  }
+  ASSERT(threw, "a missing checkpoint must throw MissingWeight");
+  for (const auto& f : files) std::remove(f.c_str());
+  std::remove((d + "/model.safetensors.index.json").c_str());
+  rmdir(dir);
 }
 
 // ---------------------------------------------------------------- empty inputs

@@ -24,6 +24,7 @@ EXPECTED = {
     "test_empty_inputs_give_empty_results", "test_errors_name_the_op_and_operands",
     "test_ops_run_on_the_scoped_stream", "test_add_rms_norm_block_boundaries",
     "test_quantized_embedding_forward_rms_norm",
+    "test_load_quantized_checkpoint_drives_embedding_and_norm",
 }
 
 
