@@ -107,6 +107,14 @@ class Ctx:
         bi = (torch.rand((V, Hd // group), device=self.dev, generator=self.gen) * 0.2 - 0.1)
         return wq, sc.to(torch.bfloat16), bi.to(torch.bfloat16)
 
+    def qtable_experts(self, E, N, K, group=64):
+        torch = self.torch
+        wq = torch.randint(0, 2 ** 32, (E, N, K // 8), dtype=torch.int64, device=self.dev,
+                           generator=self.gen).to(torch.int32)
+        sc = (torch.rand((E, N, K // group), device=self.dev, generator=self.gen) * 0.015 + 0.005)
+        bi = (torch.rand((E, N, K // group), device=self.dev, generator=self.gen) * 0.2 - 0.1)
+        return wq, sc.to(torch.bfloat16), bi.to(torch.bfloat16)
+
     def ids(self, n, V):
         return self.torch.randint(0, V, (n,), dtype=self.torch.int32, device=self.dev,
                                   generator=self.gen)
@@ -278,6 +286,76 @@ def wl_block_boundary(cx):
     return Workload("block_boundary_add_rms_norm", cfg, ks, tot, 4096 + 16384)
 
 
+def k_qmm(cx, name, sets, tab, E, N, K, T, top_k, x_div, group=64):
+    """Routed gather_qmm over (token, expert) pairs; bytes = the distinct
+    experts' weights (each read once) + x + y + the routing arrays."""
+    wq, sc, bi = tab
+    P = T * top_k
+    per_expert = N * K // 2 + 2 * N * (K // group) * 2
+    uniq = sum(len(set(st[1].tolist())) for st in sets) / len(sets)
+    x_rows = P // x_div
+    nbytes = int(uniq * per_expert) + x_rows * K * 2 + P * N * 2 + P * 8 + (E + 2) * 4
+    args = [(BF16, _vp(x), x_rows, K, x_div, None, _vp(wq), _vp(sc), _vp(bi), BF16, E, N, K,
+             group, 4, _vp(exd), I32, P, _vp(order), _vp(seg), _vp(y), N, cx.stream)
+            for x, ex, exd, order, seg, y in sets]
+    return Kernel(name, nbytes, cx.lib.hgk_gather_qmm_routed, args, T, keep=(sets, tab),
+                  cpu=("qmm", dict(E=E, N=N, K=K, group=group, x_div=x_div)))
+
+
+def k_route(cx, name, sets, E, T, top_k):
+    P = T * top_k
+    nbytes = P * 4 + P * 4 + (E + 2) * 4
+    args = [(_vp(exd), I32, P, E, _vp(order), _vp(seg), cx.stream) for exd, order, seg in sets]
+    return Kernel(name, nbytes, cx.lib.hgk_moe_route, args, T, keep=(sets,))
+
+
+def wl_qwen3_next_moe_decode(cx):
+    """Qwen3-Next-80B-A3B routed experts for one decode step of 64 sequences:
+    top-10 of 512 experts; pairs grouped by expert, gate and up (512 x 2048)
+    gather_qmm, SwiGLU, down (2048 x 512) gather_qmm, 4-bit group-64 weights;
+    two layers' expert tables (~1.8 GB) alternate so the weights stream from
+    HBM."""
+    torch = cx.torch
+    T, top_k, E, D, I = 64, 10, 512, 2048, 512
+    P = T * top_k
+    layers = 2
+    tabs = []
+    for _ in range(layers):
+        tabs.append({nm: cx.qtable_experts(E, N, K) for nm, N, K in
+                     (("gate", I, D), ("up", I, D), ("down", D, I))})
+    ns = 8
+    g = torch.Generator().manual_seed(5)
+    exs = [torch.stack([torch.randperm(E, generator=g)[:top_k] for _ in range(T)]).reshape(-1)
+           .to(torch.int32) for _ in range(ns)]
+    xs = [cx.randn((T, D), torch.bfloat16) for _ in range(ns)]
+    exd = [ex.to(cx.dev) for ex in exs]
+    routes = [(torch.empty(P, dtype=torch.int32, device=cx.dev),
+               torch.empty(E + 2, dtype=torch.int32, device=cx.dev)) for _ in range(ns)]
+    ks, outs = [k_route(cx, "moe_route", [(exd[si], *routes[si]) for si in range(ns)], E, T,
+                        top_k)], {}
+    for nm, N, K, xdiv in (("gate", I, D, top_k), ("up", I, D, top_k), ("down", D, I, 1)):
+        outs[nm] = [cx.empty((P, N), torch.bfloat16) for _ in range(ns)]
+        # buffer set si uses layer si % layers's expert tables
+        per_set = []
+        for si in range(ns):
+            x = xs[si] if nm != "down" else cx.randn((P, I), torch.bfloat16)
+            st = (x, exs[si], exd[si], routes[si][0], routes[si][1], outs[nm][si])
+            per_set.append(k_qmm(cx, f"qmm_{nm}", [st], tabs[si % layers][nm], E, N, K, T,
+                                 top_k, xdiv))
+        k = per_set[0]
+        k.argsets = [kk.argsets[0] for kk in per_set]
+        k.bytes = sum(kk.bytes for kk in per_set) // ns
+        k.keep = tuple(kk.keep for kk in per_set)
+        ks.append(k)
+    act = [(outs["gate"][si], outs["up"][si], cx.empty((P, I), torch.bfloat16))
+           for si in range(ns)]
+    ks.insert(3, k_glu(cx, "swiglu_moe", act, P, I, SILU))
+    cfg = {"workload": "qwen3-next-80b-a3b routed experts, one decode step", "sequences": T,
+           "experts": E, "top_k": top_k, "hidden": D, "expert_dim": I, "quant": "4-bit g64",
+           "expert_tables": layers, "buffer_sets": ns}
+    return Workload("qwen3_next_moe_decode", cfg, ks, ns, T)
+
+
 def wl_rmsnorm_512(cx):
     torch = cx.torch
     rows, n = 512, 2048
@@ -390,6 +468,7 @@ WORKLOADS = {
     "qwen3_next_decode": wl_qwen3_next_decode,
     "llama32_1b_chain_fused": wl_llama_chain_fused,
     "block_boundary_add_rms_norm": wl_block_boundary,
+    "qwen3_next_moe_decode": wl_qwen3_next_moe_decode,
 }
 
 
@@ -678,6 +757,18 @@ def cpu_op(spec, budget_s=1.0):
                                        out_scale=p["scale"])
         nbytes = T * (H // 2 + 4 * (H // G) + 4 + 4 * H) + 2 * H
         rows, what = T, f"{T} of {p['n']} ids (full {V}x{H} table)"
+    elif kind == "qmm":
+        E, N, K, G = p["E"], p["N"], p["K"], p["group"]
+        Pn = 16
+        Es = min(E, 16)
+        x = O.from_f32(O.normal(7024, (Pn, K)), B16)
+        wq = O.u32(7025, (Es, N, K // 8))
+        sc = O.from_f32(O.uniform(7026, (Es, N, K // G), 0.005, 0.02), B16)
+        bi = O.from_f32(O.uniform(7027, (Es, N, K // G), -0.1, 0.1), B16)
+        ex = np.arange(Pn, dtype=np.int32) % Es
+        fn = lambda: O.gather_qmm(x, B16, wq, sc, bi, B16, ex, group=G)
+        nbytes = Pn * (N * K // 2 + 4 * N * (K // G) + 2 * K + 2 * N)
+        rows, what = Pn, f"{Pn} (token, expert) pairs, distinct experts"
     else:
         raise ValueError(kind)
     fn()

@@ -1,0 +1,380 @@
+// qmm.hip -- gather_qmm for 4-bit affine weights (MLX layout) on gfx950: the
+// MoE expert projections of crates/higgs-models/src/qwen3_next.rs:294-363,
+// 844-904 (SwitchMlpWeights::forward_gather), where every (token, expert)
+// pair multiplies one activation row by one expert's weight matrix:
+//
+//   y[p, n] = sum_k x[row(p), k] * (s[e_p, n, k/g] * q[e_p, n, k] + b[e_p, n, k/g])
+//
+// with w [E, N, K/8] u32 (8 codes per word, low nibble first), scales and
+// biases [E, N, K/g], row(p) = p / x_row_div (or lhs[p]), e_p = experts[p].
+// This is transpose=true (weights stored row-major as [N, K]); M = 1 per pair,
+// as forward_gather calls it.
+//
+// Per pair the weights are read once (decode: ~one token per expert, so the
+// kernel is bound by the 4-bit weight stream). The arithmetic avoids a full
+// dequantization: a code q becomes the bf16 value 128 + q with two bit
+// operations (0x4300 | q), v_dot2c_f32_bf16 accumulates x * (128 + q) in f32
+// two codes at a time, and per half-group (32 codes) the affine part is
+//   s * (sum x*(128+q) - 128 * sum x) + b * sum x
+// with the half-group sums of x computed once per block into LDS.
+//
+// Routed form: hgk_moe_route sorts the pairs by expert; run in that order,
+// the pairs of one expert follow each other on the same XCDs, so an expert's
+// weights cross HBM about once however many of the step's tokens chose it.
+#include "../../include/higgs_hip.h"
+#include "hgk_common.h"
+#include "hgk_host.h"
+
+namespace hgk {
+
+struct QmmArgs {
+  const void* x;
+  int64_t xrows;    // rows of x; a pair whose row falls outside gets a zero row
+  int64_t xs;       // x row stride (elements)
+  int64_t xdiv;     // pair p reads x row p / xdiv (when lhs is null)
+  const int32_t* lhs;
+  const uint32_t* w;
+  const void* sc;
+  const void* bi;
+  const void* experts;
+  int experts_i32;
+  int64_t E, N, K;
+  int group;
+  int64_t pairs;
+  void* y;
+  int64_t ys;
+};
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+__device__ inline float dot2_bf16(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                         __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+
+__device__ inline int64_t pair_expert(const QmmArgs& a, int64_t p) {
+  if (a.experts_i32) {
+    const int64_t e = reinterpret_cast<const int32_t*>(a.experts)[p];
+    return e < 0 ? e + a.E : e;
+  }
+  return (int64_t)reinterpret_cast<const uint32_t*>(a.experts)[p];
+}
+
+// x row of pair p, or -1 when it is outside x (pairs < 2^16, so the
+// division is done in 32 bits)
+__device__ inline int64_t pair_row(const QmmArgs& a, int64_t p) {
+  int64_t r = a.lhs ? (int64_t)a.lhs[p] : (int64_t)((uint32_t)p / (uint32_t)a.xdiv);
+  if (a.lhs && r < 0) r += a.xrows;
+  return (r >= 0 && r < a.xrows) ? r : -1;
+}
+
+// bf16 x: one block = one pair x 64 output rows (4 waves x 16 rows); a row
+// is split over 4 lanes, lane j reading 16 bytes (32 codes) per step of 128
+// codes, so a wave's load covers 16 rows x 64 contiguous bytes. STEPS = K/128.
+// The x row is staged in LDS permuted to the code order of a word (codes 0..7
+// of a word pair as (0,4) (1,5) (2,6) (3,7)), with its half-group sums.
+// With `order` (pairs grouped by expert), block row y runs pair order[y]:
+// the pairs of one expert run back to back, and since a block's XCD is its
+// linear id modulo 8 and the grid has a multiple of 8 column tiles (or one
+// row of them), the second pair of an expert finds its weight tile in the
+// same XCD's L2 instead of HBM.
+template <class S, int STEPS>
+__global__ __launch_bounds__(256) void qmv_bf16_kernel(QmmArgs a, const int32_t* order) {
+  constexpr int K = STEPS * 128;
+  __shared__ __attribute__((aligned(16))) uint32_t xs_perm[K / 2];  // bf16 pairs in dot order
+  __shared__ float hsum[K / 32];       // sum of x over each 32-code half group
+  const int64_t p = order ? (int64_t)order[blockIdx.y] : (int64_t)blockIdx.y;
+  const int64_t e = pair_expert(a, p);
+  const int64_t xr0 = pair_row(a, p);
+  const bool valid = e >= 0 && e < a.E && xr0 >= 0;
+  const int64_t xr = xr0 >= 0 ? xr0 : 0;
+  const uint16_t* xrow = reinterpret_cast<const uint16_t*>(a.x) + xr * a.xs;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int r = lane >> 2, j = lane & 3;
+  const int64_t n = (int64_t)blockIdx.x * 64 + wave * 16 + r;
+  const bool live = n < a.N && valid;
+  const int64_t nc = n < a.N ? n : a.N - 1;
+  const int64_t ec = valid ? e : 0;
+  const uint32_t* wrow = a.w + (ec * a.N + nc) * (K / 8);
+  const int gpr = K / a.group;
+  const uint16_t* srow = reinterpret_cast<const uint16_t*>(a.sc) + (ec * a.N + nc) * gpr;
+  const uint16_t* brow = reinterpret_cast<const uint16_t*>(a.bi) + (ec * a.N + nc) * gpr;
+
+  // the weight stream goes out first; x is staged while it is in flight (a
+  // barrier orders memory operations, so loads issued after the staging
+  // barriers would wait for it)
+  u32x4 codes[STEPS];
+  uint32_t sraw[STEPS], braw[STEPS];
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s) {
+    codes[s] = *reinterpret_cast<const u32x4*>(wrow + s * 16 + j * 4);
+    const int g = (s * 128 + j * 32) / a.group;
+    sraw[s] = srow[g];
+    braw[s] = brow[g];
+  }
+
+  // stage x: thread t handles one word's worth (8 elements) of the row
+  for (int wd = threadIdx.x; wd < K / 8; wd += 256) {
+    const u32x4 v = *reinterpret_cast<const u32x4*>(xrow + wd * 8);
+    // elements 0..7 as lo/hi halves of v[0..3]: e0=v0.lo e1=v0.hi e2=v1.lo ...
+    // dot order pairs (e0,e4) (e1,e5) (e2,e6) (e3,e7)
+    xs_perm[wd * 4 + 0] = (v[0] & 0xffffu) | (v[2] << 16);
+    xs_perm[wd * 4 + 1] = (v[0] >> 16) | (v[2] & 0xffff0000u);
+    xs_perm[wd * 4 + 2] = (v[1] & 0xffffu) | (v[3] << 16);
+    xs_perm[wd * 4 + 3] = (v[1] >> 16) | (v[3] & 0xffff0000u);
+  }
+  __syncthreads();
+  for (int h = threadIdx.x; h < K / 32; h += 256) {
+    float sacc = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) sacc = dot2_bf16(xs_perm[h * 16 + q], 0x3f803f80u, sacc);
+    hsum[h] = sacc;
+  }
+  __syncthreads();
+  float acc = 0.0f;
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s) {
+    const int h = s * 4 + j;  // half group index
+    const u32x4 xq0 = *reinterpret_cast<const u32x4*>(&xs_perm[h * 16 + 0]);
+    const u32x4 xq1 = *reinterpret_cast<const u32x4*>(&xs_perm[h * 16 + 4]);
+    const u32x4 xq2 = *reinterpret_cast<const u32x4*>(&xs_perm[h * 16 + 8]);
+    const u32x4 xq3 = *reinterpret_cast<const u32x4*>(&xs_perm[h * 16 + 12]);
+    const u32x4 xw[4] = {xq0, xq1, xq2, xq3};
+    float d = 0.0f;
+#pragma unroll
+    for (int wi = 0; wi < 4; ++wi) {
+      const uint32_t c = codes[s][wi];
+      // (128 + q_i, 128 + q_{i+4}) as packed bf16, i = 0..3
+      d = dot2_bf16(xw[wi][0], (c & 0x000f000fu) | 0x43004300u, d);
+      d = dot2_bf16(xw[wi][1], ((c >> 4) & 0x000f000fu) | 0x43004300u, d);
+      d = dot2_bf16(xw[wi][2], ((c >> 8) & 0x000f000fu) | 0x43004300u, d);
+      d = dot2_bf16(xw[wi][3], ((c >> 12) & 0x000f000fu) | 0x43004300u, d);
+    }
+    const float hs = hsum[h];
+    const float sv = S::lo(sraw[s]), bv = S::lo(braw[s]);
+    acc = __builtin_fmaf(sv, d - 128.0f * hs, acc);
+    acc = __builtin_fmaf(bv, hs, acc);
+  }
+  // the row's 4 lanes are adjacent: reduce within the quad
+  acc += __shfl_xor(acc, 1, 64);
+  acc += __shfl_xor(acc, 2, 64);
+  if (j == 0 && n < a.N) {
+    const float out = live ? acc : 0.0f;
+    store1<BF16>(a.y, p * a.ys + n, out);
+  }
+}
+
+// Counting sort of pairs by expert in one block: seg[e]..seg[e+1] delimit the
+// pairs of expert e in `order`; the bucket E (seg[E]..seg[E+1]) collects
+// pairs whose expert id is out of range. Order within an expert is the order
+// in which the block's atomics land (each pair's result does not depend on it).
+__global__ __launch_bounds__(1024) void moe_route_kernel(const void* experts, int experts_i32,
+                                                         int pairs, int E, int32_t* order,
+                                                         int32_t* seg) {
+  extern __shared__ int32_t cnt[];  // E + 1 counters, then E + 2 offsets
+  int32_t* off = cnt + (E + 1);
+  for (int i = threadIdx.x; i < E + 1; i += blockDim.x) cnt[i] = 0;
+  __syncthreads();
+  auto bucket = [&](int p) {
+    int64_t e = experts_i32 ? (int64_t)reinterpret_cast<const int32_t*>(experts)[p]
+                            : (int64_t)reinterpret_cast<const uint32_t*>(experts)[p];
+    if (experts_i32 && e < 0) e += E;
+    return (e >= 0 && e < E) ? (int)e : E;
+  };
+  for (int p = threadIdx.x; p < pairs; p += blockDim.x) atomicAdd(&cnt[bucket(p)], 1);
+  __syncthreads();
+  // exclusive scan of the E + 1 counters: each thread sums a chunk, the
+  // 1024 chunk sums are scanned in LDS (Hillis-Steele), then each thread
+  // writes its chunk's offsets
+  __shared__ int32_t part[1024];
+  const int nb = E + 1;
+  const int chunk = (nb + 1023) / 1024;
+  const int c0 = threadIdx.x * chunk, c1 = min(nb, c0 + chunk);
+  int sum = 0;
+  for (int i = c0; i < c1; ++i) sum += cnt[i];
+  part[threadIdx.x] = sum;
+  __syncthreads();
+  for (int d = 1; d < 1024; d <<= 1) {
+    const int v = threadIdx.x >= d ? part[threadIdx.x - d] : 0;
+    __syncthreads();
+    part[threadIdx.x] += v;
+    __syncthreads();
+  }
+  int run = part[threadIdx.x] - sum;  // exclusive prefix of this chunk
+  for (int i = c0; i < c1; ++i) {
+    off[i] = run;
+    run += cnt[i];
+  }
+  if (threadIdx.x == 1023) off[nb] = part[1023];
+  __syncthreads();
+  for (int i = threadIdx.x; i < E + 2; i += blockDim.x) seg[i] = off[i];
+  for (int i = threadIdx.x; i < E + 1; i += blockDim.x) cnt[i] = off[i];
+  __syncthreads();
+  for (int p = threadIdx.x; p < pairs; p += blockDim.x) {
+    const int slot = atomicAdd(&cnt[bucket(p)], 1);
+    order[slot] = p;
+  }
+}
+
+// Any shape / dtype: one wave per (pair, output row), f32 arithmetic with
+// exact dequantized values, element-strided.
+template <class X, class S>
+__global__ __launch_bounds__(256) void qmv_generic_kernel(QmmArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (item >= a.pairs * a.N) return;  // whole wave leaves together
+  const int64_t p = item / a.N, n = item - p * a.N;
+  const int64_t e = pair_expert(a, p);
+  const int64_t xr = pair_row(a, p);
+  float acc = 0.0f;
+  if (e >= 0 && e < a.E && xr >= 0) {
+    const int64_t gpr = a.K / a.group;
+    for (int64_t k = lane; k < a.K; k += 64) {
+      const uint32_t q = (a.w[(e * a.N + n) * (a.K / 8) + k / 8] >> (4 * (k % 8))) & 0xfu;
+      const int64_t g = (e * a.N + n) * gpr + k / a.group;
+      const float wv = load1<S>(a.sc, g) * (float)q + load1<S>(a.bi, g);
+      acc = __builtin_fmaf(load1<X>(a.x, xr * a.xs + k), wv, acc);
+    }
+  }
+  acc = group_sum<64>(acc);
+  if (lane == 0) store1<X>(a.y, p * a.ys + n, acc);
+}
+
+namespace {
+
+template <class S>
+bool launch_bf16(const QmmArgs& a, const int32_t* order, hipStream_t s) {
+  const dim3 grid((unsigned)((a.N + 63) / 64), (unsigned)a.pairs);
+  switch (a.K) {
+    case 512: hipLaunchKernelGGL((qmv_bf16_kernel<S, 4>), grid, dim3(256), 0, s, a, order); return true;
+    case 1024: hipLaunchKernelGGL((qmv_bf16_kernel<S, 8>), grid, dim3(256), 0, s, a, order); return true;
+    case 2048: hipLaunchKernelGGL((qmv_bf16_kernel<S, 16>), grid, dim3(256), 0, s, a, order); return true;
+    case 4096: hipLaunchKernelGGL((qmv_bf16_kernel<S, 32>), grid, dim3(256), 0, s, a, order); return true;
+    default: return false;
+  }
+}
+
+template <class X, class S>
+void launch_generic(const QmmArgs& a, hipStream_t s) {
+  const int64_t items = a.pairs * a.N;
+  hipLaunchKernelGGL((qmv_generic_kernel<X, S>), dim3((unsigned)((items + 3) / 4)), dim3(256), 0, s, a);
+}
+
+}  // namespace
+}  // namespace hgk
+
+using namespace hgk;
+
+extern "C" int hgk_gather_qmm(int dtype, const void* x, int64_t x_rows, int64_t x_row_stride,
+                              int64_t x_row_div,
+                              const int32_t* lhs_indices, const uint32_t* w, const void* scales,
+                              const void* biases, int scales_dtype, int64_t n_experts, int64_t n,
+                              int64_t k, int group_size, int bits, const void* rhs_indices,
+                              int rhs_dtype, int64_t pairs, void* y, int64_t y_row_stride,
+                              void* stream) {
+  clear_error();
+  const char* fn = "hgk_gather_qmm";
+  if (bits != 4) return fail(HGK_ERR_UNSUPPORTED, "%s: bits=%d (only 4 is implemented)", fn, bits);
+  if (group_size != 32 && group_size != 64 && group_size != 128)
+    return fail(HGK_ERR_UNSUPPORTED, "%s: group_size=%d (32, 64 or 128)", fn, group_size);
+  if (dtype != DT_BF16 && dtype != DT_F16)
+    return fail(HGK_ERR_UNSUPPORTED, "%s: activation dtype must be bf16 or f16", fn);
+  if (scales_dtype != dtype)
+    return fail(HGK_ERR_UNSUPPORTED, "%s: scales/biases must have the activation dtype", fn);
+  if (rhs_dtype != DT_I32 && rhs_dtype != DT_U32)
+    return fail(HGK_ERR_ARG, "%s: expert indices must be int32 or uint32", fn);
+  if (pairs < 0 || n_experts <= 0 || n <= 0 || k <= 0 || k % group_size || k % 8)
+    return fail(HGK_ERR_ARG, "%s: bad shape pairs=%lld E=%lld N=%lld K=%lld (K a multiple of %d)", fn,
+                (long long)pairs, (long long)n_experts, (long long)n, (long long)k, group_size);
+  if (!lhs_indices && x_row_div <= 0) return fail(HGK_ERR_ARG, "%s: x_row_div must be >= 1", fn);
+  if (x_rows <= 0 || (!lhs_indices && (pairs - 1) / (x_row_div > 0 ? x_row_div : 1) >= x_rows))
+    return fail(HGK_ERR_ARG, "%s: %lld pairs with x_row_div %lld need more than %lld rows of x", fn,
+                (long long)pairs, (long long)x_row_div, (long long)x_rows);
+  if ((x_rows > 1 && x_row_stride < k) || (pairs > 1 && y_row_stride < n))
+    return fail(HGK_ERR_ARG, "%s: row strides (%lld, %lld) smaller than K=%lld / N=%lld", fn,
+                (long long)x_row_stride, (long long)y_row_stride, (long long)k, (long long)n);
+  if (!x || !w || !scales || !biases || !rhs_indices || !y) return fail(HGK_ERR_ARG, "%s: null pointer", fn);
+  if (pairs > 65535 || n_experts * n * k >= ((int64_t)1 << 42))
+    return fail(HGK_ERR_UNSUPPORTED, "%s: problem too large (pairs <= 65535)", fn);
+  if (pairs == 0) return HGK_OK;
+  QmmArgs a{};
+  a.x = x; a.xrows = x_rows; a.xs = x_row_stride; a.xdiv = x_row_div > 0 ? x_row_div : 1; a.lhs = lhs_indices;
+  a.w = w; a.sc = scales; a.bi = biases; a.experts = rhs_indices; a.experts_i32 = rhs_dtype == DT_I32;
+  a.E = n_experts; a.N = n; a.K = k; a.group = group_size; a.pairs = pairs; a.y = y;
+  a.ys = y_row_stride;
+  const hipStream_t s = as_stream(stream);
+  const bool vec_ok = dtype == DT_BF16 && aligned16(x) && x_row_stride % 8 == 0 && aligned16(w) &&
+                      (reinterpret_cast<uintptr_t>(scales) & 1) == 0;
+  if (vec_ok && launch_bf16<BF16>(a, nullptr, s)) return launch_status(fn);
+  if (dtype == DT_BF16) launch_generic<BF16, BF16>(a, s);
+  else launch_generic<F16, F16>(a, s);
+  return launch_status(fn);
+}
+
+namespace hgk {
+namespace {
+
+}  // namespace
+}  // namespace hgk
+
+extern "C" int hgk_moe_route(const void* rhs_indices, int rhs_dtype, int64_t pairs,
+                             int64_t n_experts, int32_t* order, int32_t* expert_offsets,
+                             void* stream) {
+  clear_error();
+  const char* fn = "hgk_moe_route";
+  if (rhs_dtype != DT_I32 && rhs_dtype != DT_U32)
+    return fail(HGK_ERR_ARG, "%s: expert indices must be int32 or uint32", fn);
+  if (pairs < 0 || pairs > 65535 || n_experts <= 0 || n_experts > 8192)
+    return fail(HGK_ERR_ARG, "%s: pairs=%lld (<= 65535) and n_experts=%lld (1..8192)", fn,
+                (long long)pairs, (long long)n_experts);
+  if (!order || !expert_offsets || (pairs > 0 && !rhs_indices)) return fail(HGK_ERR_ARG, "%s: null pointer", fn);
+  const size_t shmem = (size_t)(2 * n_experts + 3) * sizeof(int32_t);
+  hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(1024), shmem, as_stream(stream), rhs_indices,
+                     rhs_dtype == DT_I32 ? 1 : 0, (int)pairs, (int)n_experts, order, expert_offsets);
+  return launch_status(fn);
+}
+
+extern "C" int hgk_gather_qmm_routed(int dtype, const void* x, int64_t x_rows, int64_t x_row_stride,
+                                     int64_t x_row_div, const int32_t* lhs_indices, const uint32_t* w,
+                                     const void* scales, const void* biases, int scales_dtype,
+                                     int64_t n_experts, int64_t n, int64_t k, int group_size, int bits,
+                                     const void* rhs_indices, int rhs_dtype, int64_t pairs,
+                                     const int32_t* order, const int32_t* expert_offsets, void* y,
+                                     int64_t y_row_stride, void* stream) {
+  clear_error();
+  const char* fn = "hgk_gather_qmm_routed";
+  if (!order || !expert_offsets) return fail(HGK_ERR_ARG, "%s: null order / expert_offsets", fn);
+  (void)expert_offsets;  // the grouping is carried by `order`
+  if (n_experts > 8192) return fail(HGK_ERR_UNSUPPORTED, "%s: n_experts > 8192", fn);
+  const bool vec = dtype == DT_BF16 && scales_dtype == DT_BF16 && bits == 4 &&
+                   (group_size == 32 || group_size == 64 || group_size == 128) &&
+                   (k == 512 || k == 1024 || k == 2048 || k == 4096) && aligned16(x) &&
+                   x_row_stride % 8 == 0 && aligned16(w) &&
+                   (reinterpret_cast<uintptr_t>(scales) & 1) == 0;
+  if (!vec)  // the per-pair kernel takes every other case
+    return hgk_gather_qmm(dtype, x, x_rows, x_row_stride, x_row_div, lhs_indices, w, scales, biases,
+                          scales_dtype, n_experts, n, k, group_size, bits, rhs_indices, rhs_dtype,
+                          pairs, y, y_row_stride, stream);
+  // validate exactly as the per-pair entry point does
+  if (pairs < 0 || n_experts <= 0 || n <= 0 || k % group_size)
+    return fail(HGK_ERR_ARG, "%s: bad shape", fn);
+  if (!lhs_indices && x_row_div <= 0) return fail(HGK_ERR_ARG, "%s: x_row_div must be >= 1", fn);
+  if (x_rows <= 0 || (!lhs_indices && pairs > 0 && (pairs - 1) / x_row_div >= x_rows))
+    return fail(HGK_ERR_ARG, "%s: too few rows of x", fn);
+  if ((x_rows > 1 && x_row_stride < k) || (pairs > 1 && y_row_stride < n))
+    return fail(HGK_ERR_ARG, "%s: row strides smaller than K / N", fn);
+  if (!x || !w || !scales || !biases || !y || (pairs > 0 && !rhs_indices))
+    return fail(HGK_ERR_ARG, "%s: null pointer", fn);
+  if (pairs > 65535 || n_experts * n * k >= ((int64_t)1 << 42))
+    return fail(HGK_ERR_UNSUPPORTED, "%s: problem too large (pairs <= 65535)", fn);
+  if (pairs == 0) return HGK_OK;
+  QmmArgs a{};
+  a.x = x; a.xrows = x_rows; a.xs = x_row_stride; a.xdiv = x_row_div > 0 ? x_row_div : 1;
+  a.lhs = lhs_indices; a.w = w; a.sc = scales; a.bi = biases; a.experts = rhs_indices;
+  a.experts_i32 = rhs_dtype == DT_I32; a.E = n_experts; a.N = n; a.K = k; a.group = group_size;
+  a.pairs = pairs; a.y = y; a.ys = y_row_stride;
+  launch_bf16<BF16>(a, order, as_stream(stream));
+  return launch_status(fn);
+}

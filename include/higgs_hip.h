@@ -226,6 +226,54 @@ int hgk_quantized_embedding_rms_norm(const void* ids, int ids_dtype, int64_t n_i
                                      float eps, void* y, int y_dtype, int64_t y_row_stride,
                                      void* stream);
 
+/*
+ * gather_qmm for 4-bit affine weights in the MLX layout, transpose = true,
+ * one activation row per (token, expert) pair -- the MoE expert projections
+ * of SwitchMlpWeights::forward_gather (crates/higgs-models/src/qwen3_next.rs:
+ * 844-904), which the reference runs through mlx_gather_qmm (294-363):
+ *   y[p, n] = sum_k x[row(p), k] * (scales[e_p, n, k/g] * q[e_p, n, k] + biases[e_p, n, k/g])
+ * x [x_rows, k] (row stride x_row_stride) in bf16/f16; w [n_experts, n, k/8]
+ * u32 (8 codes per word, low nibble first); scales/biases
+ * [n_experts, n, k/group_size] in x's dtype; e_p = rhs_indices[p] (int32 or
+ * uint32, device); row(p) = lhs_indices[p] when lhs_indices (device int32) is
+ * given, else p / x_row_div (forward_gather's broadcast of one token row over
+ * its top_k experts: x_row_div = top_k for gate/up, 1 for down). y [pairs, n]
+ * in x's dtype, f32 accumulation. Rows or experts out of range give zero
+ * rows. pairs <= 65535.
+ */
+int hgk_gather_qmm(int dtype, const void* x, int64_t x_rows, int64_t x_row_stride,
+                   int64_t x_row_div, const int32_t* lhs_indices, const uint32_t* w,
+                   const void* scales, const void* biases, int scales_dtype, int64_t n_experts,
+                   int64_t n, int64_t k, int group_size, int bits, const void* rhs_indices,
+                   int rhs_dtype, int64_t pairs, void* y, int64_t y_row_stride, void* stream);
+
+/*
+ * Group (token, expert) pairs by expert for hgk_gather_qmm_routed: a counting
+ * sort on the device. order[pairs] receives pair ids grouped by expert;
+ * expert_offsets[n_experts + 2] the group boundaries (expert e's pairs are
+ * order[expert_offsets[e] .. expert_offsets[e+1]); the last group collects
+ * pairs whose expert id is out of range). pairs <= 65535, n_experts <= 8192.
+ * Both outputs are caller-owned device buffers. The same routing serves the
+ * gate, up and down projections of one MoE block.
+ */
+int hgk_moe_route(const void* rhs_indices, int rhs_dtype, int64_t pairs, int64_t n_experts,
+                  int32_t* order, int32_t* expert_offsets, void* stream);
+
+/*
+ * hgk_gather_qmm with the pairs grouped by expert (order / expert_offsets from
+ * hgk_moe_route): each expert's weights are read once for all of its pairs
+ * instead of once per pair. Same arguments and results as hgk_gather_qmm
+ * (bit-identical for the shapes the routed kernel takes: bf16, K in
+ * {512, 1024, 2048}; other shapes run the per-pair kernel).
+ */
+int hgk_gather_qmm_routed(int dtype, const void* x, int64_t x_rows, int64_t x_row_stride,
+                          int64_t x_row_div, const int32_t* lhs_indices, const uint32_t* w,
+                          const void* scales, const void* biases, int scales_dtype,
+                          int64_t n_experts, int64_t n, int64_t k, int group_size, int bits,
+                          const void* rhs_indices, int rhs_dtype, int64_t pairs,
+                          const int32_t* order, const int32_t* expert_offsets, void* y,
+                          int64_t y_row_stride, void* stream);
+
 /* ------------------------------------------------------------------------
  * Checkpoint files: the safetensors files MLX 4-bit checkpoints ship in
  * (u32-packed `.weight`, bf16/f16 `.scales`/`.biases`, bf16 norm weights).

@@ -61,6 +61,8 @@ def lib():
             "or_rms_norm": (_i32, [_vp, _i32, _i64, _vp, _i32, _i32, _f32,
                                    _vp, _i32, _i64, _i64, _i64]),
             "or_add": (_i32, [_i32, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64]),
+            "or_gather_qmm": (_i32, [_i32, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _i32,
+                                     _i64, _i64, _i64, _i32, _vp, _i64, _vp, _i64]),
             "or_rope_inv_freq": (None, [_f32, _i32, _vp, _vp]),
             "or_llama3_freqs": (None, [_f32, _i32, _f32, _f32, _f32, _f32, _vp]),
             "or_norm_rope": (_i32, [_i32, _vp, _vp, _vp, _vp, _i64, _i64, _i64,
@@ -190,6 +192,25 @@ def qembed_rms_norm(ids_arr, wq, scales, biases, s_dt, w, w_dt, eps, *, group=64
     h = qembed(np.ascontiguousarray(ids_arr).reshape(-1), wq, scales, biases, s_dt,
                group=group, bits=bits, out_scale=out_scale)
     return h, rms_norm(h, s_dt, w, w_dt, eps, plus_one=plus_one, out_dt=out_dt)
+
+
+def gather_qmm(x, x_dt, w, scales, biases, s_dt, experts, *, group=64, x_div=1, lhs=None):
+    """SwitchMlpWeights::forward_gather's gather_qmm (qwen3_next.rs:844-904):
+    x [R, K] storage array, w [E, N, K/8] u32, scales/biases [E, N, K/group],
+    experts int32 [P]; pair p uses x row lhs[p] (or p // x_div). Returns
+    y [P, N] in x's dtype: the exact contraction rounded once."""
+    x = np.ascontiguousarray(x)
+    R, K = x.shape
+    E, N, _ = w.shape
+    experts = np.ascontiguousarray(experts, np.int32)
+    P = experts.size
+    y = np.empty((P, N), storage_dtype(x_dt))
+    lhs_arr = None if lhs is None else np.ascontiguousarray(lhs, np.int32)
+    _check(lib().or_gather_qmm(x_dt, _p(x), R, K, x_div, _p(lhs_arr),
+                               _p(np.ascontiguousarray(w, np.uint32)), _p(np.ascontiguousarray(scales)),
+                               _p(np.ascontiguousarray(biases)), s_dt, E, N, K, group,
+                               _p(experts), P, _p(y), N), "gather_qmm")
+    return y
 
 
 def rope_inv_freq(base, dims, freqs=None) -> np.ndarray:

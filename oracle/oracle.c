@@ -448,3 +448,45 @@ int or_qembed(const void* ids, int id_dt, int64_t n_ids, const uint32_t* wq,
   }
   return 0;
 }
+
+/* ------------------------------------------------------------------ */
+/* gather_qmm (4-bit affine, transpose = true, one row per pair)       */
+/* ------------------------------------------------------------------ */
+
+/* y[p, n] = round_dt( sum_k x[row(p), k] * (s * q + b) ), the sum taken in
+ * f64 over exactly dequantized weights (s * q + b is exact in f64 for 16-bit
+ * s, b and 4-bit q), i.e. the mathematical value rounded once. MLX's own
+ * accumulation order and precision for quantized matmul are not restated:
+ * the parity bar for this floating-point contraction is a tolerance.
+ * Call sites: SwitchMlpWeights::forward_gather -> gather_qmm
+ * (crates/higgs-models/src/qwen3_next.rs:844-904, 294-363). row(p) = lhs[p]
+ * when lhs is given, else p / x_div; rows or experts out of range give 0. */
+int or_gather_qmm(int dt, const void* x, int64_t x_rows, int64_t x_rs, int64_t x_div,
+                  const int32_t* lhs, const uint32_t* w, const void* sc, const void* bi,
+                  int s_dt, int64_t E, int64_t N, int64_t K, int group, const int32_t* experts,
+                  int64_t pairs, void* y, int64_t y_rs) {
+  if (!x || !w || !sc || !bi || !experts || !y || K % group || K % 8 || x_div <= 0) return 1;
+  const int64_t gpr = K / group, wpr = K / 8;
+#pragma omp parallel for schedule(static)
+  for (int64_t p = 0; p < pairs; ++p) {
+    int64_t e = experts[p];
+    if (e < 0) e += E;
+    int64_t r = lhs ? (int64_t)lhs[p] : p / x_div;
+    if (lhs && r < 0) r += x_rows;
+    const int ok = e >= 0 && e < E && r >= 0 && r < x_rows;
+    for (int64_t n = 0; n < N; ++n) {
+      double acc = 0.0;
+      if (ok) {
+        const uint32_t* wr = w + (e * N + n) * wpr;
+        for (int64_t k = 0; k < K; ++k) {
+          const uint32_t q = (wr[k / 8] >> (4 * (k % 8))) & 0xfu;
+          const int64_t g = (e * N + n) * gpr + k / group;
+          const double wv = (double)ld(sc, s_dt, g) * (double)q + (double)ld(bi, s_dt, g);
+          acc += (double)ld(x, dt, r * x_rs + k) * wv;
+        }
+      }
+      st(y, dt, p * y_rs + n, rnd((float)acc, dt));
+    }
+  }
+  return 0;
+}

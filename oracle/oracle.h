@@ -115,6 +115,13 @@ int or_qembed(const void* ids, int id_dt, int64_t n_ids,
               int s_dt, int64_t vocab, int64_t hidden, int group, int bits,
               float out_scale, void* out);
 
+/* gather_qmm, 4-bit affine, transpose = true, one x row per pair: the exact
+ * (f64) contraction rounded once to dt. */
+int or_gather_qmm(int dt, const void* x, int64_t x_rows, int64_t x_rs, int64_t x_div,
+                  const int32_t* lhs, const uint32_t* w, const void* sc, const void* bi,
+                  int s_dt, int64_t E, int64_t N, int64_t K, int group, const int32_t* experts,
+                  int64_t pairs, void* y, int64_t y_rs);
+
 #ifdef __cplusplus
 }
 #endif

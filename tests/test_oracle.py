@@ -471,3 +471,82 @@ def test_qembed_rms_norm_constant_row_closed_form():
     assert np.array_equal(h, hq)
     assert np.array_equal(y, O.rms_norm(hq, O.BF16, w, O.BF16, 1e-6))
     assert not y[2].any()
+
+
+# ------------------------------------------------------------------ gather_qmm
+def _qmm_case(key, P, R, E, N, K, group=64, dt=O.BF16):
+    x = O.from_f32(O.normal(key, (R, K)), dt)
+    w = O.u32(key + 1, (E, N, K // 8))
+    s = O.from_f32(O.uniform(key + 2, (E, N, K // group), 0.005, 0.02), dt)
+    b = O.from_f32(O.uniform(key + 3, (E, N, K // group), -0.1, 0.1), dt)
+    ex = (O.u32(key + 4, (P,)) % np.uint32(E)).astype(np.int32)
+    return x, w, s, b, ex
+
+
+def _dequant_f64(w, s, b, dt, group):
+    E, N, W = w.shape
+    q = ((w[..., None] >> (4 * np.arange(8, dtype=np.uint32))) & 0xF).reshape(E, N, W * 8)
+    sf = np.repeat(O.to_f32(s, dt).astype(np.float64), group, axis=-1)
+    bf = np.repeat(O.to_f32(b, dt).astype(np.float64), group, axis=-1)
+    return q.astype(np.float64) * sf + bf
+
+
+def test_gather_qmm_matches_torch_f64_dequant_matmul():
+    """torch f64: dequantize the table, gather each pair's expert, matmul,
+    round once to bf16 -- an independent route to the same number."""
+    P, R, E, N, K, top_k = 40, 4, 6, 96, 512, 10
+    x, w, s, b, ex = _qmm_case(2201, P, R, E, N, K)
+    y = O.gather_qmm(x, O.BF16, w, s, b, O.BF16, ex, x_div=top_k)
+    wd = torch.from_numpy(_dequant_f64(w, s, b, O.BF16, 64))
+    xd = torch.from_numpy(O.to_f32(x, O.BF16).astype(np.float64))
+    rows = torch.arange(P) // top_k
+    ref = torch.einsum("pk,pnk->pn", xd[rows], wd[torch.from_numpy(ex).long()])
+    ref_bits = ref.to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert_close(y, ref_bits, O.BF16, max_ulp=1, what="gather_qmm vs torch f64")
+    assert exact_frac(y, ref_bits, O.BF16) >= 0.999
+
+
+def test_gather_qmm_closed_forms():
+    """Unit scales, zero biases and one-hot x return the raw codes; all-zero
+    codes return sum_g b_g * sum_{k in g} x_k."""
+    E, N, K = 3, 16, 128
+    w = O.u32(2211, (E, N, K // 8))
+    one = O.from_f32(np.ones((E, N, K // 64), np.float32), O.BF16)
+    zero = O.from_f32(np.zeros((E, N, K // 64), np.float32), O.BF16)
+    x = np.zeros((K, K), np.float32)
+    x[np.arange(K), np.arange(K)] = 1.0
+    xb = O.from_f32(x, O.BF16)
+    ex = np.full(K, 2, np.int32)
+    y = O.to_f32(O.gather_qmm(xb, O.BF16, w, one, zero, O.BF16, ex), O.BF16)
+    q = ((w[..., None] >> (4 * np.arange(8, dtype=np.uint32))) & 0xF).reshape(E, N, K)
+    assert np.array_equal(y, q[2].T.astype(np.float32))  # row k of y = codes at k
+    xs = O.from_f32(O.normal(2212, (4, K)), O.BF16)
+    bias = O.from_f32(O.uniform(2213, (E, N, K // 64), -0.1, 0.1), O.BF16)
+    y0 = O.gather_qmm(xs, O.BF16, np.zeros_like(w), one, bias, O.BF16, np.array([0, 1, 2, 0], np.int32))
+    xg = O.to_f32(xs, O.BF16).astype(np.float64).reshape(4, K // 64, 64).sum(-1)
+    bt = O.to_f32(bias, O.BF16).astype(np.float64)
+    ref = np.einsum("pg,png->pn", xg, bt[[0, 1, 2, 0]])
+    assert_close(y0, O.from_f32(ref.astype(np.float32), O.BF16), O.BF16, max_ulp=1,
+                 what="zero codes")
+
+
+def test_gather_qmm_routing_and_out_of_range():
+    """p // x_div routing equals explicit lhs rows; experts and rows out of
+    range give zero rows (negative expert ids wrap once, as int32 indices)."""
+    P, R, E, N, K = 12, 3, 4, 32, 256
+    x, w, s, b, ex = _qmm_case(2221, P, R, E, N, K)
+    y1 = O.gather_qmm(x, O.BF16, w, s, b, O.BF16, ex, x_div=4)
+    y2 = O.gather_qmm(x, O.BF16, w, s, b, O.BF16, ex, lhs=np.arange(P) // 4)
+    assert np.array_equal(y1, y2)
+    bad = ex.copy()
+    bad[[0, 5]] = [E, -1]
+    y3 = O.gather_qmm(x, O.BF16, w, s, b, O.BF16, bad, x_div=4)
+    assert not y3[0].any()
+    wrapped = ex.copy()
+    wrapped[5] = E - 1
+    y4 = O.gather_qmm(x, O.BF16, w, s, b, O.BF16, wrapped, x_div=4)
+    assert np.array_equal(y3[5], y4[5])
+    lhs = np.arange(P) // 4
+    lhs[3] = R
+    y5 = O.gather_qmm(x, O.BF16, w, s, b, O.BF16, ex, lhs=lhs)
+    assert not y5[3].any()
