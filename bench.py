@@ -287,32 +287,24 @@ def wl_block_boundary(cx):
 
 
 def k_qmm(cx, name, sets, tab, E, N, K, T, top_k, x_div, group=64):
-    """Routed gather_qmm over (token, expert) pairs; bytes = the distinct
-    experts' weights (each read once) + x + y + the routing arrays."""
+    """gather_qmm over (token, expert) pairs; bytes = the distinct experts'
+    weights (no credit for re-reads) + x + y + the expert ids."""
     wq, sc, bi = tab
     P = T * top_k
     per_expert = N * K // 2 + 2 * N * (K // group) * 2
     uniq = sum(len(set(st[1].tolist())) for st in sets) / len(sets)
     x_rows = P // x_div
-    nbytes = int(uniq * per_expert) + x_rows * K * 2 + P * N * 2 + P * 8 + (E + 2) * 4
+    nbytes = int(uniq * per_expert) + x_rows * K * 2 + P * N * 2 + P * 4
     args = [(BF16, _vp(x), x_rows, K, x_div, None, _vp(wq), _vp(sc), _vp(bi), BF16, E, N, K,
-             group, 4, _vp(exd), I32, P, _vp(order), _vp(seg), _vp(y), N, cx.stream)
-            for x, ex, exd, order, seg, y in sets]
-    return Kernel(name, nbytes, cx.lib.hgk_gather_qmm_routed, args, T, keep=(sets, tab),
+             group, 4, _vp(exd), I32, P, _vp(y), N, cx.stream) for x, ex, exd, y in sets]
+    return Kernel(name, nbytes, cx.lib.hgk_gather_qmm, args, T, keep=(sets, tab),
                   cpu=("qmm", dict(E=E, N=N, K=K, group=group, x_div=x_div)))
-
-
-def k_route(cx, name, sets, E, T, top_k):
-    P = T * top_k
-    nbytes = P * 4 + P * 4 + (E + 2) * 4
-    args = [(_vp(exd), I32, P, E, _vp(order), _vp(seg), cx.stream) for exd, order, seg in sets]
-    return Kernel(name, nbytes, cx.lib.hgk_moe_route, args, T, keep=(sets,))
 
 
 def wl_qwen3_next_moe_decode(cx):
     """Qwen3-Next-80B-A3B routed experts for one decode step of 64 sequences:
-    top-10 of 512 experts; pairs grouped by expert, gate and up (512 x 2048)
-    gather_qmm, SwiGLU, down (2048 x 512) gather_qmm, 4-bit group-64 weights;
+    top-10 of 512 experts; gate and up (512 x 2048) gather_qmm, SwiGLU, down
+    (2048 x 512) gather_qmm, 4-bit group-64 weights;
     two layers' expert tables (~1.8 GB) alternate so the weights stream from
     HBM."""
     torch = cx.torch
@@ -329,17 +321,14 @@ def wl_qwen3_next_moe_decode(cx):
            .to(torch.int32) for _ in range(ns)]
     xs = [cx.randn((T, D), torch.bfloat16) for _ in range(ns)]
     exd = [ex.to(cx.dev) for ex in exs]
-    routes = [(torch.empty(P, dtype=torch.int32, device=cx.dev),
-               torch.empty(E + 2, dtype=torch.int32, device=cx.dev)) for _ in range(ns)]
-    ks, outs = [k_route(cx, "moe_route", [(exd[si], *routes[si]) for si in range(ns)], E, T,
-                        top_k)], {}
+    ks, outs = [], {}
     for nm, N, K, xdiv in (("gate", I, D, top_k), ("up", I, D, top_k), ("down", D, I, 1)):
         outs[nm] = [cx.empty((P, N), torch.bfloat16) for _ in range(ns)]
         # buffer set si uses layer si % layers's expert tables
         per_set = []
         for si in range(ns):
             x = xs[si] if nm != "down" else cx.randn((P, I), torch.bfloat16)
-            st = (x, exs[si], exd[si], routes[si][0], routes[si][1], outs[nm][si])
+            st = (x, exs[si], exd[si], outs[nm][si])
             per_set.append(k_qmm(cx, f"qmm_{nm}", [st], tabs[si % layers][nm], E, N, K, T,
                                  top_k, xdiv))
         k = per_set[0]
@@ -349,7 +338,7 @@ def wl_qwen3_next_moe_decode(cx):
         ks.append(k)
     act = [(outs["gate"][si], outs["up"][si], cx.empty((P, I), torch.bfloat16))
            for si in range(ns)]
-    ks.insert(3, k_glu(cx, "swiglu_moe", act, P, I, SILU))
+    ks.insert(2, k_glu(cx, "swiglu_moe", act, P, I, SILU))
     cfg = {"workload": "qwen3-next-80b-a3b routed experts, one decode step", "sequences": T,
            "experts": E, "top_k": top_k, "hidden": D, "expert_dim": I, "quant": "4-bit g64",
            "expert_tables": layers, "buffer_sets": ns}

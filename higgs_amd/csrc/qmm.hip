@@ -18,9 +18,11 @@
 //   s * (sum x*(128+q) - 128 * sum x) + b * sum x
 // with the half-group sums of x computed once per block into LDS.
 //
-// Routed form: hgk_moe_route sorts the pairs by expert; run in that order,
-// the pairs of one expert follow each other on the same XCDs, so an expert's
-// weights cross HBM about once however many of the step's tokens chose it.
+// Decode touches ~1.25 pairs per expert, so reading an expert's tile once per
+// pair costs ~1.75x the distinct-expert bytes; grouping the pairs by expert
+// (sorted order, or one block walking an expert's pairs) measured slower on
+// MI355X -- the pairs of one expert run at the same time on different CUs,
+// and serialising them costs more than the re-read.
 #include "../../include/higgs_hip.h"
 #include "hgk_common.h"
 #include "hgk_host.h"
@@ -73,17 +75,12 @@ __device__ inline int64_t pair_row(const QmmArgs& a, int64_t p) {
 // codes, so a wave's load covers 16 rows x 64 contiguous bytes. STEPS = K/128.
 // The x row is staged in LDS permuted to the code order of a word (codes 0..7
 // of a word pair as (0,4) (1,5) (2,6) (3,7)), with its half-group sums.
-// With `order` (pairs grouped by expert), block row y runs pair order[y]:
-// the pairs of one expert run back to back, and since a block's XCD is its
-// linear id modulo 8 and the grid has a multiple of 8 column tiles (or one
-// row of them), the second pair of an expert finds its weight tile in the
-// same XCD's L2 instead of HBM.
 template <class S, int STEPS>
-__global__ __launch_bounds__(256) void qmv_bf16_kernel(QmmArgs a, const int32_t* order) {
+__global__ __launch_bounds__(256) void qmv_bf16_kernel(QmmArgs a) {
   constexpr int K = STEPS * 128;
   __shared__ __attribute__((aligned(16))) uint32_t xs_perm[K / 2];  // bf16 pairs in dot order
   __shared__ float hsum[K / 32];       // sum of x over each 32-code half group
-  const int64_t p = order ? (int64_t)order[blockIdx.y] : (int64_t)blockIdx.y;
+  const int64_t p = blockIdx.y;
   const int64_t e = pair_expert(a, p);
   const int64_t xr0 = pair_row(a, p);
   const bool valid = e >= 0 && e < a.E && xr0 >= 0;
@@ -166,58 +163,6 @@ __global__ __launch_bounds__(256) void qmv_bf16_kernel(QmmArgs a, const int32_t*
   }
 }
 
-// Counting sort of pairs by expert in one block: seg[e]..seg[e+1] delimit the
-// pairs of expert e in `order`; the bucket E (seg[E]..seg[E+1]) collects
-// pairs whose expert id is out of range. Order within an expert is the order
-// in which the block's atomics land (each pair's result does not depend on it).
-__global__ __launch_bounds__(1024) void moe_route_kernel(const void* experts, int experts_i32,
-                                                         int pairs, int E, int32_t* order,
-                                                         int32_t* seg) {
-  extern __shared__ int32_t cnt[];  // E + 1 counters, then E + 2 offsets
-  int32_t* off = cnt + (E + 1);
-  for (int i = threadIdx.x; i < E + 1; i += blockDim.x) cnt[i] = 0;
-  __syncthreads();
-  auto bucket = [&](int p) {
-    int64_t e = experts_i32 ? (int64_t)reinterpret_cast<const int32_t*>(experts)[p]
-                            : (int64_t)reinterpret_cast<const uint32_t*>(experts)[p];
-    if (experts_i32 && e < 0) e += E;
-    return (e >= 0 && e < E) ? (int)e : E;
-  };
-  for (int p = threadIdx.x; p < pairs; p += blockDim.x) atomicAdd(&cnt[bucket(p)], 1);
-  __syncthreads();
-  // exclusive scan of the E + 1 counters: each thread sums a chunk, the
-  // 1024 chunk sums are scanned in LDS (Hillis-Steele), then each thread
-  // writes its chunk's offsets
-  __shared__ int32_t part[1024];
-  const int nb = E + 1;
-  const int chunk = (nb + 1023) / 1024;
-  const int c0 = threadIdx.x * chunk, c1 = min(nb, c0 + chunk);
-  int sum = 0;
-  for (int i = c0; i < c1; ++i) sum += cnt[i];
-  part[threadIdx.x] = sum;
-  __syncthreads();
-  for (int d = 1; d < 1024; d <<= 1) {
-    const int v = threadIdx.x >= d ? part[threadIdx.x - d] : 0;
-    __syncthreads();
-    part[threadIdx.x] += v;
-    __syncthreads();
-  }
-  int run = part[threadIdx.x] - sum;  // exclusive prefix of this chunk
-  for (int i = c0; i < c1; ++i) {
-    off[i] = run;
-    run += cnt[i];
-  }
-  if (threadIdx.x == 1023) off[nb] = part[1023];
-  __syncthreads();
-  for (int i = threadIdx.x; i < E + 2; i += blockDim.x) seg[i] = off[i];
-  for (int i = threadIdx.x; i < E + 1; i += blockDim.x) cnt[i] = off[i];
-  __syncthreads();
-  for (int p = threadIdx.x; p < pairs; p += blockDim.x) {
-    const int slot = atomicAdd(&cnt[bucket(p)], 1);
-    order[slot] = p;
-  }
-}
-
 // Any shape / dtype: one wave per (pair, output row), f32 arithmetic with
 // exact dequantized values, element-strided.
 template <class X, class S>
@@ -245,13 +190,13 @@ __global__ __launch_bounds__(256) void qmv_generic_kernel(QmmArgs a) {
 namespace {
 
 template <class S>
-bool launch_bf16(const QmmArgs& a, const int32_t* order, hipStream_t s) {
+bool launch_bf16(const QmmArgs& a, hipStream_t s) {
   const dim3 grid((unsigned)((a.N + 63) / 64), (unsigned)a.pairs);
   switch (a.K) {
-    case 512: hipLaunchKernelGGL((qmv_bf16_kernel<S, 4>), grid, dim3(256), 0, s, a, order); return true;
-    case 1024: hipLaunchKernelGGL((qmv_bf16_kernel<S, 8>), grid, dim3(256), 0, s, a, order); return true;
-    case 2048: hipLaunchKernelGGL((qmv_bf16_kernel<S, 16>), grid, dim3(256), 0, s, a, order); return true;
-    case 4096: hipLaunchKernelGGL((qmv_bf16_kernel<S, 32>), grid, dim3(256), 0, s, a, order); return true;
+    case 512: hipLaunchKernelGGL((qmv_bf16_kernel<S, 4>), grid, dim3(256), 0, s, a); return true;
+    case 1024: hipLaunchKernelGGL((qmv_bf16_kernel<S, 8>), grid, dim3(256), 0, s, a); return true;
+    case 2048: hipLaunchKernelGGL((qmv_bf16_kernel<S, 16>), grid, dim3(256), 0, s, a); return true;
+    case 4096: hipLaunchKernelGGL((qmv_bf16_kernel<S, 32>), grid, dim3(256), 0, s, a); return true;
     default: return false;
   }
 }
@@ -307,74 +252,8 @@ extern "C" int hgk_gather_qmm(int dtype, const void* x, int64_t x_rows, int64_t 
   const hipStream_t s = as_stream(stream);
   const bool vec_ok = dtype == DT_BF16 && aligned16(x) && x_row_stride % 8 == 0 && aligned16(w) &&
                       (reinterpret_cast<uintptr_t>(scales) & 1) == 0;
-  if (vec_ok && launch_bf16<BF16>(a, nullptr, s)) return launch_status(fn);
+  if (vec_ok && launch_bf16<BF16>(a, s)) return launch_status(fn);
   if (dtype == DT_BF16) launch_generic<BF16, BF16>(a, s);
   else launch_generic<F16, F16>(a, s);
-  return launch_status(fn);
-}
-
-namespace hgk {
-namespace {
-
-}  // namespace
-}  // namespace hgk
-
-extern "C" int hgk_moe_route(const void* rhs_indices, int rhs_dtype, int64_t pairs,
-                             int64_t n_experts, int32_t* order, int32_t* expert_offsets,
-                             void* stream) {
-  clear_error();
-  const char* fn = "hgk_moe_route";
-  if (rhs_dtype != DT_I32 && rhs_dtype != DT_U32)
-    return fail(HGK_ERR_ARG, "%s: expert indices must be int32 or uint32", fn);
-  if (pairs < 0 || pairs > 65535 || n_experts <= 0 || n_experts > 8192)
-    return fail(HGK_ERR_ARG, "%s: pairs=%lld (<= 65535) and n_experts=%lld (1..8192)", fn,
-                (long long)pairs, (long long)n_experts);
-  if (!order || !expert_offsets || (pairs > 0 && !rhs_indices)) return fail(HGK_ERR_ARG, "%s: null pointer", fn);
-  const size_t shmem = (size_t)(2 * n_experts + 3) * sizeof(int32_t);
-  hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(1024), shmem, as_stream(stream), rhs_indices,
-                     rhs_dtype == DT_I32 ? 1 : 0, (int)pairs, (int)n_experts, order, expert_offsets);
-  return launch_status(fn);
-}
-
-extern "C" int hgk_gather_qmm_routed(int dtype, const void* x, int64_t x_rows, int64_t x_row_stride,
-                                     int64_t x_row_div, const int32_t* lhs_indices, const uint32_t* w,
-                                     const void* scales, const void* biases, int scales_dtype,
-                                     int64_t n_experts, int64_t n, int64_t k, int group_size, int bits,
-                                     const void* rhs_indices, int rhs_dtype, int64_t pairs,
-                                     const int32_t* order, const int32_t* expert_offsets, void* y,
-                                     int64_t y_row_stride, void* stream) {
-  clear_error();
-  const char* fn = "hgk_gather_qmm_routed";
-  if (!order || !expert_offsets) return fail(HGK_ERR_ARG, "%s: null order / expert_offsets", fn);
-  (void)expert_offsets;  // the grouping is carried by `order`
-  if (n_experts > 8192) return fail(HGK_ERR_UNSUPPORTED, "%s: n_experts > 8192", fn);
-  const bool vec = dtype == DT_BF16 && scales_dtype == DT_BF16 && bits == 4 &&
-                   (group_size == 32 || group_size == 64 || group_size == 128) &&
-                   (k == 512 || k == 1024 || k == 2048 || k == 4096) && aligned16(x) &&
-                   x_row_stride % 8 == 0 && aligned16(w) &&
-                   (reinterpret_cast<uintptr_t>(scales) & 1) == 0;
-  if (!vec)  // the per-pair kernel takes every other case
-    return hgk_gather_qmm(dtype, x, x_rows, x_row_stride, x_row_div, lhs_indices, w, scales, biases,
-                          scales_dtype, n_experts, n, k, group_size, bits, rhs_indices, rhs_dtype,
-                          pairs, y, y_row_stride, stream);
-  // validate exactly as the per-pair entry point does
-  if (pairs < 0 || n_experts <= 0 || n <= 0 || k % group_size)
-    return fail(HGK_ERR_ARG, "%s: bad shape", fn);
-  if (!lhs_indices && x_row_div <= 0) return fail(HGK_ERR_ARG, "%s: x_row_div must be >= 1", fn);
-  if (x_rows <= 0 || (!lhs_indices && pairs > 0 && (pairs - 1) / x_row_div >= x_rows))
-    return fail(HGK_ERR_ARG, "%s: too few rows of x", fn);
-  if ((x_rows > 1 && x_row_stride < k) || (pairs > 1 && y_row_stride < n))
-    return fail(HGK_ERR_ARG, "%s: row strides smaller than K / N", fn);
-  if (!x || !w || !scales || !biases || !y || (pairs > 0 && !rhs_indices))
-    return fail(HGK_ERR_ARG, "%s: null pointer", fn);
-  if (pairs > 65535 || n_experts * n * k >= ((int64_t)1 << 42))
-    return fail(HGK_ERR_UNSUPPORTED, "%s: problem too large (pairs <= 65535)", fn);
-  if (pairs == 0) return HGK_OK;
-  QmmArgs a{};
-  a.x = x; a.xrows = x_rows; a.xs = x_row_stride; a.xdiv = x_row_div > 0 ? x_row_div : 1;
-  a.lhs = lhs_indices; a.w = w; a.sc = scales; a.bi = biases; a.experts = rhs_indices;
-  a.experts_i32 = rhs_dtype == DT_I32; a.E = n_experts; a.N = n; a.K = k; a.group = group_size;
-  a.pairs = pairs; a.y = y; a.ys = y_row_stride;
-  launch_bf16<BF16>(a, order, as_stream(stream));
   return launch_status(fn);
 }

@@ -770,6 +770,51 @@ Array nn::QuantizedEmbedding::forward_scaled(const Array& ids, float scale) cons
 }
 
 
+// ------------------------------------------------------------------ gather_qmm
+Array gather_qmm(const Array& x, const Array& w, const Array& scales, const Array& biases,
+                 const Array& rhs_indices, bool transpose, int group_size, int bits,
+                 int64_t x_row_div, const Array* lhs_indices) {
+  const char* op = "gather_qmm";
+  Operands ops = {{"x", &x}, {"w", &w}, {"scales", &scales}, {"biases", &biases},
+                  {"idx", &rhs_indices}, {"lhs", lhs_indices}};
+  if (!transpose) fail(op, "only transpose = true (weights stored [N, K]) is implemented", ops);
+  if (x.ndim() != 2 || (x.dim(1) > 1 && x.strides()[1] != 1))
+    fail(op, "x must be [rows, K] with a unit-stride last axis", ops);
+  if (w.ndim() != 3 || w.dtype() != Dtype::Uint32 || !w.is_contiguous() || scales.ndim() != 3 ||
+      scales.shape() != biases.shape() || !scales.is_contiguous() || !biases.is_contiguous())
+    fail(op, "w must be contiguous Uint32 [E, N, K/8]; scales/biases [E, N, K/group]", ops);
+  if (!rhs_indices.is_contiguous() || (lhs_indices && !lhs_indices->is_contiguous()))
+    fail(op, "indices must be contiguous", ops);
+  const int64_t P = rhs_indices.size(), E = w.dim(0), N = w.dim(1), K = x.dim(1);
+  if (w.dim(2) * 32 / bits != K) fail(op, "w's packed width does not match x's K", ops);
+  Array y = Array::empty({P, N}, x.dtype());
+  if (P == 0) return y;
+  check(hgk_gather_qmm(static_cast<int>(x.dtype()), x.data(), x.dim(0), x.strides()[0], x_row_div,
+                       lhs_indices ? static_cast<const int32_t*>(lhs_indices->data()) : nullptr,
+                       static_cast<const uint32_t*>(w.data()), scales.data(), biases.data(),
+                       static_cast<int>(scales.dtype()), E, N, K, group_size, bits,
+                       rhs_indices.data(), static_cast<int>(rhs_indices.dtype()), P, y.data(), N,
+                       stream_arg()),
+        op, ops);
+  return y;
+}
+
+Array nn::SwitchMlpWeights::forward_gather(const Array& x, const Array& indices) const {
+  if (x.ndim() != 2 || indices.ndim() != 2 || indices.dim(0) != x.dim(0))
+    throw Exception::custom("forward_gather input must be [T, D] with indices [T, top_k] " +
+                            operands_text({{"x", &x}, {"indices", &indices}}));
+  const int64_t T = x.dim(0), top_k = indices.dim(1);
+  const Array idx = indices.reshape({T * top_k});
+  const Array g = gather_qmm(x, gate_proj.weight, gate_proj.scales, gate_proj.biases, idx, true,
+                             gate_proj.group_size, gate_proj.bits, top_k);
+  const Array u = gather_qmm(x, up_proj.weight, up_proj.scales, up_proj.biases, idx, true,
+                             up_proj.group_size, up_proj.bits, top_k);
+  const Array act = swiglu(g, u);
+  const Array d = gather_qmm(act, down_proj.weight, down_proj.scales, down_proj.biases, idx, true,
+                             down_proj.group_size, down_proj.bits, 1);
+  return d.reshape({T, top_k, d.dim(1)});
+}
+
 // ------------------------------------------------------------------ checkpoints
 namespace io {
 

@@ -22,6 +22,10 @@
 //   add_rms_norm(x, r, norm)                     h = x.add(r); norm(h) (transformer.rs:413-415)
 //   nn::QuantizedEmbedding{...}.forward(ids)     nn::QuantizedEmbedding (transformer.rs:494)
 //                                                and QEmbedding::forward (qwen3_next.rs:248-257)
+//   gather_qmm(x, w, scales, biases, rhs_indices, transpose, group_size, bits)
+//                                                qwen3_next.rs:294-363
+//   nn::SwitchMlpWeights{...}.forward_gather(x, indices)
+//                                                qwen3_next.rs:844-904
 //   io::load_quantized_safetensors_weights(params, dir, quantized)
 //                                                lib.rs:600-632 (with collect_safetensors_files
 //                                                and remap_quantized_key, lib.rs:682-723)
@@ -237,7 +241,31 @@ struct QuantizedEmbedding {
 
 Array silu_mul(const Array& gate, const Array& up);
 Array gelu_approximate_mul(const Array& gate, const Array& up);
+
+// A quantized linear layer's tensors (qwen3_next.rs:186-210): weight Uint32
+// [.., N, K*bits/32], scales/biases [.., N, K/group_size].
+struct QLinear {
+  Array weight, scales, biases;
+  int group_size = 64;
+  int bits = 4;
+};
+
+// Stacked expert weights of a switch MLP (qwen3_next.rs:824-904).
+struct SwitchMlpWeights {
+  QLinear gate_proj, up_proj, down_proj;
+  // x [T, D], indices [T, top_k] (Int32/Uint32) -> [T, top_k, D]: gate and up
+  // gather_qmm, swiglu, down gather_qmm, as forward_gather does.
+  Array forward_gather(const Array& x, const Array& indices) const;
+};
 }  // namespace nn
+
+// gather_qmm(x, w, scales, biases, rhs_indices, transpose = true, group_size,
+// bits) with one row of x per (token, expert) pair (qwen3_next.rs:294-363):
+// x [R, K]; rhs_indices [P]; pair p reads x row p / x_row_div (or
+// lhs_indices[p]). Returns [P, N].
+Array gather_qmm(const Array& x, const Array& w, const Array& scales, const Array& biases,
+                 const Array& rhs_indices, bool transpose, int group_size, int bits,
+                 int64_t x_row_div = 1, const Array* lhs_indices = nullptr);
 
 // Checkpoint loading (crates/higgs-models/src/lib.rs:574-723): safetensors
 // files in the MLX 4-bit layout, read through the library's reader.

@@ -308,29 +308,16 @@ def fused_gate_up_swiglu(gate_up: torch.Tensor, *, out=None):
 
 
 # ---------------------------------------------------------------- gather_qmm
-def moe_route(rhs_indices: torch.Tensor, n_experts: int):
-    """Pairs grouped by expert for gather_qmm(route=...): returns (order,
-    expert_offsets) as device int32 tensors (hgk_moe_route)."""
-    idx = rhs_indices.reshape(-1).contiguous()
-    order = torch.empty(idx.numel(), dtype=torch.int32, device=idx.device)
-    seg = torch.empty(n_experts + 2, dtype=torch.int32, device=idx.device)
-    check(lib().hgk_moe_route(_ptr(idx), dtype_code(idx.dtype), idx.numel(), n_experts,
-                              _ptr(order), _ptr(seg), _stream(idx.device)))
-    return order, seg
-
-
 def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
                rhs_indices: torch.Tensor, transpose: bool = True, group_size: int = 64,
                bits: int = 4, *, x_row_div: int = 1, lhs_indices: Optional[torch.Tensor] = None,
-               route=None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+               out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """gather_qmm(x, w, scales, biases, rhs_indices, transpose, group_size, bits)
     as SwitchMlpWeights::forward_gather uses it (qwen3_next.rs:844-904): one
     row of x per (token, expert) pair. x is [R, K]; w [E, N, K*bits/32] packed
     32-bit words; rhs_indices [P] expert per pair; pair p reads x row
     lhs_indices[p], or p // x_row_div (x_row_div = top_k broadcasts a token
-    over its experts). ``route`` = moe_route(rhs_indices, E) groups the pairs
-    by expert so each expert's weights are read once (same results). Returns
-    y [P, N] in x's dtype."""
+    over its experts). Returns y [P, N] in x's dtype."""
     if not transpose:
         raise HgkError(2, "gather_qmm: only transpose=True (weights stored [N, K]) is implemented")
     if x.dim() != 2 or x.stride(-1) != 1:
@@ -344,18 +331,11 @@ def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: t
     lhs = None if lhs_indices is None else lhs_indices.reshape(-1).contiguous()
     if out is None:
         out = torch.empty((P, N), dtype=x.dtype, device=x.device)
-    common = (dtype_code(x.dtype), _ptr(x), x.shape[0], x.stride(0), x_row_div, _ptr(lhs),
-              _ptr(w.contiguous()), _ptr(scales.contiguous()), _ptr(biases.contiguous()),
-              dtype_code(scales.dtype), E, N, K, group_size, bits, _ptr(idx),
-              dtype_code(idx.dtype), P)
-    if route is None:
-        check(lib().hgk_gather_qmm(*common, _ptr(out), out.stride(0), _stream(x.device)))
-    else:
-        order, seg = route
-        if order.numel() != P or seg.numel() != E + 2:
-            raise HgkError(1, "route does not match these pairs / experts")
-        check(lib().hgk_gather_qmm_routed(*common, _ptr(order), _ptr(seg), _ptr(out),
-                                          out.stride(0), _stream(x.device)))
+    check(lib().hgk_gather_qmm(dtype_code(x.dtype), _ptr(x), x.shape[0], x.stride(0), x_row_div,
+                               _ptr(lhs), _ptr(w.contiguous()), _ptr(scales.contiguous()),
+                               _ptr(biases.contiguous()), dtype_code(scales.dtype), E, N, K,
+                               group_size, bits, _ptr(idx), dtype_code(idx.dtype), P, _ptr(out),
+                               out.stride(0), _stream(x.device)))
     return out
 
 

@@ -247,33 +247,6 @@ int hgk_gather_qmm(int dtype, const void* x, int64_t x_rows, int64_t x_row_strid
                    int64_t n, int64_t k, int group_size, int bits, const void* rhs_indices,
                    int rhs_dtype, int64_t pairs, void* y, int64_t y_row_stride, void* stream);
 
-/*
- * Group (token, expert) pairs by expert for hgk_gather_qmm_routed: a counting
- * sort on the device. order[pairs] receives pair ids grouped by expert;
- * expert_offsets[n_experts + 2] the group boundaries (expert e's pairs are
- * order[expert_offsets[e] .. expert_offsets[e+1]); the last group collects
- * pairs whose expert id is out of range). pairs <= 65535, n_experts <= 8192.
- * Both outputs are caller-owned device buffers. The same routing serves the
- * gate, up and down projections of one MoE block.
- */
-int hgk_moe_route(const void* rhs_indices, int rhs_dtype, int64_t pairs, int64_t n_experts,
-                  int32_t* order, int32_t* expert_offsets, void* stream);
-
-/*
- * hgk_gather_qmm with the pairs grouped by expert (order / expert_offsets from
- * hgk_moe_route): each expert's weights are read once for all of its pairs
- * instead of once per pair. Same arguments and results as hgk_gather_qmm
- * (bit-identical for the shapes the routed kernel takes: bf16, K in
- * {512, 1024, 2048}; other shapes run the per-pair kernel).
- */
-int hgk_gather_qmm_routed(int dtype, const void* x, int64_t x_rows, int64_t x_row_stride,
-                          int64_t x_row_div, const int32_t* lhs_indices, const uint32_t* w,
-                          const void* scales, const void* biases, int scales_dtype,
-                          int64_t n_experts, int64_t n, int64_t k, int group_size, int bits,
-                          const void* rhs_indices, int rhs_dtype, int64_t pairs,
-                          const int32_t* order, const int32_t* expert_offsets, void* y,
-                          int64_t y_row_stride, void* stream);
-
 /* ------------------------------------------------------------------------
  * Checkpoint files: the safetensors files MLX 4-bit checkpoints ship in
  * (u32-packed `.weight`, bf16/f16 `.scales`/`.biases`, bf16 norm weights).

@@ -503,6 +503,60 @@ TEST(test_quantized_embedding_forward_rms_norm) {
            got_y[i], want_y[i]);
 }
 
+// ---------------------------------------------------------------- gather_qmm
+// SwitchMlpWeights::forward_gather (qwen3_next.rs:844-904): gate and up
+// gather_qmm, swiglu, down gather_qmm. Floating-point contraction: each
+// projection within 1 bf16 ulp of the oracle (or atol 1e-3 next to zero).
+TEST(test_switch_mlp_forward_gather) {
+  const int64_t T = 8, top_k = 4, E = 16, D = 1024, I = 256, G = 64;
+  auto xb = bits_of(normal(9400, T * D), OR_BF16);
+  std::vector<int32_t> idx(T * top_k);
+  std::vector<uint32_t> tmp(T * top_k);
+  or_fill_ids(9401, static_cast<uint32_t>(E), tmp.data(), T * top_k);
+  for (size_t i = 0; i < tmp.size(); ++i) idx[i] = static_cast<int32_t>(tmp[i]);
+  struct Mat { std::vector<uint32_t> w; std::vector<uint16_t> s, b; int64_t N, K; };
+  auto make = [&](uint64_t key, int64_t N, int64_t K) {
+    Mat m{std::vector<uint32_t>(E * N * K / 8), bits_of(uniform(key + 1, E * N * K / G, 0.005f, 0.02f), OR_BF16),
+          bits_of(uniform(key + 2, E * N * K / G, -0.1f, 0.1f), OR_BF16), N, K};
+    or_fill_u32(key, m.w.data(), static_cast<int64_t>(m.w.size()));
+    return m;
+  };
+  Mat gm = make(9410, I, D), um = make(9420, I, D), dm = make(9430, D, I);
+  auto ql = [&](const Mat& m) {
+    return higgs::nn::QLinear{Array::from_slice(m.w, {E, m.N, m.K / 8}),
+                              dev16(m.s, {E, m.N, m.K / G}, Dtype::Bfloat16),
+                              dev16(m.b, {E, m.N, m.K / G}, Dtype::Bfloat16), 64, 4};
+  };
+  higgs::nn::SwitchMlpWeights sw{ql(gm), ql(um), ql(dm)};
+  Array x = dev16(xb, {T, D}, Dtype::Bfloat16);
+  Array y = sw.forward_gather(x, Array::from_slice(idx, {T, top_k}));
+  ASSERT(y.shape() == Shape({T, top_k, D}), "%s", y.describe().c_str());
+  // gate and up against the oracle, then down on the device's own activation
+  const int64_t P = T * top_k;
+  auto check_close = [&](const std::vector<uint16_t>& got, const std::vector<uint16_t>& want, const char* what) {
+    std::vector<float> gf(got.size()), wf(want.size());
+    or_convert_to_f32(OR_BF16, got.data(), gf.data(), static_cast<int64_t>(got.size()));
+    or_convert_to_f32(OR_BF16, want.data(), wf.data(), static_cast<int64_t>(want.size()));
+    for (size_t i = 0; i < got.size(); ++i) {
+      const float d = std::fabs(gf[i] - wf[i]);
+      ASSERT(ulp16(got[i], want[i]) <= 1 || d <= 1e-3f, "%s at %zu: %g vs %g", what, i, gf[i], wf[i]);
+    }
+  };
+  Array idx_flat = Array::from_slice(idx, {P});
+  auto g = higgs::gather_qmm(x, sw.gate_proj.weight, sw.gate_proj.scales, sw.gate_proj.biases, idx_flat, true, 64, 4, top_k);
+  std::vector<uint16_t> want(P * I);
+  ASSERT(or_gather_qmm(OR_BF16, xb.data(), T, D, top_k, nullptr, gm.w.data(), gm.s.data(), gm.b.data(), OR_BF16, E, I,
+                       D, 64, idx.data(), P, want.data(), I) == 0, "oracle gate");
+  check_close(g.to_bits(), want, "gate");
+  auto u = higgs::gather_qmm(x, sw.up_proj.weight, sw.up_proj.scales, sw.up_proj.biases, idx_flat, true, 64, 4, top_k);
+  auto act = higgs::swiglu(g, u);
+  auto actb = act.to_bits();
+  std::vector<uint16_t> want_d(P * D);
+  ASSERT(or_gather_qmm(OR_BF16, actb.data(), P, I, 1, nullptr, dm.w.data(), dm.s.data(), dm.b.data(), OR_BF16, E, D,
+                       I, 64, idx.data(), P, want_d.data(), D) == 0, "oracle down");
+  check_close(y.to_bits(), want_d, "down");
+}
+
 // ---------------------------------------------------------------- checkpoints
 // A safetensors file written byte by byte: an 8-byte little-endian header
 // length, the JSON header, then the tensors' bytes in header order.

@@ -24,7 +24,7 @@ EXPECTED = {
     "test_empty_inputs_give_empty_results", "test_errors_name_the_op_and_operands",
     "test_ops_run_on_the_scoped_stream", "test_add_rms_norm_block_boundaries",
     "test_quantized_embedding_forward_rms_norm",
-    "test_load_quantized_checkpoint_drives_embedding_and_norm",
+    "test_load_quantized_checkpoint_drives_embedding_and_norm", "test_switch_mlp_forward_gather",
 }
 
 
@@ -50,14 +50,15 @@ def test_host_library_exports_the_mlx_shaped_api():
                 "higgs::nn::QuantizedEmbedding::forward(", "higgs::nn::silu_mul(",
                 "higgs::nn::gelu_approximate_mul(", "higgs::apply_rope(", "higgs::swiglu(",
                 "higgs::gated_rms_norm(", "higgs::qk_norm_rope(", "higgs::Array::from_slice(",
-                "higgs::add_rms_norm(", "higgs::nn::QuantizedEmbedding::forward_rms_norm("):
+                "higgs::add_rms_norm(", "higgs::nn::QuantizedEmbedding::forward_rms_norm(",
+                "higgs::gather_qmm(", "higgs::nn::SwitchMlpWeights::forward_gather("):
         assert sym in out, sym
     # the host library reaches the kernels only through the C ABI
     dyn = subprocess.run(["nm", "-D", "--undefined-only", HOST_LIB], capture_output=True,
                          text=True, check=True).stdout
     for fn in ("hgk_rms_norm", "hgk_rope", "hgk_qk_norm_rope", "hgk_glu", "hgk_gated_rms_norm",
                "hgk_quantized_embedding", "hgk_last_error", "hgk_add_rms_norm",
-               "hgk_quantized_embedding_rms_norm"):
+               "hgk_quantized_embedding_rms_norm", "hgk_gather_qmm"):
         assert fn in dyn, fn
 
 

@@ -119,63 +119,3 @@ def test_swiglu_expert_block_end_to_end(dev):
     # three roundings deep, the end-to-end bar widens to 4 ulps
     assert_close(to_host(d), d_ref, O.BF16, max_ulp=4, what="expert block end to end")
 
-
-def _route(dev, ex, E):
-    order, seg = H.moe_route(to_dev(ex, O.I32, dev), E)
-    return order.cpu().numpy(), seg.cpu().numpy()
-
-
-def test_moe_route_groups_pairs_by_expert(dev):
-    E = 512
-    ex = (O.u32(2401, (640,)) % np.uint32(E)).astype(np.int32)
-    ex[[3, 77]] = [E + 5, -1]  # -1 wraps to E - 1; E + 5 goes to the overflow bucket
-    order, seg = _route(dev, ex, E)
-    assert sorted(order.tolist()) == list(range(640))  # a permutation
-    eff = np.where(ex < 0, ex + E, ex)
-    eff = np.where((eff >= 0) & (eff < E), eff, E)
-    counts = np.bincount(eff, minlength=E + 1)
-    assert np.array_equal(np.diff(seg), counts) and seg[0] == 0 and seg[-1] == 640
-    for e in (0, 17, E - 1, E):
-        assert (eff[order[seg[e]:seg[e + 1]]] == e).all()
-
-
-@pytest.mark.parametrize("proj", ["gate_up", "down"])
-def test_routed_equals_per_pair_bitexact(dev, proj):
-    """Grouping pairs by expert changes only how often weights are read: the
-    arithmetic per pair is the same, so the results are bit-identical."""
-    T, top_k, E = 64, 10, 512
-    P = T * top_k
-    if proj == "gate_up":
-        x, w, s, b, ex = _case(2411, P, T, E, 512, 2048)
-        x_div = top_k
-    else:
-        x, w, s, b, ex = _case(2421, P, P, E, 2048, 512)
-        x_div = 1
-    ex = ex.copy()
-    ex[[5, 600]] = [E + 1, -3]
-    tx, tw, ts, tb = to_dev(x, O.BF16, dev), words_dev(w, dev), to_dev(s, O.BF16, dev), to_dev(b, O.BF16, dev)
-    tex = to_dev(ex, O.I32, dev)
-    plain = H.gather_qmm(tx, tw, ts, tb, tex, x_row_div=x_div)
-    routed = H.gather_qmm(tx, tw, ts, tb, tex, x_row_div=x_div, route=H.moe_route(tex, E))
-    assert np.array_equal(to_host(routed), to_host(plain))
-    assert not to_host(routed)[5].any()
-    ref = O.gather_qmm(x, O.BF16, w, s, b, O.BF16, ex, x_div=x_div)
-    _check(to_host(routed), ref, O.BF16, f"routed {proj}")
-
-
-def test_routed_heavy_experts_and_variants(dev):
-    """Many pairs on few experts (more than one chunk of staged rows per
-    expert), K 1024 with group 32 and 128, and lhs routing."""
-    for K, group, E, P in ((1024, 32, 3, 50), (1024, 128, 7, 33), (512, 64, 2, 9)):
-        x, w, s, b, ex = _case(2430 + K + group + E, P, P, E, 256, K, group=group)
-        lhs = (np.arange(P) * 5) % P
-        tx, tw, ts, tb = (to_dev(x, O.BF16, dev), words_dev(w, dev), to_dev(s, O.BF16, dev),
-                          to_dev(b, O.BF16, dev))
-        tex = to_dev(ex, O.I32, dev)
-        tl = to_dev(lhs.astype(np.int32), O.I32, dev)
-        plain = H.gather_qmm(tx, tw, ts, tb, tex, group_size=group, lhs_indices=tl)
-        routed = H.gather_qmm(tx, tw, ts, tb, tex, group_size=group, lhs_indices=tl,
-                              route=H.moe_route(tex, E))
-        assert np.array_equal(to_host(routed), to_host(plain)), (K, group, E)
-        ref = O.gather_qmm(x, O.BF16, w, s, b, O.BF16, ex, group=group, lhs=lhs)
-        _check(to_host(routed), ref, O.BF16, f"routed K={K} g={group} E={E}")
