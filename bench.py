@@ -345,6 +345,51 @@ def wl_qwen3_next_moe_decode(cx):
     return Workload("qwen3_next_moe_decode", cfg, ks, ns, T)
 
 
+def k_gdn(cx, name, sets, wq, wk, alog, dtb, B, T, Hk, Dk, Hv, Dv):
+    """Gated-delta recurrence with the fused q/k norm; bytes = state read and
+    written once + q, k, v, a, b read + y written."""
+    nbytes = (2 * B * Hv * Dv * Dk * 2 + B * T * (2 * Hk * Dk + Hv * Dv + 2 * Hv) * 2 +
+              B * T * Hv * Dv * 2 + 2 * Dk * 2 + 2 * Hv * 4)
+    args = [(BF16, _vp(q), _vp(k), _vp(v), _vp(alog), _vp(a), _vp(dtb), _vp(b), F32, _vp(st),
+             _vp(wq), _vp(wk), _f(1e-6), B, T, Hk, Dk, Hv, Dv, _vp(y), _vp(so), cx.stream)
+            for q, k, v, a, b, st, y, so in sets]
+    return Kernel(name, nbytes, cx.lib.hgk_gated_delta, args, B * T,
+                  keep=(sets, wq, wk, alog, dtb),
+                  cpu=("gdn", dict(B=B, T=T, Hk=Hk, Dk=Dk, Hv=Hv, Dv=Dv)))
+
+
+def _gdn_sets(cx, ns, B, T, Hk, Dk, Hv, Dv):
+    torch = cx.torch
+    r = lambda shape, lo, hi: (torch.rand(shape, device=cx.dev, generator=cx.gen) * (hi - lo) + lo
+                               ).to(torch.bfloat16)
+    return [(r((B, T, Hk, Dk), -1, 1), r((B, T, Hk, Dk), -1, 1), r((B, T, Hv, Dv), -1, 1),
+             r((B, T, Hv), -1, 1), r((B, T, Hv), -1, 1), r((B, Hv, Dv, Dk), -0.1, 0.1),
+             cx.empty((B, T, Hv, Dv), torch.bfloat16), cx.empty((B, Hv, Dv, Dk), torch.bfloat16))
+            for _ in range(ns)]
+
+
+def wl_qwen3_next_gdn(cx):
+    """Qwen3-Next-80B-A3B linear-attention recurrence (Hk 16, Dk 128, Hv 32,
+    Dv 128, bf16, the constant-weight q/k norm fused): one decode token for 64
+    sequences (bound by the 1 MB bf16 state per sequence), and a 4 x 512-token
+    prefill."""
+    torch = cx.torch
+    Hk, Dk, Hv, Dv = 16, 128, 32, 128
+    from higgs_amd.ops import gdn_qk_norm_weights
+    wq, wk = gdn_qk_norm_weights(Dk, torch.bfloat16, cx.dev)
+    alog = (torch.rand(Hv, device=cx.dev, generator=cx.gen) - 1.0).contiguous()
+    dtb = (torch.rand(Hv, device=cx.dev, generator=cx.gen) - 0.5).contiguous()
+    ns = 8
+    ks = [k_gdn(cx, "gdn_decode_64seq", _gdn_sets(cx, ns, 64, 1, Hk, Dk, Hv, Dv), wq, wk, alog,
+                dtb, 64, 1, Hk, Dk, Hv, Dv),
+          k_gdn(cx, "gdn_prefill_4x512", _gdn_sets(cx, ns, 4, 512, Hk, Dk, Hv, Dv), wq, wk, alog,
+                dtb, 4, 512, Hk, Dk, Hv, Dv)]
+    cfg = {"workload": "qwen3-next-80b-a3b gated-delta recurrence", "k_heads": Hk, "head_k_dim": Dk,
+           "v_heads": Hv, "head_v_dim": Dv, "decode_sequences": 64, "prefill": "4 x 512",
+           "buffer_sets": ns}
+    return Workload("qwen3_next_gdn", cfg, ks, ns, 64 + 4 * 512)
+
+
 def wl_rmsnorm_512(cx):
     torch = cx.torch
     rows, n = 512, 2048
@@ -458,6 +503,7 @@ WORKLOADS = {
     "llama32_1b_chain_fused": wl_llama_chain_fused,
     "block_boundary_add_rms_norm": wl_block_boundary,
     "qwen3_next_moe_decode": wl_qwen3_next_moe_decode,
+    "qwen3_next_gdn": wl_qwen3_next_gdn,
 }
 
 
@@ -758,6 +804,20 @@ def cpu_op(spec, budget_s=1.0):
         fn = lambda: O.gather_qmm(x, B16, wq, sc, bi, B16, ex, group=G)
         nbytes = Pn * (N * K // 2 + 4 * N * (K // G) + 2 * K + 2 * N)
         rows, what = Pn, f"{Pn} (token, expert) pairs, distinct experts"
+    elif kind == "gdn":
+        Bs = min(p["B"], 4)
+        Ts = min(p["T"], 16)
+        Hk, Dk, Hv, Dv = p["Hk"], p["Dk"], p["Hv"], p["Dv"]
+        u = lambda key, shape, lo, hi: O.from_f32(O.uniform(key, shape, lo, hi), B16)
+        q, k = u(7028, (Bs, Ts, Hk, Dk), -1, 1), u(7029, (Bs, Ts, Hk, Dk), -1, 1)
+        v = u(7030, (Bs, Ts, Hv, Dv), -1, 1)
+        a_, b_ = u(7031, (Bs, Ts, Hv), -1, 1), u(7032, (Bs, Ts, Hv), -1, 1)
+        st = u(7033, (Bs, Hv, Dv, Dk), -0.1, 0.1)
+        al, db = O.uniform(7034, (Hv,), -1, 0), O.uniform(7035, (Hv,), -0.5, 0.5)
+        wq, wk = O.gdn_qk_norm_weights(Dk, B16)
+        fn = lambda: O.gated_delta(q, k, v, al, a_, db, b_, B16, state=st, qw=wq, kw=wk)
+        nbytes = (2 * Bs * Hv * Dv * Dk * 2 + Bs * Ts * (2 * Hk * Dk + 2 * Hv * Dv + 2 * Hv) * 2)
+        rows, what = Bs * Ts, f"{Bs} sequences x {Ts} tokens (f64 recurrence)"
     else:
         raise ValueError(kind)
     fn()

@@ -15,6 +15,8 @@ Each function keeps the reference call's name and argument meaning:
     add_rms_norm(x, r, weight, eps)          h = x.add(r); norm(h) (transformer.rs:413-415)
     QuantizedEmbedding(...).forward(ids)     nn::QuantizedEmbedding / QEmbedding::forward
     gather_qmm(x, w, scales, biases, rhs_indices)   qwen3_next.rs:294-363, 844-904
+    gated_delta(q, k, v, a_log, a, dt_bias, b, state)
+                                             qwen3_next.rs:376-451, 1152-1201
     QuantizedEmbedding(...).forward_rms_norm(ids, w, eps)
                                              embed_tokens + the first input_layernorm
                                              (transformer.rs:494, 407)
@@ -337,6 +339,44 @@ def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: t
                                group_size, bits, _ptr(idx), dtype_code(idx.dtype), P, _ptr(out),
                                out.stride(0), _stream(x.device)))
     return out
+
+
+# ---------------------------------------------------------------- GatedDeltaNet
+def gdn_qk_norm_weights(head_k_dim: int, dtype: torch.dtype, device):
+    """GatedDeltaNet's constant q/k norm weights (qwen3_next.rs:1111-1130):
+    s = 1/sqrt(Dk) in f32; q's weight is s*s, k's is s, cast to `dtype`."""
+    s = torch.tensor(1.0, dtype=torch.float32) / torch.sqrt(torch.tensor(float(head_k_dim)))
+    wq = torch.full((head_k_dim,), float(s * s), dtype=torch.float32).to(dtype)
+    wk = torch.full((head_k_dim,), float(s), dtype=torch.float32).to(dtype)
+    return wq.to(device), wk.to(device)
+
+
+def gated_delta(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, a_log: torch.Tensor,
+                a: torch.Tensor, dt_bias: torch.Tensor, b: torch.Tensor,
+                state: Optional[torch.Tensor] = None, *, q_norm_w: Optional[torch.Tensor] = None,
+                k_norm_w: Optional[torch.Tensor] = None, eps: float = 1e-6,
+                state_out: Optional[torch.Tensor] = None):
+    """The gated-delta recurrence (gated_delta_kernel_ffi, qwen3_next.rs:376-451)
+    with the optional constant-weight q/k RMSNorm fused in: q, k [B, T, Hk, Dk],
+    v [B, T, Hv, Dv], a, b [B, T, Hv], a_log, dt_bias [Hv], state [B, Hv, Dv, Dk]
+    or None (zeros). Returns (y [B, T, Hv, Dv], new_state)."""
+    B, T, Hk, Dk = q.shape
+    Hv, Dv = v.shape[2], v.shape[3]
+    for t in (q, k, v, a, b):
+        if not t.is_contiguous() or t.dtype != q.dtype:
+            raise HgkError(1, "q, k, v, a, b must be contiguous and share a dtype")
+    if a_log.dtype != dt_bias.dtype:
+        raise HgkError(1, "a_log and dt_bias must share a dtype")
+    y = torch.empty((B, T, Hv, Dv), dtype=q.dtype, device=q.device)
+    if state_out is None:
+        state_out = torch.empty((B, Hv, Dv, Dk), dtype=q.dtype, device=q.device)
+    check(lib().hgk_gated_delta(dtype_code(q.dtype), _ptr(q), _ptr(k), _ptr(v),
+                                _ptr(a_log.contiguous()), _ptr(a), _ptr(dt_bias.contiguous()),
+                                _ptr(b), dtype_code(a_log.dtype),
+                                None if state is None else _ptr(state.contiguous()),
+                                _ptr(q_norm_w), _ptr(k_norm_w), eps, B, T, Hk, Dk, Hv, Dv,
+                                _ptr(y), _ptr(state_out), _stream(q.device)))
+    return y, state_out
 
 
 # ---------------------------------------------------------------- embedding

@@ -247,6 +247,26 @@ int hgk_gather_qmm(int dtype, const void* x, int64_t x_rows, int64_t x_row_strid
                    int64_t n, int64_t k, int group_size, int bits, const void* rhs_indices,
                    int rhs_dtype, int64_t pairs, void* y, int64_t y_row_stride, void* stream);
 
+/*
+ * The GatedDeltaNet recurrence of Qwen3-Next's linear-attention layers -- the
+ * reference's own gated-delta kernel (crates/higgs-models/src/qwen3_next.rs:
+ * 376-451, called at 1187-1201) -- with the constant-weight q/k RMSNorm that
+ * precedes it (1172-1173) fused in when q_norm_w/k_norm_w are given:
+ *   g = exp(-exp(a_log) * softplus(a_t + dt_bias)), beta = sigmoid(b_t)
+ *   s = s * g; delta = (v_t - s . k_t) * beta; s = s + k_t * delta; y_t = s . q_t
+ * q, k [B, T, Hk, Dk], v [B, T, Hv, Dv], a, b [B, T, Hv] and y [B, T, Hv, Dv]
+ * contiguous in `dtype`; a_log, dt_bias [Hv] in param_dtype; state_in and
+ * state_out [B, Hv, Dv, Dk] in `dtype` (state_in NULL: zeros; state_out may be
+ * state_in). Value head hv reads key head hv / (Hv / Hk). The state is f32
+ * inside a call and rounded to `dtype` at its end, as in the reference.
+ * head_k_dim in {32, 64, 128, 256}; batch * v_heads <= 65535.
+ */
+int hgk_gated_delta(int dtype, const void* q, const void* k, const void* v, const void* a_log,
+                    const void* a, const void* dt_bias, const void* b, int param_dtype,
+                    const void* state_in, const void* q_norm_w, const void* k_norm_w, float eps,
+                    int64_t batch, int64_t seq_len, int64_t k_heads, int64_t head_k_dim,
+                    int64_t v_heads, int64_t head_v_dim, void* y, void* state_out, void* stream);
+
 /* ------------------------------------------------------------------------
  * Checkpoint files: the safetensors files MLX 4-bit checkpoints ship in
  * (u32-packed `.weight`, bf16/f16 `.scales`/`.biases`, bf16 norm weights).

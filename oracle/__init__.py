@@ -63,6 +63,8 @@ def lib():
             "or_add": (_i32, [_i32, _vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64]),
             "or_gather_qmm": (_i32, [_i32, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _i32,
                                      _i64, _i64, _i64, _i32, _vp, _i64, _vp, _i64]),
+            "or_gated_delta": (_i32, [_i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp,
+                                      _f32, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp]),
             "or_rope_inv_freq": (None, [_f32, _i32, _vp, _vp]),
             "or_llama3_freqs": (None, [_f32, _i32, _f32, _f32, _f32, _f32, _vp]),
             "or_norm_rope": (_i32, [_i32, _vp, _vp, _vp, _vp, _i64, _i64, _i64,
@@ -211,6 +213,31 @@ def gather_qmm(x, x_dt, w, scales, biases, s_dt, experts, *, group=64, x_div=1, 
                                _p(np.ascontiguousarray(biases)), s_dt, E, N, K, group,
                                _p(experts), P, _p(y), N), "gather_qmm")
     return y
+
+
+def gated_delta(q, k, v, a_log, a, dt_bias, b, dt, *, p_dt=F32, state=None, qw=None, kw=None,
+                eps=1e-6):
+    """GatedDeltaNet recurrence (qwen3_next.rs:376-451): q, k [B,T,Hk,Dk],
+    v [B,T,Hv,Dv], a, b [B,T,Hv] in dt; a_log, dt_bias [Hv] in p_dt; state
+    [B,Hv,Dv,Dk] in dt or None. qw/kw: the constant q/k norm weights [Dk] in
+    dt (1172-1173), or None. Returns (y [B,T,Hv,Dv], state_out) in dt."""
+    B, T, Hk, Dk = q.shape
+    Hv, Dv = v.shape[2], v.shape[3]
+    y = np.empty((B, T, Hv, Dv), storage_dtype(dt))
+    so = np.empty((B, Hv, Dv, Dk), storage_dtype(dt))
+    c = lambda arr: None if arr is None else np.ascontiguousarray(arr)
+    q, k, v, a, b, a_log, dt_bias, state, qw, kw = map(c, (q, k, v, a, b, a_log, dt_bias, state, qw, kw))
+    _check(lib().or_gated_delta(dt, _p(q), _p(k), _p(v), _p(a_log), _p(a), _p(dt_bias), _p(b), p_dt,
+                                _p(state), _p(qw), _p(kw), eps, B, T, Hk, Dk, Hv, Dv, _p(y), _p(so)),
+           "gated_delta")
+    return y, so
+
+
+def gdn_qk_norm_weights(Dk: int, dt: int):
+    """The constant q/k norm weights of GatedDeltaNet (qwen3_next.rs:1111-1130):
+    s = 1/sqrt(Dk) in f32; q's weight is s*s, k's is s, each cast to dt."""
+    s = np.float32(1.0) / np.sqrt(np.float32(Dk))
+    return (from_f32(np.full(Dk, s * s, np.float32), dt), from_f32(np.full(Dk, s, np.float32), dt))
 
 
 def rope_inv_freq(base, dims, freqs=None) -> np.ndarray:

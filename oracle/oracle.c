@@ -33,6 +33,7 @@
 #include "oracle.h"
 
 #include <math.h>
+#include <stdlib.h>
 #include <stdint.h>
 #include <string.h>
 
@@ -488,5 +489,82 @@ int or_gather_qmm(int dt, const void* x, int64_t x_rows, int64_t x_rs, int64_t x
       st(y, dt, p * y_rs + n, rnd((float)acc, dt));
     }
   }
+  return 0;
+}
+
+/* ------------------------------------------------------------------ */
+/* GatedDeltaNet recurrence                                            */
+/* ------------------------------------------------------------------ */
+
+/* The gated-delta recurrence of the reference's Metal kernel
+ * (crates/higgs-models/src/qwen3_next.rs:376-451), here in f64 per state row:
+ *   g = exp(-exp(a_log) * softplus(a_t + dt_bias)), beta = sigmoid(b_t)
+ *   s = s * g; kv = s.k_t; delta = (v_t - kv) * beta; s = s + k_t * delta;
+ *   y_t = s.q_t
+ * with q, k [B,T,Hk,Dk], v [B,T,Hv,Dv], a, b [B,T,Hv], a_log, dt_bias [Hv]
+ * (dtype p_dt), state [B,Hv,Dv,Dk] read and written in dt (state_in may be
+ * NULL: zeros). When qw/kw are given, q and k are first normalised as
+ * or_rms_norm(x, w, eps) rows of Dk in dt (qwen3_next.rs:1172-1173). The
+ * reference kernel runs in f32 with its own reduction order: the parity bar
+ * against this f64 restatement is a tolerance. */
+int or_gated_delta(int dt, const void* q, const void* k, const void* v, const void* a_log,
+                   const void* a, const void* dt_bias, const void* b, int p_dt,
+                   const void* state_in, const void* qw, const void* kw, float eps,
+                   int64_t B, int64_t T, int64_t Hk, int64_t Dk, int64_t Hv, int64_t Dv,
+                   void* y, void* state_out) {
+  if (!q || !k || !v || !a_log || !a || !dt_bias || !b || !y || !state_out || Hv % Hk) return 1;
+  const size_t es = dt == OR_F32 ? 4 : 2;
+  const void* qn = q;
+  const void* kn = k;
+  void* qbuf = NULL;
+  void* kbuf = NULL;
+  if (qw && kw) {
+    const int64_t rows = B * T * Hk;
+    qbuf = malloc((size_t)(rows * Dk) * es);
+    kbuf = malloc((size_t)(rows * Dk) * es);
+    if (!qbuf || !kbuf) { free(qbuf); free(kbuf); return 1; }
+    or_rms_norm(q, dt, Dk, qw, dt, 0, eps, qbuf, dt, Dk, rows, Dk);
+    or_rms_norm(k, dt, Dk, kw, dt, 0, eps, kbuf, dt, Dk, rows, Dk);
+    qn = qbuf;
+    kn = kbuf;
+  }
+#pragma omp parallel for collapse(2) schedule(static)
+  for (int64_t bi = 0; bi < B; ++bi) {
+    for (int64_t hv = 0; hv < Hv; ++hv) {
+      const int64_t hk = hv / (Hv / Hk);
+      const double A = exp((double)ld(a_log, p_dt, hv));
+      const double dtb = (double)ld(dt_bias, p_dt, hv);
+      double* sv = (double*)malloc((size_t)(Dv * Dk) * sizeof(double));
+      for (int64_t d = 0; d < Dv * Dk; ++d)
+        sv[d] = state_in ? (double)ld(state_in, dt, (bi * Hv + hv) * Dv * Dk + d) : 0.0;
+      for (int64_t t = 0; t < T; ++t) {
+        const double x = (double)ld(a, dt, (bi * T + t) * Hv + hv) + dtb;
+        const double sp = (x > 0.0 ? x : 0.0) + log1p(exp(-fabs(x)));
+        const double g = exp(-A * sp);
+        const double beta = 1.0 / (1.0 + exp(-(double)ld(b, dt, (bi * T + t) * Hv + hv)));
+        const int64_t qk = ((bi * T + t) * Hk + hk) * Dk;
+        for (int64_t dv = 0; dv < Dv; ++dv) {
+          double* s = sv + dv * Dk;
+          double kv = 0.0;
+          for (int64_t i = 0; i < Dk; ++i) {
+            s[i] *= g;
+            kv += s[i] * (double)ld(kn, dt, qk + i);
+          }
+          const double delta = ((double)ld(v, dt, ((bi * T + t) * Hv + hv) * Dv + dv) - kv) * beta;
+          double out = 0.0;
+          for (int64_t i = 0; i < Dk; ++i) {
+            s[i] += (double)ld(kn, dt, qk + i) * delta;
+            out += s[i] * (double)ld(qn, dt, qk + i);
+          }
+          st(y, dt, ((bi * T + t) * Hv + hv) * Dv + dv, rnd((float)out, dt));
+        }
+      }
+      for (int64_t d = 0; d < Dv * Dk; ++d)
+        st(state_out, dt, (bi * Hv + hv) * Dv * Dk + d, rnd((float)sv[d], dt));
+      free(sv);
+    }
+  }
+  free(qbuf);
+  free(kbuf);
   return 0;
 }

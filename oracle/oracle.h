@@ -122,6 +122,14 @@ int or_gather_qmm(int dt, const void* x, int64_t x_rows, int64_t x_rs, int64_t x
                   int s_dt, int64_t E, int64_t N, int64_t K, int group, const int32_t* experts,
                   int64_t pairs, void* y, int64_t y_rs);
 
+/* GatedDeltaNet recurrence (qwen3_next.rs:376-451) in f64, with the optional
+ * constant-weight q/k RMSNorm (1172-1173) in front. */
+int or_gated_delta(int dt, const void* q, const void* k, const void* v, const void* a_log,
+                   const void* a, const void* dt_bias, const void* b, int p_dt,
+                   const void* state_in, const void* qw, const void* kw, float eps,
+                   int64_t B, int64_t T, int64_t Hk, int64_t Dk, int64_t Hv, int64_t Dv,
+                   void* y, void* state_out);
+
 #ifdef __cplusplus
 }
 #endif

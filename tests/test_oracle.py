@@ -550,3 +550,90 @@ def test_gather_qmm_routing_and_out_of_range():
     lhs[3] = R
     y5 = O.gather_qmm(x, O.BF16, w, s, b, O.BF16, ex, lhs=lhs)
     assert not y5[3].any()
+
+
+# ------------------------------------------------------------------ GatedDeltaNet
+def _gdn_inputs(key, B, T, Hk, Dk, Hv, Dv, dt=O.F32):
+    """The reference tests' distributions (qwen3_next.rs:2577-2595)."""
+    u = lambda k, shape, lo, hi: O.from_f32(O.uniform(key + k, shape, lo, hi), dt)
+    return dict(q=u(0, (B, T, Hk, Dk), -1, 1), k=u(1, (B, T, Hk, Dk), -1, 1),
+                v=u(2, (B, T, Hv, Dv), -1, 1), a_log=O.uniform(key + 3, (Hv,), -1, 0),
+                a=u(4, (B, T, Hv), -1, 1), dt_bias=O.uniform(key + 5, (Hv,), -0.5, 0.5),
+                b=u(6, (B, T, Hv), -1, 1), state=u(7, (B, Hv, Dv, Dk), -0.1, 0.1))
+
+
+def _gdn_torch_f64(inp, dt):
+    """An independent torch f64 restatement of the step loop (the shape of the
+    reference's gated_delta_step_ref, qwen3_next.rs:2452-2486)."""
+    f = lambda x: torch.from_numpy(O.to_f32(x, dt).astype(np.float64))
+    q, k, v, a, b, S = (f(inp[n]) for n in ("q", "k", "v", "a", "b", "state"))
+    a_log = torch.from_numpy(inp["a_log"].astype(np.float64))
+    dtb = torch.from_numpy(inp["dt_bias"].astype(np.float64))
+    Hk, Hv = q.shape[2], v.shape[2]
+    rep = Hv // Hk
+    ys = []
+    for t in range(q.shape[1]):
+        g = torch.exp(-torch.exp(a_log) * torch.nn.functional.softplus(a[:, t] + dtb))
+        beta = torch.sigmoid(b[:, t])
+        qt = q[:, t].repeat_interleave(rep, dim=1)
+        kt = k[:, t].repeat_interleave(rep, dim=1)
+        S = S * g[..., None, None]
+        kv = (S * kt[:, :, None, :]).sum(-1)
+        delta = (v[:, t] - kv) * beta[..., None]
+        S = S + kt[:, :, None, :] * delta[..., None]
+        ys.append((S * qt[:, :, None, :]).sum(-1))
+    return torch.stack(ys, 1), S
+
+
+@pytest.mark.parametrize("shape", [(1, 3, 2, 32, 4, 32), (2, 5, 16, 128, 32, 16)])
+def test_gated_delta_matches_torch_f64(shape):
+    B, T, Hk, Dk, Hv, Dv = shape
+    inp = _gdn_inputs(2501 + T, *shape)
+    y, s = O.gated_delta(inp["q"], inp["k"], inp["v"], inp["a_log"], inp["a"], inp["dt_bias"],
+                         inp["b"], O.F32, state=inp["state"])
+    ty, ts = _gdn_torch_f64(inp, O.F32)
+    np.testing.assert_allclose(y, ty.numpy(), rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(s, ts.numpy(), rtol=1e-5, atol=1e-6)
+
+
+def test_gated_delta_closed_forms():
+    """a = dt_bias = 0 and a_log = 0 give g = 2^-1 exactly; with k = 0 the
+    update leaves s = g * s0, so y = (s0 . q) / 2. With s0 = 0, a huge b
+    (beta = 1) and k = e_j, one step gives s[dv] = v[dv] e_j and y = v q_j."""
+    B, T, Hk, Dk, Hv, Dv = 1, 1, 1, 32, 2, 8
+    inp = _gdn_inputs(2511, B, T, Hk, Dk, Hv, Dv)
+    z = lambda shape: np.zeros(shape, np.float32)
+    y, s = O.gated_delta(inp["q"], z((B, T, Hk, Dk)), inp["v"], z(Hv), z((B, T, Hv)), z(Hv),
+                         inp["b"], O.F32, state=inp["state"])
+    s0 = inp["state"].astype(np.float64)
+    np.testing.assert_allclose(s, s0 * 0.5, rtol=0, atol=0)
+    ref = 0.5 * np.einsum("bhvk,bk->bhv", s0, inp["q"][:, 0, 0].astype(np.float64))
+    np.testing.assert_allclose(y[:, 0], ref, rtol=1e-6, atol=1e-7)
+    j = 5
+    k = z((B, T, Hk, Dk))
+    k[..., j] = 1.0
+    y, s = O.gated_delta(inp["q"], k, inp["v"], z(Hv), z((B, T, Hv)), z(Hv),
+                         np.full((B, T, Hv), 60.0, np.float32), O.F32, state=None)
+    np.testing.assert_allclose(s[0, :, :, j], inp["v"][0, 0], rtol=1e-6)
+    assert not np.delete(s, j, axis=-1).any()
+    np.testing.assert_allclose(y[0, 0], inp["v"][0, 0] * inp["q"][0, 0, 0, j], rtol=1e-6)
+
+
+def test_gated_delta_norm_weights_and_rounding():
+    """The fused q/k norm is rms_norm with the constant weights s*s and s
+    (s = 1/sqrt(Dk) in f32, cast to the dtype): bf16(1/128) and
+    bf16(0.0883883) at Dk = 128; a bf16 run equals the run on pre-normalised
+    inputs, and the state and y come back rounded to bf16."""
+    wq, wk = O.gdn_qk_norm_weights(128, O.BF16)
+    assert O.to_f32(wq, O.BF16)[0] == np.float32(1 / 128)
+    assert O.to_f32(wk, O.BF16)[0] == np.float32(0.08837890625)
+    shape = (1, 2, 2, 128, 4, 8)
+    inp = _gdn_inputs(2521, *shape, dt=O.BF16)
+    args = (inp["v"], inp["a_log"], inp["a"], inp["dt_bias"], inp["b"], O.BF16)
+    y1, s1 = O.gated_delta(inp["q"], inp["k"], *args, state=inp["state"], qw=wq, kw=wk)
+    B, T, Hk, Dk = inp["q"].shape
+    qn = O.rms_norm(inp["q"].reshape(-1, Dk), O.BF16, wq, O.BF16, 1e-6).reshape(inp["q"].shape)
+    kn = O.rms_norm(inp["k"].reshape(-1, Dk), O.BF16, wk, O.BF16, 1e-6).reshape(inp["k"].shape)
+    y2, s2 = O.gated_delta(qn, kn, *args, state=inp["state"])
+    assert np.array_equal(y1, y2) and np.array_equal(s1, s2)
+    assert y1.dtype == np.uint16 and s1.dtype == np.uint16
