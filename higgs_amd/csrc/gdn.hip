@@ -14,10 +14,21 @@
 // (1/Dk for q, 1/sqrt(Dk) for k, in the activation dtype; 1172-1173) when the
 // caller passes those weights.
 //
-// Work split: as in the reference, 32 lanes own one state row (Dk/32 values
-// each), so a wave64 holds two rows and both dot products reduce over 32
-// lanes; a block of 256 threads owns 8 rows (dv) of one (b, hv). The loads of
-// step t+1 are issued before step t's arithmetic.
+// Kernels (all with the same per-row arithmetic; the dot products are f32
+// sums whose order differs from the reference's, within the stated bars):
+//  * token (T = 1, the decode step): no LDS and no barrier. A 16-lane group
+//    owns 8 consecutive state rows (Dk/16 columns per lane), so each dot
+//    product reduces inside a DPP row. Every load is issued up front, the small
+//    ones (gates, q, k, v, norm weights) before the state rows, so the q/k norm
+//    and the gates run while the state is in flight; each row is then
+//    converted, advanced, packed and stored on its own.
+//  * decode (T = 2): as token, with the state held in f32 across the steps.
+//  * chunk (T > 2): stages 16 steps at a time in LDS -- q and k normalised
+//    once per step, g and beta once per step, v for the block's 32 rows -- and
+//    every lane carries two state rows whose chains interleave; the next
+//    chunk's global loads are issued before the current chunk's recurrence,
+//    and y is staged in LDS and stored per step as one run of 32 rows.
+//  * row (any alignment): 32 lanes per row, step t+1 loaded during step t.
 #include <cmath>
 
 #include "../../include/higgs_hip.h"
@@ -38,6 +49,7 @@ struct GdnArgs {
   const void* qw;  // fused norm weights [Dk] (activation dtype) or null
   const void* kw;
   int pdt;         // dtype of a_log / dt_bias
+  int hgrp;        // v heads per k head
   float eps;
   float inv_dk;
   int64_t B, T, Hk, Dk, Hv, Dv;
@@ -52,10 +64,24 @@ __device__ inline float sum32(float v) {
   return v;
 }
 
+// Raw storage word of element e of X (16-bit types zero-extended), kept
+// unconverted so that a load issued ahead of its use is not waited on early.
+template <class X>
+__device__ inline uint32_t ldraw(const void* base, int64_t e) {
+  if constexpr (X::kBytes == 2) return reinterpret_cast<const uint16_t*>(base)[e];
+  else return reinterpret_cast<const uint32_t*>(base)[e];
+}
+
+template <class X>
+__device__ inline float cvt(uint32_t w) {
+  if constexpr (X::kBytes == 2) return X::lo(w);
+  else return u2f(w);
+}
+
 template <class X, int NPT>
 struct GdnStep {
-  float q[NPT], k[NPT];
-  float v, at, bt;
+  uint32_t q[NPT], k[NPT];
+  uint32_t v, at, bt;
 };
 
 template <class X, int NPT>
@@ -64,13 +90,48 @@ __device__ inline void gdn_load(const GdnArgs& a, GdnStep<X, NPT>& s, int64_t bi
   const int64_t qk = ((bi * a.T + t) * a.Hk + hk) * a.Dk + (int64_t)j * NPT;
 #pragma unroll
   for (int i = 0; i < NPT; ++i) {
-    s.q[i] = load1<X>(a.q, qk + i);
-    s.k[i] = load1<X>(a.k, qk + i);
+    s.q[i] = ldraw<X>(a.q, qk + i);
+    s.k[i] = ldraw<X>(a.k, qk + i);
   }
-  s.v = load1<X>(a.v, ((bi * a.T + t) * a.Hv + hv) * a.Dv + dv);
-  s.at = load1<X>(a.a, (bi * a.T + t) * a.Hv + hv);
-  s.bt = load1<X>(a.b, (bi * a.T + t) * a.Hv + hv);
+  s.v = ldraw<X>(a.v, ((bi * a.T + t) * a.Hv + hv) * a.Dv + dv);
+  s.at = ldraw<X>(a.a, (bi * a.T + t) * a.Hv + hv);
+  s.bt = ldraw<X>(a.b, (bi * a.T + t) * a.Hv + hv);
 }
+
+// One element of a_log / dt_bias (runtime dtype): the storage word is loaded
+// unconverted in each dtype's branch and converted after the join, so the
+// load is not waited on inside the branch.
+__device__ inline float load_param(const void* base, int dt, int64_t e) {
+  uint32_t w;
+  if (dt == DT_F32) w = reinterpret_cast<const uint32_t*>(base)[e];
+  else w = reinterpret_cast<const uint16_t*>(base)[e];
+  if (dt == DT_F32) return u2f(w);
+  if (dt == DT_BF16) return u2f(w << 16);
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)w);
+}
+
+// Sum over the 16 lanes of a DPP row (every lane receives the sum).
+template <int CTRL>
+__device__ inline float dpp_f(float v) {
+  return u2f((uint32_t)__builtin_amdgcn_update_dpp(0, (int)f2u(v), CTRL, 0xF, 0xF, true));
+}
+
+__device__ inline float sum16(float v) {
+  v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_f<0x141>(v);  // row_half_mirror
+  v += dpp_f<0x140>(v);  // row_mirror
+  return v;
+}
+
+// softplus, g and beta of one step (qwen3_next.rs:398-402).
+__device__ inline float gdn_gate(float at, float dtb, float A) {
+  const float x = at + dtb;
+  const float sp = fmaxf(x, 0.0f) + log1pf(expf(-fabsf(x)));
+  return expf(-A * sp);
+}
+
+__device__ inline float gdn_beta(float bt) { return 1.0f / (1.0f + expf(-bt)); }
 
 // q or k row normalised as rms_norm(x, w, eps) in dtype X: n = round(x * r),
 // out = round(n * w), with the sum of squares taken in f64 over the row.
@@ -86,11 +147,10 @@ __device__ inline void gdn_norm(float* x, const float* w, float inv_dk, float ep
 }
 
 template <class X, int NPT, bool NORM>
-__global__ __launch_bounds__(256) void gated_delta_kernel(GdnArgs a) {
+__global__ __launch_bounds__(256) void gated_delta_row_kernel(GdnArgs a) {
   const int row = threadIdx.x >> 5, j = threadIdx.x & 31;
-  const int64_t bh = blockIdx.y;
-  const int64_t bi = bh / a.Hv, hv = bh - bi * a.Hv;
-  const int64_t hk = hv / (a.Hv / a.Hk);
+  const int64_t hv = blockIdx.y, bi = blockIdx.z;
+  const int64_t hk = (int)blockIdx.y / a.hgrp;
   const int64_t dv0 = (int64_t)blockIdx.x * 8 + row;
   const bool live = dv0 < a.Dv;
   const int64_t dv = live ? dv0 : a.Dv - 1;
@@ -107,34 +167,39 @@ __global__ __launch_bounds__(256) void gated_delta_kernel(GdnArgs a) {
       wk[i] = load1<X>(a.kw, (int64_t)j * NPT + i);
     }
   }
-  const float A = expf(load1_dt(a.a_log, a.pdt, hv));
-  const float dtb = load1_dt(a.dt_bias, a.pdt, hv);
+  const float A = expf(load_param(a.a_log, a.pdt, hv));
+  const float dtb = load_param(a.dt_bias, a.pdt, hv);
 
   GdnStep<X, NPT> cur, nxt;
   if (a.T > 0) gdn_load<X, NPT>(a, cur, bi, 0, hk, hv, dv, j);
   for (int64_t t = 0; t < a.T; ++t) {
-    if (t + 1 < a.T) gdn_load<X, NPT>(a, nxt, bi, t + 1, hk, hv, dv, j);
-    if constexpr (NORM) {
-      gdn_norm<X, NPT>(cur.q, wq, a.inv_dk, a.eps);
-      gdn_norm<X, NPT>(cur.k, wk, a.inv_dk, a.eps);
+    // step t+1, or step t again on the last step: an unconditional load
+    gdn_load<X, NPT>(a, nxt, bi, t + 1 < a.T ? t + 1 : t, hk, hv, dv, j);
+    float q[NPT], k[NPT];
+#pragma unroll
+    for (int i = 0; i < NPT; ++i) {
+      q[i] = cvt<X>(cur.q[i]);
+      k[i] = cvt<X>(cur.k[i]);
     }
-    const float x = cur.at + dtb;
-    const float sp = fmaxf(x, 0.0f) + log1pf(expf(-fabsf(x)));
-    const float g = expf(-A * sp);
-    const float beta = 1.0f / (1.0f + expf(-cur.bt));
+    if constexpr (NORM) {
+      gdn_norm<X, NPT>(q, wq, a.inv_dk, a.eps);
+      gdn_norm<X, NPT>(k, wk, a.inv_dk, a.eps);
+    }
+    const float g = gdn_gate(cvt<X>(cur.at), dtb, A);
+    const float beta = gdn_beta(cvt<X>(cur.bt));
     float kv = 0.0f;
 #pragma unroll
     for (int i = 0; i < NPT; ++i) {
       st[i] = st[i] * g;
-      kv = __builtin_fmaf(st[i], cur.k[i], kv);
+      kv = __builtin_fmaf(st[i], k[i], kv);
     }
     kv = sum32(kv);
-    const float delta = (cur.v - kv) * beta;
+    const float delta = (cvt<X>(cur.v) - kv) * beta;
     float out = 0.0f;
 #pragma unroll
     for (int i = 0; i < NPT; ++i) {
-      st[i] = __builtin_fmaf(cur.k[i], delta, st[i]);
-      out = __builtin_fmaf(st[i], cur.q[i], out);
+      st[i] = __builtin_fmaf(k[i], delta, st[i]);
+      out = __builtin_fmaf(st[i], q[i], out);
     }
     out = sum32(out);
     if (j == 0 && live) store1<X>(a.y, ((bi * a.T + t) * a.Hv + hv) * a.Dv + dv, out);
@@ -146,18 +211,549 @@ __global__ __launch_bounds__(256) void gated_delta_kernel(GdnArgs a) {
   }
 }
 
+// ---------------------------------------------------------------- chunked
+// N contiguous elements of X at element e, N * sizeof(X) in {4 .. 64} bytes
+// and aligned to min(16, N * sizeof(X)).
+template <class X, int N>
+__device__ inline void load_row_part(const void* base, int64_t e, float* v) {
+  constexpr int BYTES = N * X::kBytes;
+  const char* p = reinterpret_cast<const char*>(base) + e * X::kBytes;
+  if constexpr (BYTES == 4) {
+    const uint32_t w = *reinterpret_cast<const uint32_t*>(p);
+    if constexpr (X::kBytes == 2) { v[0] = X::lo(w); v[1] = X::hi(w); }
+    else v[0] = u2f(w);
+  } else if constexpr (BYTES == 8) {
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    const u32x2 w = *reinterpret_cast<const u32x2*>(p);
+    if constexpr (X::kBytes == 2) { v[0] = X::lo(w[0]); v[1] = X::hi(w[0]); v[2] = X::lo(w[1]); v[3] = X::hi(w[1]); }
+    else { v[0] = u2f(w[0]); v[1] = u2f(w[1]); }
+  } else {
+    static_assert(BYTES % 16 == 0, "whole chunks");
+    load_elems<X, N>(base, e, v);
+  }
+}
+
+template <class X, int N>
+__device__ inline void store_row_part(void* base, int64_t e, const float* v) {
+  constexpr int BYTES = N * X::kBytes;
+  char* p = reinterpret_cast<char*>(base) + e * X::kBytes;
+  if constexpr (BYTES == 4) {
+    if constexpr (X::kBytes == 2) *reinterpret_cast<uint32_t*>(p) = X::pack(v[0], v[1]);
+    else *reinterpret_cast<float*>(p) = v[0];
+  } else if constexpr (BYTES == 8) {
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    u32x2 w;
+    if constexpr (X::kBytes == 2) { w[0] = X::pack(v[0], v[1]); w[1] = X::pack(v[2], v[3]); }
+    else { w[0] = f2u(v[0]); w[1] = f2u(v[1]); }
+    *reinterpret_cast<u32x2*>(p) = w;
+  } else {
+    store_elems<X, N, false>(base, e, v);
+  }
+}
+
+constexpr int kChunk = 16;  // steps staged per chunk
+constexpr int kRows = 32;   // state rows per block (4 waves x 4 DPP rows x 2)
+
+// Per-thread registers of one chunk's global loads, kept raw until publish.
+// q/k: thread owns part (tid & 7) of row (tid >> 3) = step (tid >> 4), q or k
+// by bit 3; v: step (tid >> 4), rows 2 * (tid & 15) + {0, 1}; a or b: the
+// first 2 * kChunk threads, one step each.
+template <class X, int DK>
+struct GdnChunkRaw {
+  static constexpr int NE = DK / 8;                 // q/k elements per thread
+  static constexpr int NW = NE * X::kBytes / 4;     // as 32-bit words
+  uint32_t qk[NW];
+  uint32_t v0, v1, ab;
+};
+
+template <class X, int DK>
+__device__ inline void gdn_fetch(const GdnArgs& a, GdnChunkRaw<X, DK>& r, int64_t bi, int64_t hk,
+                                 int64_t hv, int64_t dv0, int64_t t0, int tid) {
+  using R = GdnChunkRaw<X, DK>;
+  const int64_t last = a.T - 1;
+  {
+    const int s = tid >> 4, isk = (tid >> 3) & 1, part = tid & 7;
+    const int64_t t = t0 + s < last ? t0 + s : last;
+    const void* src = isk ? (const void*)a.k : (const void*)a.q;
+    const char* p = reinterpret_cast<const char*>(src) +
+                    ((((bi * a.T + t) * a.Hk + hk) * DK) + part * R::NE) * X::kBytes;
+    if constexpr (R::NW % 4 == 0) {
+#pragma unroll
+      for (int c = 0; c < R::NW / 4; ++c) {
+        const u32x4 w = reinterpret_cast<const u32x4*>(p)[c];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) r.qk[4 * c + i] = w[i];
+      }
+    } else {
+      typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+      static_assert(R::NW == 2, "8-byte part");
+      const u32x2 w = *reinterpret_cast<const u32x2*>(p);
+      r.qk[0] = w[0];
+      r.qk[1] = w[1];
+    }
+  }
+  {
+    const int s = tid >> 4, pr = tid & 15;
+    const int64_t t = t0 + s < last ? t0 + s : last;
+    const int64_t d0 = dv0 + 2 * pr < a.Dv ? dv0 + 2 * pr : a.Dv - 1;
+    const int64_t d1 = dv0 + 2 * pr + 1 < a.Dv ? dv0 + 2 * pr + 1 : a.Dv - 1;
+    const int64_t base = ((bi * a.T + t) * a.Hv + hv) * a.Dv;
+    r.v0 = ldraw<X>(a.v, base + d0);
+    r.v1 = ldraw<X>(a.v, base + d1);
+  }
+  {
+    const int s = tid & (kChunk - 1);
+    const int64_t t = t0 + s < last ? t0 + s : last;
+    r.ab = ldraw<X>(tid < kChunk ? (const void*)a.a : (const void*)a.b, (bi * a.T + t) * a.Hv + hv);
+  }
+}
+
+template <class X, int NPT, bool NORM>
+__global__ __launch_bounds__(256) void gated_delta_chunk_kernel(GdnArgs a) {
+  constexpr int DK = 16 * NPT;
+  using Raw = GdnChunkRaw<X, DK>;
+  constexpr int NE = Raw::NE;
+  __shared__ __align__(16) float qs[kChunk][DK];
+  __shared__ __align__(16) float ks[kChunk][DK];
+  __shared__ __align__(16) float vs[kChunk][kRows];
+  __shared__ __align__(16) float ys[kChunk][kRows];
+  __shared__ __align__(16) float gb[kChunk][2];
+
+  const int tid = threadIdx.x;
+  const int64_t hv = blockIdx.y, bi = blockIdx.z;
+  const int64_t hk = (int)blockIdx.y / a.hgrp;
+  const int64_t dv0 = (int64_t)blockIdx.x * kRows;
+
+  // this lane's two state rows: local rows rl, rl + 1; columns j * NPT ..
+  const int lane = tid & 63, j = lane & 15;
+  const int rl = (tid >> 6) * 8 + (lane >> 4) * 2;
+  float st[2][NPT];
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int64_t dv = dv0 + rl + r < a.Dv ? dv0 + rl + r : a.Dv - 1;
+    const int64_t e = ((bi * a.Hv + hv) * a.Dv + dv) * DK + (int64_t)j * NPT;
+    if (a.state_in) load_row_part<X, NPT>(a.state_in, e, st[r]);
+    else {
+#pragma unroll
+      for (int i = 0; i < NPT; ++i) st[r][i] = 0.0f;
+    }
+  }
+
+  Raw raw;
+  if (a.T > 0) gdn_fetch<X, DK>(a, raw, bi, hk, hv, dv0, 0, tid);
+
+  // publish-side constants: this thread's norm weights (q or k, fixed by tid)
+  const int ns = tid >> 4, nisk = (tid >> 3) & 1, npart = tid & 7;
+  float wn[NE];
+  if constexpr (NORM) {
+#pragma unroll
+    for (int i = 0; i < NE; ++i) wn[i] = load1<X>(nisk ? a.kw : a.qw, npart * NE + i);
+  }
+  const float A = expf(load_param(a.a_log, a.pdt, hv));
+  const float dtb = load_param(a.dt_bias, a.pdt, hv);
+  const bool dv_even = (a.Dv & 1) == 0;
+
+  // y of the chunk at t0 (n steps) from ys to global, one run of rows per step
+  auto store_y = [&](int64_t t0, int n) {
+    const int s = tid >> 4, pr = tid & 15;
+    const int64_t d0 = dv0 + 2 * pr;
+    if (s < n && d0 < a.Dv) {
+      const int64_t e = ((bi * a.T + t0 + s) * a.Hv + hv) * a.Dv + d0;
+      const float y0 = ys[s][2 * pr], y1 = ys[s][2 * pr + 1];
+      if constexpr (X::kBytes == 2) {
+        if (dv_even) {
+          reinterpret_cast<uint32_t*>(a.y)[e >> 1] = X::pack(y0, y1);
+        } else {
+          store1<X>(a.y, e, y0);
+          if (d0 + 1 < a.Dv) store1<X>(a.y, e + 1, y1);
+        }
+      } else {
+        if (dv_even) {
+          reinterpret_cast<f32x2*>(a.y)[e >> 1] = f32x2{y0, y1};
+        } else {
+          store1<X>(a.y, e, y0);
+          if (d0 + 1 < a.Dv) store1<X>(a.y, e + 1, y1);
+        }
+      }
+    }
+  };
+
+  for (int64_t t0 = 0; t0 < a.T; t0 += kChunk) {
+    const int n = a.T - t0 < kChunk ? (int)(a.T - t0) : kChunk;
+    __syncthreads();  // the previous chunk's readers of qs/ks/vs/gb and writers of ys are done
+    if (t0 > 0) store_y(t0 - kChunk, kChunk);
+    {
+      float x[NE];
+#pragma unroll
+      for (int i = 0; i < NE; ++i) x[i] = elem<X>(raw.qk, i);
+      if constexpr (NORM) {
+        double ss = 0.0;
+#pragma unroll
+        for (int i = 0; i < NE; ++i) ss = __builtin_fma((double)x[i], (double)x[i], ss);
+        ss = group_sum<8>(ss);
+        const float r = rms_scale(ss, a.inv_dk, a.eps);
+#pragma unroll
+        for (int i = 0; i < NE; ++i) x[i] = X::round(X::round(x[i] * r) * wn[i]);
+      }
+      float* dst = (nisk ? &ks[ns][0] : &qs[ns][0]) + npart * NE;
+#pragma unroll
+      for (int i = 0; i < NE; i += 4)
+        *reinterpret_cast<float4*>(dst + i) = make_float4(x[i], x[i + 1], x[i + 2], x[i + 3]);
+      const int pr = tid & 15;
+      *reinterpret_cast<f32x2*>(&vs[ns][2 * pr]) = f32x2{cvt<X>(raw.v0), cvt<X>(raw.v1)};
+      if (tid < 2 * kChunk) {
+        const float ab = cvt<X>(raw.ab);
+        gb[tid & (kChunk - 1)][tid >> 4] = tid < kChunk ? gdn_gate(ab, dtb, A) : gdn_beta(ab);
+      }
+    }
+    __syncthreads();
+    if (t0 + kChunk < a.T) gdn_fetch<X, DK>(a, raw, bi, hk, hv, dv0, t0 + kChunk, tid);
+
+    // LDS reads of the next step are issued before a step's arithmetic, into
+    // the other of two register sets (steps alternate between them)
+    float qa[NPT], ka[NPT], qb[NPT], kb[NPT];
+    f32x2 va, ga, vb, gbb;
+    auto rd = [&](float* q, float* k, f32x2& v, f32x2& g, int s) {
+#pragma unroll
+      for (int i = 0; i < NPT; i += 2) {
+        const f32x2 qq = *reinterpret_cast<const f32x2*>(&qs[s][j * NPT + i]);
+        const f32x2 kk = *reinterpret_cast<const f32x2*>(&ks[s][j * NPT + i]);
+        q[i] = qq[0]; q[i + 1] = qq[1];
+        k[i] = kk[0]; k[i + 1] = kk[1];
+      }
+      v = *reinterpret_cast<const f32x2*>(&vs[s][rl]);
+      g = *reinterpret_cast<const f32x2*>(&gb[s][0]);
+    };
+    auto step = [&](const float* q, const float* k, f32x2 vv, f32x2 g2, int s) {
+      const float g = g2[0], beta = g2[1];
+      float out[2];
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        float kv = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NPT; ++i) {
+          st[r][i] = st[r][i] * g;
+          kv = __builtin_fmaf(st[r][i], k[i], kv);
+        }
+        kv = sum16(kv);
+        const float delta = (vv[r] - kv) * beta;
+        float o = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NPT; ++i) {
+          st[r][i] = __builtin_fmaf(k[i], delta, st[r][i]);
+          o = __builtin_fmaf(st[r][i], q[i], o);
+        }
+        out[r] = sum16(o);
+      }
+      if (j == 0) *reinterpret_cast<f32x2*>(&ys[s][rl]) = f32x2{out[0], out[1]};
+    };
+    rd(qa, ka, va, ga, 0);
+    for (int s = 0; s < n; s += 2) {
+      rd(qb, kb, vb, gbb, s + 1 < n ? s + 1 : s);
+      step(qa, ka, va, ga, s);
+      if (s + 1 < n) {
+        rd(qa, ka, va, ga, s + 2 < n ? s + 2 : s + 1);
+        step(qb, kb, vb, gbb, s + 1);
+      }
+    }
+  }
+  if (a.T > 0) {
+    __syncthreads();
+    const int64_t tl = ((a.T - 1) / kChunk) * kChunk;
+    store_y(tl, (int)(a.T - tl));
+  }
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    if (dv0 + rl + r < a.Dv) {
+      const int64_t e = ((bi * a.Hv + hv) * a.Dv + dv0 + rl + r) * DK + (int64_t)j * NPT;
+      store_row_part<X, NPT>(a.state_out, e, st[r]);
+    }
+  }
+}
+
+#ifndef HGK_GDN_RPL
+#define HGK_GDN_RPL 8
+#endif
+#ifndef HGK_GDN_WPB
+#define HGK_GDN_WPB 4
+#endif
+// ---------------------------------------------------------------- decode
+// Few steps (decode): no LDS and no barrier. Each 16-lane group owns RPL
+// consecutive state rows (Dk/16 columns per lane), normalises the step's q
+// and k itself and computes g and beta itself; the state rows' vector loads
+// are issued first, so a wave keeps RPL * 16 * Dk * sizeof(X) bytes in
+// flight from its first instructions.
+template <class X, int NPT, bool NORM, int RPL>
+__global__ __launch_bounds__(256) void gated_delta_decode_kernel(GdnArgs a) {
+  constexpr int DK = 16 * NPT;
+  const int tid = threadIdx.x, lane = tid & 63, j = lane & 15;
+  const int64_t hv = blockIdx.y, bi = blockIdx.z;
+  const int64_t hk = (int)blockIdx.y / a.hgrp;
+  const int64_t r0 = (int64_t)blockIdx.x * (16 * RPL) + ((tid >> 6) * 4 + (lane >> 4)) * RPL;
+
+  float st[RPL][NPT];
+#pragma unroll
+  for (int r = 0; r < RPL; ++r) {
+    const int64_t dv = r0 + r < a.Dv ? r0 + r : a.Dv - 1;
+    const int64_t e = ((bi * a.Hv + hv) * a.Dv + dv) * DK + (int64_t)j * NPT;
+    if (a.state_in) load_row_part<X, NPT>(a.state_in, e, st[r]);
+    else {
+#pragma unroll
+      for (int i = 0; i < NPT; ++i) st[r][i] = 0.0f;
+    }
+  }
+  float wq[NPT], wk[NPT];
+  if constexpr (NORM) {
+    load_row_part<X, NPT>(a.qw, (int64_t)j * NPT, wq);
+    load_row_part<X, NPT>(a.kw, (int64_t)j * NPT, wk);
+  }
+  const float A = expf(load_param(a.a_log, a.pdt, hv));
+  const float dtb = load_param(a.dt_bias, a.pdt, hv);
+
+  for (int64_t t = 0; t < a.T; ++t) {
+    const int64_t row = (bi * a.T + t) * a.Hv + hv;
+    float q[NPT], k[NPT], v[RPL];
+    load_row_part<X, NPT>(a.q, ((bi * a.T + t) * a.Hk + hk) * DK + (int64_t)j * NPT, q);
+    load_row_part<X, NPT>(a.k, ((bi * a.T + t) * a.Hk + hk) * DK + (int64_t)j * NPT, k);
+#pragma unroll
+    for (int r = 0; r < RPL; ++r) v[r] = load1<X>(a.v, row * a.Dv + (r0 + r < a.Dv ? r0 + r : a.Dv - 1));
+    const float g = gdn_gate(load1<X>(a.a, row), dtb, A);
+    const float beta = gdn_beta(load1<X>(a.b, row));
+    if constexpr (NORM) {
+#pragma unroll
+      for (int w = 0; w < 2; ++w) {
+        float* x = w ? k : q;
+        const float* wt = w ? wk : wq;
+        double ss = 0.0;
+#pragma unroll
+        for (int i = 0; i < NPT; ++i) ss = __builtin_fma((double)x[i], (double)x[i], ss);
+        ss = group_sum<16>(ss);
+        const float rs = rms_scale(ss, a.inv_dk, a.eps);
+#pragma unroll
+        for (int i = 0; i < NPT; ++i) x[i] = X::round(X::round(x[i] * rs) * wt[i]);
+      }
+    }
+    float out[RPL];
+#pragma unroll
+    for (int r = 0; r < RPL; ++r) {
+      float kv = 0.0f;
+#pragma unroll
+      for (int i = 0; i < NPT; ++i) {
+        st[r][i] = st[r][i] * g;
+        kv = __builtin_fmaf(st[r][i], k[i], kv);
+      }
+      kv = sum16(kv);
+      const float delta = (v[r] - kv) * beta;
+      float o = 0.0f;
+#pragma unroll
+      for (int i = 0; i < NPT; ++i) {
+        st[r][i] = __builtin_fmaf(k[i], delta, st[r][i]);
+        o = __builtin_fmaf(st[r][i], q[i], o);
+      }
+      out[r] = sum16(o);
+    }
+    if (j == 0) {
+#pragma unroll
+      for (int r = 0; r < RPL; ++r)
+        if (r0 + r < a.Dv) store1<X>(a.y, row * a.Dv + r0 + r, out[r]);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < RPL; ++r) {
+    if (r0 + r < a.Dv) {
+      const int64_t e = ((bi * a.Hv + hv) * a.Dv + r0 + r) * DK + (int64_t)j * NPT;
+      store_row_part<X, NPT>(a.state_out, e, st[r]);
+    }
+  }
+}
+
+// One token (T = 1): as the decode kernel, but the state rows stay packed in
+// their storage words until their turn, and each row is converted, advanced,
+// packed and stored on its own, so only one row is live in f32 at a time
+// (fewer VGPRs, more waves per SIMD to overlap the loads).
+template <class X, int NPT>
+__device__ inline void load_row_raw(const void* base, int64_t e, uint32_t* w) {
+  constexpr int NW = NPT * X::kBytes / 4;
+  const char* p = reinterpret_cast<const char*>(base) + e * X::kBytes;
+  if constexpr (NW == 1) {
+    w[0] = *reinterpret_cast<const uint32_t*>(p);
+  } else if constexpr (NW == 2) {
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    const u32x2 v = *reinterpret_cast<const u32x2*>(p);
+    w[0] = v[0]; w[1] = v[1];
+  } else {
+#pragma unroll
+    for (int c = 0; c < NW / 4; ++c) {
+      const u32x4 v = reinterpret_cast<const u32x4*>(p)[c];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) w[4 * c + i] = v[i];
+    }
+  }
+}
+
+template <class X, class P, int NPT, bool NORM, int RPL>
+__global__ __launch_bounds__(256) void gated_delta_token_kernel(GdnArgs a) {
+  constexpr int DK = 16 * NPT;
+  constexpr int NW = NPT * X::kBytes / 4;
+  const int tid = threadIdx.x, lane = tid & 63, j = lane & 15;
+  const int64_t hv = blockIdx.y, bi = blockIdx.z;
+  const int64_t hk = (int)blockIdx.y / a.hgrp;
+  const int64_t r0 = (int64_t)blockIdx.x * (blockDim.x / 16 * RPL) + ((tid >> 6) * 4 + (lane >> 4)) * RPL;
+  const int64_t sbase = (bi * a.Hv + hv) * a.Dv;
+  const int64_t row = bi * a.Hv + hv;  // T == 1
+
+  // Issue order: the small loads first, then the state rows, so that the
+  // norm and the gates wait only for the former while the state is in flight.
+  uint32_t araw, braw, vraw[RPL];
+  uint32_t qraw[NW], kraw[NW], wqraw[NW], wkraw[NW];
+  const uint32_t alog_raw = ldraw<P>(a.a_log, hv);
+  const uint32_t dtb_raw = ldraw<P>(a.dt_bias, hv);
+  araw = ldraw<X>(a.a, row);
+  braw = ldraw<X>(a.b, row);
+  load_row_raw<X, NPT>(a.q, (bi * a.Hk + hk) * DK + (int64_t)j * NPT, qraw);
+  load_row_raw<X, NPT>(a.k, (bi * a.Hk + hk) * DK + (int64_t)j * NPT, kraw);
+  if constexpr (NORM) {
+    load_row_raw<X, NPT>(a.qw, (int64_t)j * NPT, wqraw);
+    load_row_raw<X, NPT>(a.kw, (int64_t)j * NPT, wkraw);
+  }
+#pragma unroll
+  for (int r = 0; r < RPL; ++r) vraw[r] = ldraw<X>(a.v, row * a.Dv + (r0 + r < a.Dv ? r0 + r : a.Dv - 1));
+  uint32_t raw[RPL][NW];
+  if (a.state_in) {
+#pragma unroll
+    for (int r = 0; r < RPL; ++r) {
+      const int64_t dv = r0 + r < a.Dv ? r0 + r : a.Dv - 1;
+      load_row_raw<X, NPT>(a.state_in, (sbase + dv) * DK + (int64_t)j * NPT, raw[r]);
+    }
+  }
+
+  const float g = gdn_gate(cvt<X>(araw), cvt<P>(dtb_raw), expf(cvt<P>(alog_raw)));
+  const float beta = gdn_beta(cvt<X>(braw));
+  float q[NPT], k[NPT];
+#pragma unroll
+  for (int i = 0; i < NPT; ++i) {
+    q[i] = elem<X>(qraw, i);
+    k[i] = elem<X>(kraw, i);
+  }
+  if constexpr (NORM) {
+#pragma unroll
+    for (int w = 0; w < 2; ++w) {
+      float* x = w ? k : q;
+      const uint32_t* wr = w ? wkraw : wqraw;
+      double ss = 0.0;
+#pragma unroll
+      for (int i = 0; i < NPT; ++i) ss = __builtin_fma((double)x[i], (double)x[i], ss);
+      ss = group_sum<16>(ss);
+      const float rs = rms_scale(ss, a.inv_dk, a.eps);
+#pragma unroll
+      for (int i = 0; i < NPT; ++i) x[i] = X::round(X::round(x[i] * rs) * elem<X>(wr, i));
+    }
+  }
+  float out[RPL];
+#pragma unroll
+  for (int r = 0; r < RPL; ++r) {
+    float st[NPT];
+    if (a.state_in) {
+#pragma unroll
+      for (int i = 0; i < NPT; ++i) st[i] = elem<X>(raw[r], i);
+    } else {
+#pragma unroll
+      for (int i = 0; i < NPT; ++i) st[i] = 0.0f;
+    }
+    float kv = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NPT; ++i) {
+      st[i] = st[i] * g;
+      kv = __builtin_fmaf(st[i], k[i], kv);
+    }
+    kv = sum16(kv);
+    const float delta = (cvt<X>(vraw[r]) - kv) * beta;
+    float o = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NPT; ++i) {
+      st[i] = __builtin_fmaf(k[i], delta, st[i]);
+      o = __builtin_fmaf(st[i], q[i], o);
+    }
+    out[r] = sum16(o);
+    if (r0 + r < a.Dv) store_row_part<X, NPT>(a.state_out, (sbase + r0 + r) * DK + (int64_t)j * NPT, st);
+  }
+  if (j == 0) {
+#pragma unroll
+    for (int r = 0; r < RPL; ++r)
+      if (r0 + r < a.Dv) store1<X>(a.y, row * a.Dv + r0 + r, out[r]);
+  }
+}
+
 namespace {
 
 template <class X, bool NORM>
-bool launch_x(const GdnArgs& a, hipStream_t s) {
-  const dim3 grid((unsigned)((a.Dv + 7) / 8), (unsigned)(a.B * a.Hv));
+bool launch_decode(const GdnArgs& a, hipStream_t s) {
+  constexpr int RPL = 4;
+  const dim3 grid((unsigned)((a.Dv + 16 * RPL - 1) / (16 * RPL)), (unsigned)a.Hv, (unsigned)a.B);
   switch (a.Dk) {
-    case 32: hipLaunchKernelGGL((gated_delta_kernel<X, 1, NORM>), grid, dim3(256), 0, s, a); return true;
-    case 64: hipLaunchKernelGGL((gated_delta_kernel<X, 2, NORM>), grid, dim3(256), 0, s, a); return true;
-    case 128: hipLaunchKernelGGL((gated_delta_kernel<X, 4, NORM>), grid, dim3(256), 0, s, a); return true;
-    case 256: hipLaunchKernelGGL((gated_delta_kernel<X, 8, NORM>), grid, dim3(256), 0, s, a); return true;
+    case 32: hipLaunchKernelGGL((gated_delta_decode_kernel<X, 2, NORM, RPL>), grid, dim3(256), 0, s, a); return true;
+    case 64: hipLaunchKernelGGL((gated_delta_decode_kernel<X, 4, NORM, RPL>), grid, dim3(256), 0, s, a); return true;
+    case 128: hipLaunchKernelGGL((gated_delta_decode_kernel<X, 8, NORM, RPL>), grid, dim3(256), 0, s, a); return true;
+    case 256: hipLaunchKernelGGL((gated_delta_decode_kernel<X, 16, NORM, RPL>), grid, dim3(256), 0, s, a); return true;
     default: return false;
   }
+}
+
+template <class X, class P, bool NORM>
+bool launch_token_p(const GdnArgs& a, hipStream_t s) {
+  constexpr int RPL = HGK_GDN_RPL, WPB = HGK_GDN_WPB, ROWS = 4 * RPL * WPB;
+  const dim3 grid((unsigned)((a.Dv + ROWS - 1) / ROWS), (unsigned)a.Hv, (unsigned)a.B);
+  const dim3 block(64 * WPB);
+  switch (a.Dk) {
+    case 32: hipLaunchKernelGGL((gated_delta_token_kernel<X, P, 2, NORM, RPL>), grid, block, 0, s, a); return true;
+    case 64: hipLaunchKernelGGL((gated_delta_token_kernel<X, P, 4, NORM, RPL>), grid, block, 0, s, a); return true;
+    case 128: hipLaunchKernelGGL((gated_delta_token_kernel<X, P, 8, NORM, RPL>), grid, block, 0, s, a); return true;
+    case 256: hipLaunchKernelGGL((gated_delta_token_kernel<X, P, 16, NORM, RPL>), grid, block, 0, s, a); return true;
+    default: return false;
+  }
+}
+
+// a_log / dt_bias in f32 or in the activation dtype (other pairings take the
+// decode kernel, which reads them in any float dtype)
+template <class X, bool NORM>
+bool launch_token(const GdnArgs& a, hipStream_t s) {
+  if (a.pdt == DT_F32) return launch_token_p<X, F32, NORM>(a, s);
+  if (a.pdt == X::kCode) return launch_token_p<X, X, NORM>(a, s);
+  return launch_decode<X, NORM>(a, s);
+}
+
+template <class X, bool NORM>
+bool launch_rows(const GdnArgs& a, hipStream_t s) {
+  const dim3 grid((unsigned)((a.Dv + 7) / 8), (unsigned)a.Hv, (unsigned)a.B);
+  switch (a.Dk) {
+    case 32: hipLaunchKernelGGL((gated_delta_row_kernel<X, 1, NORM>), grid, dim3(256), 0, s, a); return true;
+    case 64: hipLaunchKernelGGL((gated_delta_row_kernel<X, 2, NORM>), grid, dim3(256), 0, s, a); return true;
+    case 128: hipLaunchKernelGGL((gated_delta_row_kernel<X, 4, NORM>), grid, dim3(256), 0, s, a); return true;
+    case 256: hipLaunchKernelGGL((gated_delta_row_kernel<X, 8, NORM>), grid, dim3(256), 0, s, a); return true;
+    default: return false;
+  }
+}
+
+template <class X, bool NORM>
+bool launch_chunks(const GdnArgs& a, hipStream_t s) {
+  const dim3 grid((unsigned)((a.Dv + kRows - 1) / kRows), (unsigned)a.Hv, (unsigned)a.B);
+  switch (a.Dk) {
+    case 32: hipLaunchKernelGGL((gated_delta_chunk_kernel<X, 2, NORM>), grid, dim3(256), 0, s, a); return true;
+    case 64: hipLaunchKernelGGL((gated_delta_chunk_kernel<X, 4, NORM>), grid, dim3(256), 0, s, a); return true;
+    case 128: hipLaunchKernelGGL((gated_delta_chunk_kernel<X, 8, NORM>), grid, dim3(256), 0, s, a); return true;
+    case 256: hipLaunchKernelGGL((gated_delta_chunk_kernel<X, 16, NORM>), grid, dim3(256), 0, s, a); return true;
+    default: return false;
+  }
+}
+
+// Steps per call up to which the barrier-free decode kernel runs.
+constexpr int64_t kDecodeMaxSteps = 2;
+
+template <class X, bool NORM>
+bool launch_x(const GdnArgs& a, hipStream_t s, bool aligned) {
+  if (!aligned) return launch_rows<X, NORM>(a, s);
+  if (a.T == 1) return launch_token<X, NORM>(a, s);
+  return a.T <= kDecodeMaxSteps ? launch_decode<X, NORM>(a, s) : launch_chunks<X, NORM>(a, s);
 }
 
 }  // namespace
@@ -188,20 +784,24 @@ extern "C" int hgk_gated_delta(int dtype, const void* q, const void* k, const vo
   if (!(eps >= 0.0f)) return fail(HGK_ERR_ARG, "%s: eps must be >= 0", fn);
   if (!q || !k || !v || !a_log || !a || !dt_bias || !b || !y || !state_out)
     return fail(HGK_ERR_ARG, "%s: null pointer", fn);
-  if (batch * v_heads > 65535) return fail(HGK_ERR_UNSUPPORTED, "%s: batch * v_heads > 65535", fn);
+  if (batch > 65535 || v_heads > 65535) return fail(HGK_ERR_UNSUPPORTED, "%s: batch or v_heads > 65535", fn);
   if (batch == 0) return HGK_OK;
   GdnArgs g{};
   g.q = q; g.k = k; g.v = v; g.a_log = a_log; g.a = a; g.dt_bias = dt_bias; g.b = b;
   g.state_in = state_in; g.qw = q_norm_w; g.kw = k_norm_w; g.pdt = param_dtype; g.eps = eps;
   g.inv_dk = (float)(1.0 / (double)head_k_dim);
   g.B = batch; g.T = seq_len; g.Hk = k_heads; g.Dk = head_k_dim; g.Hv = v_heads; g.Dv = head_v_dim;
+  g.hgrp = (int)(v_heads / k_heads);
   g.y = y; g.state_out = state_out;
   const hipStream_t s = as_stream(stream);
   const bool norm = q_norm_w != nullptr;
+  // the chunked kernel loads q, k and state rows with 4- to 16-byte vector loads
+  auto al = [](const void* p) { return p == nullptr || ((uintptr_t)p & 15u) == 0; };
+  const bool aligned = al(q) && al(k) && al(state_in) && al(state_out);
   bool ok;
-  if (dtype == DT_BF16) ok = norm ? launch_x<BF16, true>(g, s) : launch_x<BF16, false>(g, s);
-  else if (dtype == DT_F16) ok = norm ? launch_x<F16, true>(g, s) : launch_x<F16, false>(g, s);
-  else ok = norm ? launch_x<F32, true>(g, s) : launch_x<F32, false>(g, s);
+  if (dtype == DT_BF16) ok = norm ? launch_x<BF16, true>(g, s, aligned) : launch_x<BF16, false>(g, s, aligned);
+  else if (dtype == DT_F16) ok = norm ? launch_x<F16, true>(g, s, aligned) : launch_x<F16, false>(g, s, aligned);
+  else ok = norm ? launch_x<F32, true>(g, s, aligned) : launch_x<F32, false>(g, s, aligned);
   if (!ok) return fail(HGK_ERR_UNSUPPORTED, "%s: head_k_dim not supported", fn);
   return launch_status(fn);
 }

@@ -259,7 +259,10 @@ int hgk_gather_qmm(int dtype, const void* x, int64_t x_rows, int64_t x_row_strid
  * state_out [B, Hv, Dv, Dk] in `dtype` (state_in NULL: zeros; state_out may be
  * state_in). Value head hv reads key head hv / (Hv / Hk). The state is f32
  * inside a call and rounded to `dtype` at its end, as in the reference.
- * head_k_dim in {32, 64, 128, 256}; batch * v_heads <= 65535.
+ * head_k_dim in {32, 64, 128, 256}; batch <= 65535 and v_heads <= 65535.
+ * With q, k and the state 16-byte aligned a vectorised kernel runs (one
+ * token per call, a few tokens, or 16-step chunks staged in LDS); otherwise a
+ * per-row kernel of the same arithmetic.
  */
 int hgk_gated_delta(int dtype, const void* q, const void* k, const void* v, const void* a_log,
                     const void* a, const void* dt_bias, const void* b, int param_dtype,

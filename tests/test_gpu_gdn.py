@@ -70,9 +70,9 @@ def _check(got, ref, dt, what):
         assert ef >= 0.99, what
 
 
-@pytest.mark.parametrize("shape", [(1, 1, 1, 32, 1, 32), (1, 1, 2, 32, 4, 32), (1, 3, 2, 32, 4, 32),
-                                   (1, 1, 16, 128, 32, 128)],
-                         ids=["Hk=Hv=1", "gqa", "T=3 gqa", "model dims"])
+@pytest.mark.parametrize("shape", [(1, 1, 1, 32, 1, 32), (1, 1, 2, 32, 4, 32), (1, 2, 2, 32, 4, 32),
+                                   (1, 3, 2, 32, 4, 32), (1, 1, 16, 128, 32, 128)],
+                         ids=["Hk=Hv=1", "gqa", "T=2 gqa", "T=3 gqa", "model dims"])
 def test_matches_oracle_f32_reference_cases(dev, shape):
     """The reference's own kernel-vs-ops cases (qwen3_next.rs:2489-2512)."""
     inp = _inputs(2600 + sum(shape), *shape, O.F32)
@@ -91,17 +91,39 @@ def test_qwen3_next_decode_bf16_with_norm(dev):
     _check(s, rs, O.BF16, "decode state")
 
 
-def test_decode_steps_chain_state_through_bf16(dev):
+def test_two_token_decode_bf16_with_norm(dev):
+    """Two tokens per call (a speculative-decode shape) on the decode kernel,
+    model dims, ragged Dv."""
+    inp = _inputs(2705, 8, 2, 16, 128, 32, 100, O.BF16)
+    y, s = _run(dev, inp, O.BF16, norm=True)
+    ry, rs = _oracle(inp, O.BF16, norm=True)
+    _check(y, ry, O.BF16, "2-token y")
+    _check(s, rs, O.BF16, "2-token state")
+
+
+@pytest.mark.parametrize("norm", [True, False], ids=["qk-norm", "raw-qk"])
+def test_decode_steps_chain_state_through_bf16(dev, norm):
     """Token by token (T = 1 per call, the state stored in bf16 between calls,
     as the reference's cache holds it). Each step is checked against the
-    oracle run from the device's own previous state, at the 1-ulp bar. The
-    two chains are also compared end to end: a state value that sits on a
-    bf16 rounding tie can round either way in one step and the difference
-    then feeds every later step, so after 6 steps the bar is a stated
-    |diff| <= 2e-2 (y and state values are O(0.1-1))."""
+    oracle run from the device's own previous state, at the 1-ulp bar.
+
+    With the model's q/k norm (|k|^2 = 1, so the delta-rule map
+    s -> s (1 - beta k k^T) is contractive) the device chain is also compared
+    with the oracle's own chain end to end: a state value on a bf16 rounding
+    tie can round either way in one step, and the bar for that after 6 steps
+    is a stated |diff| <= 2e-3 (a few bf16 ulps at state magnitude 0.1). With
+    raw q/k (|k|^2 ~ Dk / 3) the map expands, |y| grows to ~40 within 6 steps
+    and y is a cancellation of terms far larger than itself, so an end-to-end
+    bar says nothing there; that case is checked step by step only."""
     shape = (4, 6, 4, 128, 8, 64)
     inp = _inputs(2711, *shape, O.BF16)
-    T = shape[1]
+    T, Dk = shape[1], shape[3]
+    kw, okw = {}, {}
+    if norm:
+        wq, wk = H.gdn_qk_norm_weights(Dk, torch.bfloat16, dev)
+        kw = dict(q_norm_w=wq, k_norm_w=wk)
+        owq, owk = O.gdn_qk_norm_weights(Dk, O.BF16)
+        okw = dict(qw=owq, kw=owk)
     st_dev = to_dev(inp["state"], O.BF16, dev)
     st_chain = inp["state"]
     d = _dev(inp, O.BF16, dev)
@@ -109,18 +131,20 @@ def test_decode_steps_chain_state_through_bf16(dev):
         sl = lambda x: x[:, t:t + 1].contiguous()
         st_prev = to_host(st_dev)
         y, st_dev = H.gated_delta(sl(d["q"]), sl(d["k"]), sl(d["v"]), d["a_log"], sl(d["a"]),
-                                  d["dt_bias"], sl(d["b"]), st_dev)
+                                  d["dt_bias"], sl(d["b"]), st_dev, **kw)
         one = {n: inp[n][:, t:t + 1] for n in ("q", "k", "v", "a", "b")}
         args = (one["q"], one["k"], one["v"], inp["a_log"], one["a"], inp["dt_bias"], one["b"], O.BF16)
-        ry, rs = O.gated_delta(*args, state=st_prev)
+        ry, rs = O.gated_delta(*args, state=st_prev, **okw)
         _check(to_host(y), ry, O.BF16, f"step {t} y")
         _check(to_host(st_dev), rs, O.BF16, f"step {t} state")
-        cy, st_chain = O.gated_delta(*args, state=st_chain)
-        diff = np.abs(O.to_f32(to_host(y), O.BF16) - O.to_f32(cy, O.BF16)).max()
-        assert diff <= 2e-2, f"step {t}: chains apart by {diff}"
-    diff = np.abs(O.to_f32(to_host(st_dev), O.BF16) - O.to_f32(st_chain, O.BF16)).max()
-    print(f"[gdn] chain state after {T} steps: max|diff|={diff:.2e}", flush=True)
-    assert diff <= 2e-2
+        if norm:
+            cy, st_chain = O.gated_delta(*args, state=st_chain, **okw)
+            diff = np.abs(O.to_f32(to_host(y), O.BF16) - O.to_f32(cy, O.BF16)).max()
+            assert diff <= 2e-3, f"step {t}: y chains apart by {diff}"
+    if norm:
+        diff = np.abs(O.to_f32(to_host(st_dev), O.BF16) - O.to_f32(st_chain, O.BF16)).max()
+        print(f"[gdn] chain state after {T} steps: max|diff|={diff:.2e}", flush=True)
+        assert diff <= 2e-3
 
 
 @pytest.mark.parametrize("Dk,Dv", [(32, 36), (64, 64), (256, 128)])
@@ -146,3 +170,26 @@ def test_zero_state_and_in_place_state(dev):
     assert s2.data_ptr() == st.data_ptr()
     ry2, rs2 = _oracle(inp, O.BF16)
     _check(to_host(s2), rs2, O.BF16, "in-place state")
+
+
+def test_unaligned_inputs_take_the_per_row_kernel(dev):
+    """q, k and the state at an odd element offset (not 16-byte aligned): the
+    per-row kernel runs them, to the same bar."""
+    shape = (2, 5, 2, 64, 4, 48)
+    inp = _inputs(2741, *shape, O.BF16)
+    d = _dev(inp, O.BF16, dev)
+
+    def shifted(t):
+        buf = torch.empty(t.numel() + 1, dtype=t.dtype, device=dev)
+        v = buf[1:].view(t.shape)
+        v.copy_(t)
+        return v
+
+    q, k, st = shifted(d["q"]), shifted(d["k"]), shifted(d["state"])
+    assert q.data_ptr() % 16 != 0
+    wq, wk = H.gdn_qk_norm_weights(64, torch.bfloat16, dev)
+    y, s = H.gated_delta(q, k, d["v"], d["a_log"], d["a"], d["dt_bias"], d["b"], st,
+                         q_norm_w=wq, k_norm_w=wk)
+    ry, rs = _oracle(inp, O.BF16, norm=True)
+    _check(to_host(y), ry, O.BF16, "unaligned y")
+    _check(to_host(s), rs, O.BF16, "unaligned state")
