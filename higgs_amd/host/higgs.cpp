@@ -815,6 +815,54 @@ Array nn::SwitchMlpWeights::forward_gather(const Array& x, const Array& indices)
   return d.reshape({T, top_k, d.dim(1)});
 }
 
+// ------------------------------------------------------------------ gated delta
+std::pair<Array, Array> gated_delta(const Array& q, const Array& k, const Array& v,
+                                    const Array& a_log, const Array& a, const Array& dt_bias,
+                                    const Array& b, const Array* state_in, const Array* q_norm_w,
+                                    const Array* k_norm_w, float eps) {
+  const char* op = "gated_delta";
+  Operands ops = {{"q", &q},   {"k", &k}, {"v", &v},         {"a_log", &a_log},
+                  {"a", &a},   {"dt_bias", &dt_bias},        {"b", &b},
+                  {"state", state_in}, {"q_norm_w", q_norm_w}, {"k_norm_w", k_norm_w}};
+  if (q.ndim() != 4 || k.shape() != q.shape() || v.ndim() != 4 || a.ndim() != 3 ||
+      b.shape() != a.shape())
+    fail(op, "q, k must be [B, T, Hk, Dk], v [B, T, Hv, Dv], a and b [B, T, Hv]", ops);
+  const int64_t B = q.dim(0), T = q.dim(1), Hk = q.dim(2), Dk = q.dim(3);
+  const int64_t Hv = v.dim(2), Dv = v.dim(3);
+  if (v.dim(0) != B || v.dim(1) != T || a.dim(0) != B || a.dim(1) != T || a.dim(2) != Hv)
+    fail(op, "batch, steps or v heads disagree", ops);
+  for (const Array* t : {&q, &k, &v, &a, &b})
+    if (!t->is_contiguous() || t->dtype() != q.dtype())
+      fail(op, "q, k, v, a, b must be contiguous and share a dtype", ops);
+  if (a_log.size() != Hv || dt_bias.size() != Hv || a_log.dtype() != dt_bias.dtype() ||
+      !a_log.is_contiguous() || !dt_bias.is_contiguous())
+    fail(op, "a_log and dt_bias must be contiguous [Hv] of one dtype", ops);
+  if (state_in && (state_in->shape() != Shape({B, Hv, Dv, Dk}) || !state_in->is_contiguous() ||
+                   state_in->dtype() != q.dtype()))
+    fail(op, "state must be contiguous [B, Hv, Dv, Dk] in q's dtype", ops);
+  if ((q_norm_w == nullptr) != (k_norm_w == nullptr)) fail(op, "pass both norm weights or neither", ops);
+  if (q_norm_w && (q_norm_w->size() != Dk || k_norm_w->size() != Dk ||
+                   q_norm_w->dtype() != q.dtype() || k_norm_w->dtype() != q.dtype() ||
+                   !q_norm_w->is_contiguous() || !k_norm_w->is_contiguous()))
+    fail(op, "norm weights must be contiguous [Dk] in q's dtype", ops);
+  Array y = Array::empty({B, T, Hv, Dv}, q.dtype());
+  Array st = Array::empty({B, Hv, Dv, Dk}, q.dtype());
+  if (B == 0) return {y, st};
+  check(hgk_gated_delta(static_cast<int>(q.dtype()), q.data(), k.data(), v.data(), a_log.data(),
+                        a.data(), dt_bias.data(), b.data(), static_cast<int>(a_log.dtype()),
+                        state_in ? state_in->data() : nullptr,
+                        q_norm_w ? q_norm_w->data() : nullptr, k_norm_w ? k_norm_w->data() : nullptr,
+                        eps, B, T, Hk, Dk, Hv, Dv, y.data(), st.data(), stream_arg()),
+        op, ops);
+  return {y, st};
+}
+
+std::pair<Array, Array> gdn_qk_norm_weights(int64_t head_k_dim, Dtype dt) {
+  const float s = 1.0f / std::sqrt(static_cast<float>(head_k_dim));
+  std::vector<float> wq(head_k_dim, s * s), wk(head_k_dim, s);
+  return {Array::from_slice(wq, {head_k_dim}, dt), Array::from_slice(wk, {head_k_dim}, dt)};
+}
+
 // ------------------------------------------------------------------ checkpoints
 namespace io {
 

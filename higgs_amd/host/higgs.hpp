@@ -267,6 +267,21 @@ Array gather_qmm(const Array& x, const Array& w, const Array& scales, const Arra
                  const Array& rhs_indices, bool transpose, int group_size, int bits,
                  int64_t x_row_div = 1, const Array* lhs_indices = nullptr);
 
+// gated_delta_kernel_ffi(q, k, v, a_log, a, dt_bias, b, state_in, ...)
+// (qwen3_next.rs:559-630): the GatedDeltaNet recurrence over T steps, q/k
+// [B, T, Hk, Dk], v [B, T, Hv, Dv], a/b [B, T, Hv], a_log/dt_bias [Hv],
+// state_in [B, Hv, Dv, Dk] (nullptr: zeros). With q_norm_w/k_norm_w the
+// constant-weight q/k rms_norm in front of it (qwen3_next.rs:1172-1173) runs
+// in the same kernel. Returns (y [B, T, Hv, Dv], state_out).
+std::pair<Array, Array> gated_delta(const Array& q, const Array& k, const Array& v,
+                                    const Array& a_log, const Array& a, const Array& dt_bias,
+                                    const Array& b, const Array* state_in,
+                                    const Array* q_norm_w = nullptr,
+                                    const Array* k_norm_w = nullptr, float eps = 1e-6f);
+// Those constant weights: (s * s, s) with s = 1/sqrt(head_k_dim) in f32
+// (qwen3_next.rs:1075-1094), cast to dt as at 1165-1169.
+std::pair<Array, Array> gdn_qk_norm_weights(int64_t head_k_dim, Dtype dt);
+
 // Checkpoint loading (crates/higgs-models/src/lib.rs:574-723): safetensors
 // files in the MLX 4-bit layout, read through the library's reader.
 namespace io {

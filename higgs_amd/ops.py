@@ -343,7 +343,7 @@ def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: t
 
 # ---------------------------------------------------------------- GatedDeltaNet
 def gdn_qk_norm_weights(head_k_dim: int, dtype: torch.dtype, device):
-    """GatedDeltaNet's constant q/k norm weights (qwen3_next.rs:1111-1130):
+    """GatedDeltaNet's constant q/k norm weights (qwen3_next.rs:1075-1094, cast to the input dtype at 1165-1169):
     s = 1/sqrt(Dk) in f32; q's weight is s*s, k's is s, cast to `dtype`."""
     s = torch.tensor(1.0, dtype=torch.float32) / torch.sqrt(torch.tensor(float(head_k_dim)))
     wq = torch.full((head_k_dim,), float(s * s), dtype=torch.float32).to(dtype)

@@ -234,7 +234,7 @@ def gated_delta(q, k, v, a_log, a, dt_bias, b, dt, *, p_dt=F32, state=None, qw=N
 
 
 def gdn_qk_norm_weights(Dk: int, dt: int):
-    """The constant q/k norm weights of GatedDeltaNet (qwen3_next.rs:1111-1130):
+    """The constant q/k norm weights of GatedDeltaNet (qwen3_next.rs:1075-1094):
     s = 1/sqrt(Dk) in f32; q's weight is s*s, k's is s, each cast to dt."""
     s = np.float32(1.0) / np.sqrt(np.float32(Dk))
     return (from_f32(np.full(Dk, s * s, np.float32), dt), from_f32(np.full(Dk, s, np.float32), dt))

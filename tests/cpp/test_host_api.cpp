@@ -16,6 +16,7 @@
 #include <functional>
 #include <map>
 #include <string>
+#include <tuple>
 #include <vector>
 
 #include <unistd.h>
@@ -555,6 +556,80 @@ TEST(test_switch_mlp_forward_gather) {
   ASSERT(or_gather_qmm(OR_BF16, actb.data(), P, I, 1, nullptr, dm.w.data(), dm.s.data(), dm.b.data(), OR_BF16, E, D,
                        I, 64, idx.data(), P, want_d.data(), D) == 0, "oracle down");
   check_close(y.to_bits(), want_d, "down");
+}
+
+// The reference's gated-delta kernel tests (qwen3_next.rs:1700-1722,
+// 2421-2450): all-ones q, k, v and a, zero a_log, dt_bias, b and state, Hk 2,
+// Hv 4, Dk = Dv = 32, f32. One step gives delta = 1/2, s = 1/2 everywhere and
+// y = 32 / 2 = 16 exactly; a second step from that state equals the oracle's,
+// and one two-step call equals two one-step calls (sequential dependence).
+// Then Qwen3-Next's decode shape in bf16 with the fused q/k norm against the
+// oracle (1 ulp, atol 1e-3).
+TEST(test_gated_delta_reference_cases_and_decode) {
+  const int64_t B = 1, Hk = 2, Dk = 32, Hv = 4, Dv = 32;
+  auto ones = [](int64_t n) { return std::vector<float>(n, 1.0f); };
+  auto zeros = [](int64_t n) { return std::vector<float>(n, 0.0f); };
+  auto f32 = [](const std::vector<float>& v, const Shape& s) { return Array::from_slice(v, s); };
+  for (int64_t T : {1, 2}) {
+    Array q = f32(ones(B * T * Hk * Dk), {B, T, Hk, Dk});
+    Array v = f32(ones(B * T * Hv * Dv), {B, T, Hv, Dv});
+    Array a = f32(ones(B * T * Hv), {B, T, Hv}), b = f32(zeros(B * T * Hv), {B, T, Hv});
+    Array al = f32(zeros(Hv), {Hv}), db = f32(zeros(Hv), {Hv});
+    Array s0 = f32(zeros(B * Hv * Dv * Dk), {B, Hv, Dv, Dk});
+    auto [y, s] = higgs::gated_delta(q, q, v, al, a, db, b, &s0);
+    ASSERT(y.shape() == Shape({B, T, Hv, Dv}) && s.shape() == Shape({B, Hv, Dv, Dk}), "%s",
+           y.describe().c_str());
+    auto yv = y.to_f32();
+    for (int64_t i = 0; i < Hv * Dv; ++i) ASSERT(yv[i] == 16.0f, "T=%lld y[%lld] = %g", (long long)T, (long long)i, yv[i]);
+    // the oracle on the same inputs
+    std::vector<float> oy(B * T * Hv * Dv), os(B * Hv * Dv * Dk);
+    auto qh = ones(B * T * Hk * Dk), vh = ones(B * T * Hv * Dv), ah = ones(B * T * Hv), bh = zeros(B * T * Hv);
+    auto alh = zeros(Hv), sh = zeros(B * Hv * Dv * Dk);
+    ASSERT(or_gated_delta(OR_F32, qh.data(), qh.data(), vh.data(), alh.data(), ah.data(), alh.data(), bh.data(),
+                          OR_F32, sh.data(), nullptr, nullptr, 1e-6f, B, T, Hk, Dk, Hv, Dv, oy.data(), os.data()) == 0,
+           "oracle");
+    for (size_t i = 0; i < oy.size(); ++i)
+      ASSERT(std::fabs(yv[i] - oy[i]) <= 1e-4f * std::max(1.0f, std::fabs(oy[i])), "T=%lld y[%zu] %g vs %g",
+             (long long)T, i, yv[i], oy[i]);
+    if (T == 1) {
+      // state passthrough: a second one-step call from s equals the T = 2 run
+      auto [y2, s2] = higgs::gated_delta(q, q, v, al, a, db, b, &s);
+      Array q2 = f32(ones(B * 2 * Hk * Dk), {B, 2, Hk, Dk}), v2 = f32(ones(B * 2 * Hv * Dv), {B, 2, Hv, Dv});
+      Array a2 = f32(ones(B * 2 * Hv), {B, 2, Hv}), b2 = f32(zeros(B * 2 * Hv), {B, 2, Hv});
+      auto [yy, ss] = higgs::gated_delta(q2, q2, v2, al, a2, db, b2, &s0);
+      auto y2v = y2.to_f32(), yyv = yy.to_f32(), s2v = s2.to_f32(), ssv = ss.to_f32();
+      ASSERT(y2v[0] != 16.0f, "the second step must see the first step's state");
+      for (int64_t i = 0; i < Hv * Dv; ++i)
+        ASSERT(std::fabs(y2v[i] - yyv[Hv * Dv + i]) <= 1e-5f * std::fabs(yyv[Hv * Dv + i]), "step 2 y[%lld]", (long long)i);
+      for (size_t i = 0; i < s2v.size(); ++i)
+        ASSERT(std::fabs(s2v[i] - ssv[i]) <= 1e-5f * std::max(1.0f, std::fabs(ssv[i])), "step 2 state[%zu]", i);
+    }
+  }
+  // Qwen3-Next decode: 8 sequences, Hk 16, Dk 128, Hv 32, Dv 128, bf16, fused norm
+  const int64_t Bd = 8, Hkd = 16, Dkd = 128, Hvd = 32, Dvd = 128;
+  auto bq = bits_of(uniform(9500, Bd * Hkd * Dkd, -1, 1), OR_BF16), bk = bits_of(uniform(9501, Bd * Hkd * Dkd, -1, 1), OR_BF16);
+  auto bv = bits_of(uniform(9502, Bd * Hvd * Dvd, -1, 1), OR_BF16);
+  auto ba = bits_of(uniform(9503, Bd * Hvd, -1, 1), OR_BF16), bb = bits_of(uniform(9504, Bd * Hvd, -1, 1), OR_BF16);
+  auto bs = bits_of(uniform(9505, Bd * Hvd * Dvd * Dkd, -0.1f, 0.1f), OR_BF16);
+  auto alog = uniform(9506, Hvd, -1, 0), dtb = uniform(9507, Hvd, -0.5f, 0.5f);
+  auto [wq, wk] = higgs::gdn_qk_norm_weights(Dkd, Dtype::Bfloat16);
+  Array st = dev16(bs, {Bd, Hvd, Dvd, Dkd}, Dtype::Bfloat16);
+  Array al = f32(alog, {Hvd}), db = f32(dtb, {Hvd});
+  auto [y, s] = higgs::gated_delta(dev16(bq, {Bd, 1, Hkd, Dkd}, Dtype::Bfloat16), dev16(bk, {Bd, 1, Hkd, Dkd}, Dtype::Bfloat16),
+                                   dev16(bv, {Bd, 1, Hvd, Dvd}, Dtype::Bfloat16), al, dev16(ba, {Bd, 1, Hvd}, Dtype::Bfloat16),
+                                   db, dev16(bb, {Bd, 1, Hvd}, Dtype::Bfloat16), &st, &wq, &wk);
+  auto wqb = wq.to_bits(), wkb = wk.to_bits();
+  std::vector<uint16_t> oy(Bd * Hvd * Dvd), os(bs.size());
+  ASSERT(or_gated_delta(OR_BF16, bq.data(), bk.data(), bv.data(), alog.data(), ba.data(), dtb.data(), bb.data(), OR_F32,
+                        bs.data(), wqb.data(), wkb.data(), 1e-6f, Bd, 1, Hkd, Dkd, Hvd, Dvd, oy.data(), os.data()) == 0,
+         "oracle decode");
+  for (auto [got, want, what] : {std::tuple{y.to_bits(), oy, "y"}, std::tuple{s.to_bits(), os, "state"}}) {
+    std::vector<float> gf(got.size()), wf(want.size());
+    or_convert_to_f32(OR_BF16, got.data(), gf.data(), static_cast<int64_t>(got.size()));
+    or_convert_to_f32(OR_BF16, want.data(), wf.data(), static_cast<int64_t>(want.size()));
+    for (size_t i = 0; i < got.size(); ++i)
+      ASSERT(ulp16(got[i], want[i]) <= 1 || std::fabs(gf[i] - wf[i]) <= 1e-3f, "%s[%zu] %g vs %g", what, i, gf[i], wf[i]);
+  }
 }
 
 // ---------------------------------------------------------------- checkpoints
