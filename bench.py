@@ -25,6 +25,7 @@ import sys
 import time
 
 PEAK_HBM_GBS = 8000.0
+PEAK_BF16_TFLOPS = 2500.0  # dense bf16 MFMA, MI355X
 BF16, F32, F16, U32, I32 = 1, 0, 2, 3, 4
 SILU, GELU = 0, 1
 
@@ -46,8 +47,9 @@ class Kernel:
     back to torch's caching allocator, and graph capture (which empties that
     cache) would unmap it under the launches."""
 
-    def __init__(self, name, nbytes, fn, argsets, tokens=0, keep=(), cpu=None):
+    def __init__(self, name, nbytes, fn, argsets, tokens=0, keep=(), cpu=None, flops=0):
         self.name, self.bytes, self.fn, self.tokens = name, nbytes, fn, tokens
+        self.flops = flops  # MFMA-bound kernels: algorithmic flops per launch
         self.argsets = [tuple(a) for a in argsets]
         self.keep = keep
         self.cpu = cpu  # (kind, params) for the oracle's timing of the same op
@@ -345,6 +347,39 @@ def wl_qwen3_next_moe_decode(cx):
     return Workload("qwen3_next_moe_decode", cfg, ks, ns, T)
 
 
+def k_qlinear(cx, name, sets, M, N, K, group=64):
+    """quantized_matmul x [M, K] . W^T (W [N, K] 4-bit group 64): bytes =
+    weights + scales/biases + x + y; flops = 2 M N K."""
+    nbytes = N * K // 2 + 2 * N * (K // group) * 2 + M * K * 2 + M * N * 2
+    args = [(BF16, _vp(x), M, K, _vp(wq), _vp(sc), _vp(bi), BF16, N, K, group, 4, _vp(y), N,
+             cx.stream) for x, (wq, sc, bi), y in sets]
+    return Kernel(name, nbytes, cx.lib.hgk_quantized_matmul, args, M, keep=(sets,),
+                  cpu=("qlinear", dict(M=M, N=N, K=K, group=group)), flops=2 * M * N * K)
+
+
+def wl_qwen3_next_qlinear(cx):
+    """Qwen3-Next-80B-A3B GatedDeltaNet input projection in_proj_qkvz
+    (hidden 2048 -> 2 x 16 x 128 + 2 x 32 x 128 = 12288, 4-bit group 64) as
+    QLinear::forward runs it: a decode step of 64 sequences (M = 64; 24 weight
+    sets, ~340 MB, rotate so the weights stream from HBM) and a 4096-token
+    prefill (M = 4096, matrix-core bound)."""
+    torch = cx.torch
+    N, K = 12288, 2048
+    nd = 24
+    tabs = [tuple(t[0] for t in cx.qtable_experts(1, N, K)) for _ in range(nd)]
+    dec = [(cx.randn((64, K), torch.bfloat16), tabs[i], cx.empty((64, N), torch.bfloat16))
+           for i in range(nd)]
+    npf = 2
+    pre = [(cx.randn((4096, K), torch.bfloat16), tabs[i], cx.empty((4096, N), torch.bfloat16))
+           for i in range(npf)]
+    k_pre = k_qlinear(cx, "qlinear_prefill_4096", pre, 4096, N, K)
+    k_pre.argsets = [k_pre.argsets[i % npf] for i in range(nd)]
+    ks = [k_qlinear(cx, "qlinear_decode_64", dec, 64, N, K), k_pre]
+    cfg = {"workload": "qwen3-next-80b-a3b in_proj_qkvz quantized_matmul", "N": N, "K": K,
+           "quant": "4-bit g64", "decode_rows": 64, "prefill_rows": 4096, "weight_sets": nd}
+    return Workload("qwen3_next_qlinear", cfg, ks, nd, 64 + 4096)
+
+
 def k_gdn(cx, name, sets, wq, wk, alog, dtb, B, T, Hk, Dk, Hv, Dv):
     """Gated-delta recurrence with the fused q/k norm; bytes = state read and
     written once + q, k, v, a, b read + y written."""
@@ -504,6 +539,7 @@ WORKLOADS = {
     "block_boundary_add_rms_norm": wl_block_boundary,
     "qwen3_next_moe_decode": wl_qwen3_next_moe_decode,
     "qwen3_next_gdn": wl_qwen3_next_gdn,
+    "qwen3_next_qlinear": wl_qwen3_next_qlinear,
 }
 
 
@@ -614,6 +650,9 @@ def kernel_times(cx, wl, graph, per_group=20, groups=5):
                     "launches": groups * per_group, "method": "graph" if graph else "eager",
                     "gbs": k.bytes / (avg * 1e-3) / 1e9,
                     "frac_of_peak": k.bytes / (avg * 1e-3) / 1e9 / PEAK_HBM_GBS})
+        if k.flops:
+            per[-1]["tflops"] = k.flops / (avg * 1e-3) / 1e12
+            per[-1]["frac_of_mfma_peak"] = per[-1]["tflops"] / PEAK_BF16_TFLOPS
     return per
 
 
@@ -804,6 +843,16 @@ def cpu_op(spec, budget_s=1.0):
         fn = lambda: O.gather_qmm(x, B16, wq, sc, bi, B16, ex, group=G)
         nbytes = Pn * (N * K // 2 + 4 * N * (K // G) + 2 * K + 2 * N)
         rows, what = Pn, f"{Pn} (token, expert) pairs, distinct experts"
+    elif kind == "qlinear":
+        Ms = min(p["M"], 4)
+        N, K, group = p["N"], p["K"], p["group"]
+        x = O.from_f32(O.normal(7040, (Ms, K)), B16)
+        w = O.u32(7041, (N, K // 8))
+        sc = O.from_f32(O.uniform(7042, (N, K // group), 0.005, 0.02), B16)
+        bi = O.from_f32(O.uniform(7043, (N, K // group), -0.1, 0.1), B16)
+        fn = lambda: O.quantized_matmul(x, B16, w, sc, bi, B16, group=group)
+        nbytes = N * K // 2 + 2 * N * (K // group) * 2 + Ms * K * 2 + Ms * N * 2
+        rows, what = Ms, f"{Ms} rows x {N} x {K} (f64 contraction)"
     elif kind == "gdn":
         Bs = min(p["B"], 4)
         Ts = min(p["T"], 16)

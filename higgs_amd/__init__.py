@@ -1,11 +1,13 @@
 """higgs_amd -- MI355X (gfx950) HIP kernels for the per-layer ops of
 panbanda/higgs' higgs-models (RMSNorm variants, RoPE variants, SwiGLU/GeGLU,
-the Qwen3-Next gated norm, the 4-bit QuantizedEmbedding gather and the fused
-residual-add + RMSNorm and embedding + RMSNorm forms), exposed
+the Qwen3-Next gated norm, the 4-bit QuantizedEmbedding gather, the fused
+residual-add + RMSNorm and embedding + RMSNorm forms, the 4-bit
+quantized_matmul / gather_qmm projections and the GatedDeltaNet recurrence),
+exposed
 through the C ABI in include/higgs_hip.h and mirrored here for Python callers.
 """
 from ._lib import HgkError, LIB_PATH, lib  # noqa: F401
 from .ops import (QuantizedEmbedding, add_rms_norm, gated_rms_norm, gelu_approximate_mul,  # noqa: F401
                   fused_gate_up_swiglu, gather_qmm, gated_delta, gdn_qk_norm_weights,
-                  llama3_rope_freqs, qk_norm_rope, rms_norm, rope,
+                  llama3_rope_freqs, qk_norm_rope, quantized_matmul, rms_norm, rope,
                   rope_inv_freq, silu_mul, swiglu)

@@ -1,0 +1,30 @@
+// qgemm.h -- the MFMA quantized matmul (qgemm.hip) as used by the
+// quantized_matmul entry point (qmm.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace hgk {
+
+struct QgemmArgs {
+  const uint16_t* x;
+  int64_t xs;         // x row stride (elements, a multiple of 8)
+  const uint32_t* w;  // [N, K/8]
+  const uint16_t* sc; // [N, K/64]
+  const uint16_t* bi;
+  int64_t M, N, K;
+  uint16_t* y;
+  int64_t ys;         // y row stride (elements)
+};
+
+// Rows of x at or above which the MFMA kernel runs (below: one GEMV per row).
+constexpr int64_t kQgemmMinRows = 16;
+
+// bf16 activations and scales, group 64, 4 bits, x 16-byte aligned with a
+// row stride that is a multiple of 8, w 8-byte aligned.
+bool qgemm_supported(int dtype, int sdt, int group_size, int bits, const void* x, int64_t xs,
+                     const void* w, int64_t k);
+void qgemm_launch(const QgemmArgs& a, hipStream_t s);
+
+}  // namespace hgk

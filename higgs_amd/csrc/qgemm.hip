@@ -1,0 +1,375 @@
+// qgemm.hip -- quantized_matmul(x, w, scales, biases, transpose = true, 64, 4)
+// on gfx950 MFMA: QLinear::forward (crates/higgs-models/src/qwen3_next.rs:
+// 174-221), y[m, n] = sum_k x[m, k] * (s[n, k/64] * q[n, k] + b[n, k/64]),
+// with w [N, K/8] u32 (8 codes per word, low nibble first) and scales/biases
+// [N, K/64] in the activation dtype (bf16).
+//
+// Exact products, one group at a time. A code q enters the matrix core as
+// the bf16 number 128 + q (two bit operations per pair of codes), x as
+// itself, so every product x * (128 + q) is exact and the MFMA sums them in
+// f32. Per 64-code group g the block has C_g[m, n] = sum x (128 + q) and the
+// row sums Sx_g[m] = sum x, and the affine part is applied once per group in
+// f32:   acc += s[n, g] * C_g + (b[n, g] - 128 s[n, g]) * Sx_g[m].
+// No weight is ever rounded to bf16, so the result is the exact contraction
+// up to f32 summation error, rounded to bf16 once at the end.
+//
+// Layout: a block computes BM x 128 of y with 4 waves (2 x 2), each a
+// (BM/2) x 64 tile of 16 x 16 MFMA tiles (v_mfma_f32_16x16x32_bf16: lane l
+// supplies row l%16 of A and column l%16 of B, 8 k-values each; it receives
+// rows 4(l/16)+r of column l%16). The k-order inside an MFMA is free as long
+// as A and B agree: lane group j = l/16 supplies, for the two MFMAs of a
+// group, words 2j and 2j+1 of the group's 8 code words (16 consecutive k).
+// So a lane's B operand is read straight from global memory as one 8-byte
+// load per column and group (no LDS), and x is staged in LDS as it is,
+// together with its per-group row sums (dot products with ones). The x tile
+// is double-buffered in LDS (one barrier per group) and the next group's x,
+// codes, scales and biases are loaded while the current group's MFMAs run.
+#include "../../include/higgs_hip.h"
+#include "hgk_common.h"
+#include "hgk_host.h"
+#include "qgemm.h"
+
+namespace hgk {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+
+constexpr int kQgBN = 128;   // output columns per block
+constexpr int kQgPitch = 72; // LDS row pitch of the x tile (64 + 8 elements)
+
+// 8 codes of one word (code i at bits 4i) -> the 8 bf16 values 128 + q_i in
+// order: the low and high nibbles of each byte are split apart, v_perm_b32
+// pairs byte j of each into one word, and the exponent bits of 128 are OR-ed
+// in.
+__device__ inline bf16x8_t expand_codes(uint32_t c) {
+  const uint32_t lo = c & 0x0f0f0f0fu;          // q0 q2 q4 q6
+  const uint32_t hi = (c >> 4) & 0x0f0f0f0fu;   // q1 q3 q5 q7
+  u32x4 v;
+  v[0] = __builtin_amdgcn_perm(hi, lo, 0x0c040c00u) | 0x43004300u;  // (q0, q1)
+  v[1] = __builtin_amdgcn_perm(hi, lo, 0x0c050c01u) | 0x43004300u;  // (q2, q3)
+  v[2] = __builtin_amdgcn_perm(hi, lo, 0x0c060c02u) | 0x43004300u;  // (q4, q5)
+  v[3] = __builtin_amdgcn_perm(hi, lo, 0x0c070c03u) | 0x43004300u;  // (q6, q7)
+  return __builtin_bit_cast(bf16x8_t, v);
+}
+
+typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
+
+__device__ inline float dot2_ones(uint32_t w, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_v, w),
+                                         __builtin_bit_cast(bf16x2_v, 0x3f803f80u), c, false);
+}
+
+// Sum of the 8 bf16 values of a 16-byte piece: four dot products with (1, 1).
+// The words are taken out of the vector one by one into plain registers
+// first (with the vector element feeding the builtin directly, this compiler
+// read the first word four times).
+__device__ inline float sum8_bf16(u32x4 v) {
+  uint32_t w0 = v[0], w1 = v[1], w2 = v[2], w3 = v[3];
+  asm volatile("" : "+v"(w0), "+v"(w1), "+v"(w2), "+v"(w3));
+  float s = dot2_ones(w0, 0.0f);
+  s = dot2_ones(w1, s);
+  s = dot2_ones(w2, s);
+  return dot2_ones(w3, s);
+}
+
+// Sum over the 8 lanes of a DPP half-row.
+__device__ inline float sum8_lanes(float v) {
+  v += u2f((uint32_t)__builtin_amdgcn_update_dpp(0, (int)f2u(v), 0xB1, 0xF, 0xF, true));
+  v += u2f((uint32_t)__builtin_amdgcn_update_dpp(0, (int)f2u(v), 0x4E, 0xF, 0xF, true));
+  v += u2f((uint32_t)__builtin_amdgcn_update_dpp(0, (int)f2u(v), 0x141, 0xF, 0xF, true));
+  return v;
+}
+
+template <int BM>
+__global__ __launch_bounds__(256) void qgemm_kernel(QgemmArgs a) {
+  constexpr int MT = BM / 32;          // 16-row MFMA tiles per wave
+  constexpr int NT = 4;                // 16-column MFMA tiles per wave
+  constexpr int XCH = BM * 8 / 256;    // 16-byte x chunks per thread per group
+  static_assert(XCH >= 1, "BM >= 32");
+  __shared__ __align__(16) uint16_t xs[2][BM][kQgPitch];
+  __shared__ __align__(16) float sx[2][BM];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int64_t m0 = (int64_t)blockIdx.y * BM, n0 = (int64_t)blockIdx.x * kQgBN;
+  const int KW = (int)(a.K / 8), G = (int)(a.K / 64);
+
+  // this thread's x chunks: chunk c = tid + 256 i -> row c / 8, word c % 8
+  const uint16_t* xrow[XCH];
+#pragma unroll
+  for (int i = 0; i < XCH; ++i) {
+    const int64_t r = m0 + (tid + 256 * i) / 8;
+    xrow[i] = a.x + (r < a.M ? r : a.M - 1) * a.xs + ((tid + 256 * i) & 7) * 8;
+  }
+  // this lane's weight columns (one per 16-column tile)
+  const uint32_t* wcol[NT];
+  const uint16_t* scol[NT];
+  const uint16_t* bcol[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const int64_t n = n0 + wn * 64 + t * 16 + l16;
+    const int64_t nc = n < a.N ? n : a.N - 1;
+    wcol[t] = a.w + nc * KW + 2 * lg;
+    scol[t] = a.sc + nc * G;
+    bcol[t] = a.bi + nc * G;
+  }
+
+  u32x4 xr[XCH];
+  u32x2_t wr[NT];
+  uint32_t sr[NT], br[NT];
+  auto fetch = [&](int g) {
+#pragma unroll
+    for (int i = 0; i < XCH; ++i) xr[i] = *reinterpret_cast<const u32x4*>(xrow[i] + g * 64);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      wr[t] = *reinterpret_cast<const u32x2_t*>(wcol[t] + g * 8);
+      sr[t] = scol[t][g];
+      br[t] = bcol[t][g];
+    }
+  };
+
+  f32x4_t acc[MT][NT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[i][t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+  fetch(0);
+  for (int g = 0; g < G; ++g) {
+    const int buf = g & 1;
+    // publish this group's x (permuted) and its row sums
+#pragma unroll
+    for (int i = 0; i < XCH; ++i) {
+      const int c = tid + 256 * i;
+      *reinterpret_cast<u32x4*>(&xs[buf][c / 8][(c & 7) * 8]) = xr[i];
+      const float s8 = sum8_lanes(sum8_bf16(xr[i]));
+      if ((c & 7) == 0) sx[buf][c / 8] = s8;
+    }
+    // this group's codes, scales and biases stay in registers for the MFMAs
+    bf16x8_t bw[NT][2];
+    float s[NT], bp[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      bw[t][0] = expand_codes(wr[t][0]);
+      bw[t][1] = expand_codes(wr[t][1]);
+      s[t] = BF16::lo(sr[t]);
+      bp[t] = BF16::lo(br[t]) - 128.0f * s[t];
+    }
+    __syncthreads();
+    if (g + 1 < G) fetch(g + 1);
+
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+      const int row = wm * (BM / 2) + i * 16;
+      const bf16x8_t a0 = *reinterpret_cast<const bf16x8_t*>(&xs[buf][row + l16][(2 * lg) * 8]);
+      const bf16x8_t a1 = *reinterpret_cast<const bf16x8_t*>(&xs[buf][row + l16][(2 * lg + 1) * 8]);
+      const f32x4_t sxr = *reinterpret_cast<const f32x4_t*>(&sx[buf][row + 4 * lg]);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        f32x4_t c = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, bw[t][0], c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, bw[t][1], c, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          acc[i][t][r] = __builtin_fmaf(s[t], c[r], __builtin_fmaf(bp[t], sxr[r], acc[i][t][r]));
+      }
+    }
+  }
+
+  // y: lane holds rows 4 lg + r of column l16 of each tile
+#pragma unroll
+  for (int i = 0; i < MT; ++i) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t m = m0 + wm * (BM / 2) + i * 16 + 4 * lg + r;
+      if (m >= a.M) continue;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const int64_t n = n0 + wn * 64 + t * 16 + l16;
+        if (n < a.N) a.y[m * a.ys + n] = (uint16_t)(BF16::pack(acc[i][t][r], 0.0f) & 0xffffu);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------- skinny
+// Few rows (M <= 64, the decode step of a batch): the weights are the whole
+// cost. A block is 16 waves over 64 columns: wave w takes column tile w % 4
+// and, of every 512-wide K chunk (8 groups), the two groups 2 (w / 4) and
+// 2 (w / 4) + 1, so a wave's share of the weights is small and all of it for
+// two chunks is in flight at once. x is staged in LDS per chunk, double
+// buffered (one barrier per chunk; the next chunk's x is loaded into
+// registers before the next weights and written to the other buffer after
+// the current chunk's MFMAs). The four group slices' partial sums meet in LDS
+// at the end.
+constexpr int kSkCG = 8;     // groups per chunk
+constexpr int kSkPitch = kSkCG * 64 + 8;
+
+// Per-lane weights of one chunk: codes of this wave's two groups for this
+// lane's column, and their two scales and biases.
+struct SkW {
+  u32x2_t w[2];
+  uint32_t s, b;
+};
+
+template <int MT>
+__global__ __launch_bounds__(1024) void qgemm_skinny_kernel(QgemmArgs a) {
+  constexpr int ROWS = 16 * MT;
+  constexpr int XCH = ROWS * 64 / 1024;  // 16-byte x pieces per thread per chunk
+  __shared__ __align__(16) uint16_t xs[2][ROWS][kSkPitch];
+  __shared__ __align__(16) float sx[2][kSkCG][ROWS];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nt = wave & 3, sl = wave >> 2;
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int64_t n = (int64_t)blockIdx.x * 64 + nt * 16 + l16;
+  const int64_t nc = n < a.N ? n : a.N - 1;
+  const int KW = (int)(a.K / 8), G = (int)(a.K / 64), NC = G / kSkCG;
+  const uint32_t* wcol = a.w + nc * KW + 2 * lg;
+  const uint16_t* scol = a.sc + nc * G;
+  const uint16_t* bcol = a.bi + nc * G;
+
+  auto fetch_w = [&](SkW& r, int c) {
+    const int g0 = c * kSkCG + 2 * sl;
+    r.w[0] = *reinterpret_cast<const u32x2_t*>(wcol + g0 * 8);
+    r.w[1] = *reinterpret_cast<const u32x2_t*>(wcol + (g0 + 1) * 8);
+    r.s = *reinterpret_cast<const uint32_t*>(scol + g0);
+    r.b = *reinterpret_cast<const uint32_t*>(bcol + g0);
+  };
+  // x pieces of one chunk: piece q = tid + 1024 i -> row q / 64, word q % 64
+  u32x4 xr[XCH];
+  auto load_x = [&](int c) {
+#pragma unroll
+    for (int i = 0; i < XCH; ++i) {
+      const int q = tid + 1024 * i, row = q >> 6, wd = q & 63;
+      const int64_t rr = row < a.M ? row : a.M - 1;
+      xr[i] = *reinterpret_cast<const u32x4*>(a.x + rr * a.xs + c * kSkCG * 64 + wd * 8);
+    }
+  };
+  auto stage = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < XCH; ++i) {
+      const int q = tid + 1024 * i, row = q >> 6, wd = q & 63;
+      *reinterpret_cast<u32x4*>(&xs[buf][row][wd * 8]) = xr[i];
+      const float s8 = sum8_lanes(sum8_bf16(xr[i]));
+      if ((wd & 7) == 0) sx[buf][wd >> 3][row] = s8;
+    }
+  };
+
+  f32x4_t acc[MT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i) acc[i] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+  auto compute = [&](const SkW& r, int buf) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int gi = 2 * sl + h;
+      uint32_t w0 = r.w[h][0], w1 = r.w[h][1];
+      asm volatile("" : "+v"(w0), "+v"(w1));
+      const bf16x8_t b0 = expand_codes(w0);
+      const bf16x8_t b1 = expand_codes(w1);
+      const float s = h ? BF16::hi(r.s) : BF16::lo(r.s);
+      const float bp = (h ? BF16::hi(r.b) : BF16::lo(r.b)) - 128.0f * s;
+      f32x4_t cc[MT];
+#pragma unroll
+      for (int i = 0; i < MT; ++i) {
+        const bf16x8_t a0 = *reinterpret_cast<const bf16x8_t*>(&xs[buf][i * 16 + l16][gi * 64 + (2 * lg) * 8]);
+        const bf16x8_t a1 = *reinterpret_cast<const bf16x8_t*>(&xs[buf][i * 16 + l16][gi * 64 + (2 * lg + 1) * 8]);
+        cc[i] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        cc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b0, cc[i], 0, 0, 0);
+        cc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1, cc[i], 0, 0, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < MT; ++i) {
+        const f32x4_t sxr = *reinterpret_cast<const f32x4_t*>(&sx[buf][gi][i * 16 + 4 * lg]);
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr)
+          acc[i][rr] = __builtin_fmaf(s, cc[i][rr], __builtin_fmaf(bp, sxr[rr], acc[i][rr]));
+      }
+      // the group's update completes here: without it the MFMAs of every
+      // group are issued first and all their results held at once
+#pragma unroll
+      for (int i = 0; i < MT; ++i) asm volatile("" : "+v"(acc[i]));
+    }
+  };
+
+  SkW ra, rb;
+  fetch_w(ra, 0);
+  if (NC > 1) fetch_w(rb, 1);
+  load_x(0);
+  stage(0);
+  for (int c = 0; c < NC; c += 2) {
+    // chunk c (buffer 0, weights ra)
+    __syncthreads();
+    if (c + 1 < NC) load_x(c + 1);
+    compute(ra, 0);
+    if (c + 2 < NC) fetch_w(ra, c + 2);
+    if (c + 1 < NC) stage(1);
+    if (c + 1 >= NC) break;
+    // chunk c + 1 (buffer 1, weights rb)
+    __syncthreads();
+    if (c + 2 < NC) load_x(c + 2);
+    compute(rb, 1);
+    if (c + 3 < NC) fetch_w(rb, c + 3);
+    if (c + 2 < NC) stage(0);
+  }
+
+  // the four group slices' partial sums: slices 1..3 through LDS to slice 0
+  __syncthreads();
+  float* red = reinterpret_cast<float*>(&xs[0][0][0]);  // 3 x 4 x MT*4 x 64 floats
+  static_assert(3 * 4 * MT * 4 * 64 * 4 <= (int)sizeof(xs), "reduction fits the x buffers");
+  if (sl > 0) {
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr)
+        red[(((sl - 1) * 4 + nt) * MT * 4 + i * 4 + rr) * 64 + lane] = acc[i][rr];
+  }
+  __syncthreads();
+  if (sl > 0 || n >= a.N) return;
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      float v = acc[i][rr];
+#pragma unroll
+      for (int k = 0; k < 3; ++k) v += red[((k * 4 + nt) * MT * 4 + i * 4 + rr) * 64 + lane];
+      const int64_t m = i * 16 + 4 * lg + rr;
+      if (m < a.M) a.y[m * a.ys + n] = (uint16_t)(BF16::pack(v, 0.0f) & 0xffffu);
+    }
+}
+
+bool skinny_launch(const QgemmArgs& a, hipStream_t s) {
+  if (a.K % (64 * kSkCG)) return false;
+  const dim3 grid((unsigned)((a.N + 63) / 64));
+  switch ((a.M + 15) / 16) {
+    case 1: hipLaunchKernelGGL(qgemm_skinny_kernel<1>, grid, dim3(1024), 0, s, a); return true;
+    case 2: hipLaunchKernelGGL(qgemm_skinny_kernel<2>, grid, dim3(1024), 0, s, a); return true;
+    case 3: hipLaunchKernelGGL(qgemm_skinny_kernel<3>, grid, dim3(1024), 0, s, a); return true;
+    default: hipLaunchKernelGGL(qgemm_skinny_kernel<4>, grid, dim3(1024), 0, s, a); return true;
+  }
+}
+
+bool qgemm_supported(int dtype, int sdt, int group_size, int bits, const void* x, int64_t xs,
+                     const void* w, int64_t k) {
+  return dtype == DT_BF16 && sdt == DT_BF16 && group_size == 64 && bits == 4 && k % 64 == 0 &&
+         (reinterpret_cast<uintptr_t>(x) & 15) == 0 && xs % 8 == 0 &&
+         (reinterpret_cast<uintptr_t>(w) & 7) == 0 && ((k / 8) % 2) == 0;
+}
+
+void qgemm_launch(const QgemmArgs& a, hipStream_t s) {
+  const unsigned gx = (unsigned)((a.N + kQgBN - 1) / kQgBN);
+  if (a.M <= 64 && skinny_launch(a, s)) return;
+  if (a.M <= 64) {
+    hipLaunchKernelGGL(qgemm_kernel<32>, dim3(gx, (unsigned)((a.M + 31) / 32)), dim3(256), 0, s, a);
+  } else if (a.M <= 512) {
+    hipLaunchKernelGGL(qgemm_kernel<64>, dim3(gx, (unsigned)((a.M + 63) / 64)), dim3(256), 0, s, a);
+  } else {
+    hipLaunchKernelGGL(qgemm_kernel<128>, dim3(gx, (unsigned)((a.M + 127) / 128)), dim3(256), 0, s, a);
+  }
+}
+
+}  // namespace hgk

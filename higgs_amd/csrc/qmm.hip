@@ -26,6 +26,7 @@
 #include "../../include/higgs_hip.h"
 #include "hgk_common.h"
 #include "hgk_host.h"
+#include "qgemm.h"
 
 namespace hgk {
 
@@ -55,6 +56,7 @@ __device__ inline float dot2_bf16(uint32_t a, uint32_t b, float c) {
 }
 
 __device__ inline int64_t pair_expert(const QmmArgs& a, int64_t p) {
+  if (a.experts == nullptr) return 0;  // quantized_matmul: one weight matrix
   if (a.experts_i32) {
     const int64_t e = reinterpret_cast<const int32_t*>(a.experts)[p];
     return e < 0 ? e + a.E : e;
@@ -250,6 +252,56 @@ extern "C" int hgk_gather_qmm(int dtype, const void* x, int64_t x_rows, int64_t 
   a.E = n_experts; a.N = n; a.K = k; a.group = group_size; a.pairs = pairs; a.y = y;
   a.ys = y_row_stride;
   const hipStream_t s = as_stream(stream);
+  const bool vec_ok = dtype == DT_BF16 && aligned16(x) && x_row_stride % 8 == 0 && aligned16(w) &&
+                      (reinterpret_cast<uintptr_t>(scales) & 1) == 0;
+  if (vec_ok && launch_bf16<BF16>(a, s)) return launch_status(fn);
+  if (dtype == DT_BF16) launch_generic<BF16, BF16>(a, s);
+  else launch_generic<F16, F16>(a, s);
+  return launch_status(fn);
+}
+
+extern "C" int hgk_quantized_matmul(int dtype, const void* x, int64_t m, int64_t x_row_stride,
+                                    const uint32_t* w, const void* scales, const void* biases,
+                                    int scales_dtype, int64_t n, int64_t k, int group_size,
+                                    int bits, void* y, int64_t y_row_stride, void* stream) {
+  clear_error();
+  const char* fn = "hgk_quantized_matmul";
+  if (bits != 4) return fail(HGK_ERR_UNSUPPORTED, "%s: bits=%d (only 4 is implemented)", fn, bits);
+  if (group_size != 32 && group_size != 64 && group_size != 128)
+    return fail(HGK_ERR_UNSUPPORTED, "%s: group_size=%d (32, 64 or 128)", fn, group_size);
+  if (dtype != DT_BF16 && dtype != DT_F16)
+    return fail(HGK_ERR_UNSUPPORTED, "%s: activation dtype must be bf16 or f16", fn);
+  if (scales_dtype != dtype)
+    return fail(HGK_ERR_UNSUPPORTED, "%s: scales/biases must have the activation dtype", fn);
+  if (m < 0 || n <= 0 || k <= 0 || k % group_size || k % 8)
+    return fail(HGK_ERR_ARG, "%s: bad shape M=%lld N=%lld K=%lld (K a multiple of %d)", fn,
+                (long long)m, (long long)n, (long long)k, group_size);
+  if ((m > 1 && x_row_stride < k) || (m > 1 && y_row_stride < n))
+    return fail(HGK_ERR_ARG, "%s: row strides (%lld, %lld) smaller than K=%lld / N=%lld", fn,
+                (long long)x_row_stride, (long long)y_row_stride, (long long)k, (long long)n);
+  if (!x || !w || !scales || !biases || !y) return fail(HGK_ERR_ARG, "%s: null pointer", fn);
+  if (n * k >= ((int64_t)1 << 42) || m >= ((int64_t)1 << 31))
+    return fail(HGK_ERR_UNSUPPORTED, "%s: problem too large", fn);
+  if (m == 0) return HGK_OK;
+  const hipStream_t s = as_stream(stream);
+  if (m >= kQgemmMinRows &&
+      qgemm_supported(dtype, scales_dtype, group_size, bits, x, x_row_stride, w, k) &&
+      (m + 127) / 128 <= 65535) {
+    QgemmArgs g{};
+    g.x = static_cast<const uint16_t*>(x); g.xs = x_row_stride; g.w = w;
+    g.sc = static_cast<const uint16_t*>(scales); g.bi = static_cast<const uint16_t*>(biases);
+    g.M = m; g.N = n; g.K = k; g.y = static_cast<uint16_t*>(y); g.ys = y_row_stride;
+    qgemm_launch(g, s);
+    return launch_status(fn);
+  }
+  if (m > 65535)
+    return fail(HGK_ERR_UNSUPPORTED, "%s: M=%lld rows need the MFMA path (bf16, group 64, aligned x)",
+                fn, (long long)m);
+  // one GEMV per row: the gather kernel with a single weight matrix
+  QmmArgs a{};
+  a.x = x; a.xrows = m; a.xs = x_row_stride; a.xdiv = 1; a.lhs = nullptr;
+  a.w = w; a.sc = scales; a.bi = biases; a.experts = nullptr; a.experts_i32 = 0;
+  a.E = 1; a.N = n; a.K = k; a.group = group_size; a.pairs = m; a.y = y; a.ys = y_row_stride;
   const bool vec_ok = dtype == DT_BF16 && aligned16(x) && x_row_stride % 8 == 0 && aligned16(w) &&
                       (reinterpret_cast<uintptr_t>(scales) & 1) == 0;
   if (vec_ok && launch_bf16<BF16>(a, s)) return launch_status(fn);

@@ -341,6 +341,36 @@ def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: t
     return out
 
 
+def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
+                     biases: torch.Tensor, transpose: bool = True, group_size: int = 64,
+                     bits: int = 4, *, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """quantized_matmul(x, w, scales, biases, transpose, group_size, bits) as
+    QLinear::forward calls it (qwen3_next.rs:174-221): x [..., K], w [N,
+    K*bits/32] packed 32-bit words, scales/biases [N, K/group_size]. Returns
+    y [..., N] in x's dtype. M >= 16 rows in bf16 with group 64 run on the
+    matrix cores; fewer rows, f16 or other groups run one GEMV per row."""
+    if not transpose:
+        raise HgkError(2, "quantized_matmul: only transpose=True (weights stored [N, K]) is implemented")
+    if w.dim() != 2 or scales.dim() != 2 or scales.shape != biases.shape:
+        raise HgkError(1, "w must be [N, K/8]; scales and biases [N, K/group]")
+    K = x.shape[-1]
+    N = w.shape[0]
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, K)
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    M = x2.shape[0]
+    if out is None:
+        out = torch.empty((*lead, N), dtype=x.dtype, device=x.device)
+    o2 = out.view(-1, N)
+    check(lib().hgk_quantized_matmul(dtype_code(x.dtype), _ptr(x2), M, x2.stride(0) if M else K,
+                                     _ptr(w.contiguous()), _ptr(scales.contiguous()),
+                                     _ptr(biases.contiguous()), dtype_code(scales.dtype), N, K,
+                                     group_size, bits, _ptr(o2), o2.stride(0) if M else N,
+                                     _stream(x.device)))
+    return out
+
+
 # ---------------------------------------------------------------- GatedDeltaNet
 def gdn_qk_norm_weights(head_k_dim: int, dtype: torch.dtype, device):
     """GatedDeltaNet's constant q/k norm weights (qwen3_next.rs:1075-1094, cast to the input dtype at 1165-1169):

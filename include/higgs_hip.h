@@ -248,6 +248,21 @@ int hgk_gather_qmm(int dtype, const void* x, int64_t x_rows, int64_t x_row_strid
                    int rhs_dtype, int64_t pairs, void* y, int64_t y_row_stride, void* stream);
 
 /*
+ * quantized_matmul(x, w, scales, biases, transpose = true, group_size, bits):
+ * QLinear::forward (crates/higgs-models/src/qwen3_next.rs:174-221, via
+ * quantized_forward 174-183). x [M, K] (row stride x_row_stride, unit column
+ * stride) in `dtype`; w [N, K*bits/32] u32; scales/biases [N, K/group_size]
+ * in scales_dtype; y [M, N] (row stride y_row_stride). bits = 4,
+ * group_size 32, 64 or 128, bf16 or f16 with scales of the same dtype. With
+ * bf16, group 64 and M >= 16 the matrix cores run it (exact products, f32
+ * sums, one rounding); otherwise one GEMV per row (M <= 65535).
+ */
+int hgk_quantized_matmul(int dtype, const void* x, int64_t m, int64_t x_row_stride,
+                         const uint32_t* w, const void* scales, const void* biases,
+                         int scales_dtype, int64_t n, int64_t k, int group_size, int bits,
+                         void* y, int64_t y_row_stride, void* stream);
+
+/*
  * The GatedDeltaNet recurrence of Qwen3-Next's linear-attention layers -- the
  * reference's own gated-delta kernel (crates/higgs-models/src/qwen3_next.rs:
  * 376-451, called at 1187-1201) -- with the constant-weight q/k RMSNorm that

@@ -215,6 +215,15 @@ def gather_qmm(x, x_dt, w, scales, biases, s_dt, experts, *, group=64, x_div=1, 
     return y
 
 
+def quantized_matmul(x, x_dt, w, scales, biases, s_dt, *, group=64):
+    """QLinear::forward's quantized_matmul (qwen3_next.rs:174-183): x [M, K],
+    w [N, K/8] u32, scales/biases [N, K/group]; y [M, N] in x's dtype, the
+    exact contraction rounded once (gather_qmm with one expert)."""
+    M = np.asarray(x).shape[0]
+    return gather_qmm(x, x_dt, np.asarray(w)[None], np.asarray(scales)[None],
+                      np.asarray(biases)[None], s_dt, np.zeros(M, np.int32), group=group)
+
+
 def gated_delta(q, k, v, a_log, a, dt_bias, b, dt, *, p_dt=F32, state=None, qw=None, kw=None,
                 eps=1e-6):
     """GatedDeltaNet recurrence (qwen3_next.rs:376-451): q, k [B,T,Hk,Dk],
