@@ -4,6 +4,9 @@
 // with w [N, K/8] u32 (8 codes per word, low nibble first) and scales/biases
 // [N, K/64] in the activation dtype (bf16).
 //
+// Three kernels: the exact-product kernel below (16 < M <= 512), the skinny
+// kernel for M <= 64 and the hi/lo-plane kernel for M > 512 (further down).
+//
 // Exact products, one group at a time. A code q enters the matrix core as
 // the bf16 number 128 + q (two bit operations per pair of codes), x as
 // itself, so every product x * (128 + q) is exact and the MFMA sums them in
@@ -342,6 +345,139 @@ __global__ __launch_bounds__(1024) void qgemm_skinny_kernel(QgemmArgs a) {
     }
 }
 
+// ---------------------------------------------------------------- hi/lo
+// Many rows (prefill): the matrix cores are the bound, and the per-group f32
+// epilogue of the exact form costs as much VALU time as the MFMAs take. Here
+// each block dequantizes its 128-column weight tile once per group into LDS
+// as two bf16 planes, w = s*q + b (one f32 rounding) = hi + lo with
+// hi = the top 16 bits of w and lo = bf16(w - hi) (|error| <= 2^-17 |w|),
+// and the MFMAs run over both planes straight into the accumulators (no
+// epilogue, no row sums). A block is 8 waves (4 x 2) of 64 x 64 tiles:
+// 256 rows x 128 columns; x and the two planes are double-buffered in LDS,
+// one barrier per group, and the next group's x, codes, scales and biases
+// are loaded while the current group's MFMAs run.
+constexpr int kHlBM = 256, kHlBN = 128;
+
+// two f32 -> packed bf16 pair by truncation (the hi plane) and by rounding
+__device__ inline uint32_t pack_hi(float a, float b) {
+  return (f2u(a) >> 16) | (f2u(b) & 0xffff0000u);
+}
+
+__global__ __launch_bounds__(512) void qgemm_hl_kernel(QgemmArgs a) {
+  constexpr int MT = 4, NT = 4;
+  __shared__ __align__(16) uint16_t xs[2][kHlBM][kQgPitch];
+  __shared__ __align__(16) uint16_t wh[2][kHlBN][kQgPitch];
+  __shared__ __align__(16) uint16_t wl[2][kHlBN][kQgPitch];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;   // 4 x 2 waves
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int64_t m0 = (int64_t)blockIdx.y * kHlBM, n0 = (int64_t)blockIdx.x * kHlBN;
+  const int KW = (int)(a.K / 8), G = (int)(a.K / 64);
+
+  // x: 256 rows x 8 pieces of 16 B per group; piece c = tid + 512 i
+  const uint16_t* xrow[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int c = tid + 512 * i;
+    const int64_t r = m0 + c / 8;
+    xrow[i] = a.x + (r < a.M ? r : a.M - 1) * a.xs + (c & 7) * 8;
+  }
+  // weights: column tid / 4 of the tile, words 2 (tid % 4) and 2 (tid % 4) + 1
+  const int wcn = tid >> 2, wpart = tid & 3;
+  const int64_t wn_ = n0 + wcn < a.N ? n0 + wcn : a.N - 1;
+  const uint32_t* wsrc = a.w + wn_ * KW + 2 * wpart;
+  const uint16_t* ssrc = a.sc + wn_ * G;
+  const uint16_t* bsrc = a.bi + wn_ * G;
+
+  u32x4 xr[4];
+  u32x2_t wr;
+  uint32_t sr, br;
+  auto fetch = [&](int g) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) xr[i] = *reinterpret_cast<const u32x4*>(xrow[i] + g * 64);
+    wr = *reinterpret_cast<const u32x2_t*>(wsrc + g * 8);
+    sr = ssrc[g];
+    br = bsrc[g];
+  };
+  // write the fetched group into LDS buffer `buf`: x as it is, weights as
+  // the hi and lo planes of s * q + b
+  auto publish = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = tid + 512 * i;
+      *reinterpret_cast<u32x4*>(&xs[buf][c / 8][(c & 7) * 8]) = xr[i];
+    }
+    const float sc = BF16::lo(sr), bi = BF16::lo(br);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t c = wr[h];
+      float w[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) w[k] = __builtin_fmaf(sc, (float)((c >> (4 * k)) & 15u), bi);
+      u32x4 hi, lo;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        hi[k] = pack_hi(w[2 * k], w[2 * k + 1]);
+        const float h0 = u2f(f2u(w[2 * k]) & 0xffff0000u), h1 = u2f(f2u(w[2 * k + 1]) & 0xffff0000u);
+        lo[k] = BF16::pack(w[2 * k] - h0, w[2 * k + 1] - h1);
+      }
+      *reinterpret_cast<u32x4*>(&wh[buf][wcn][(2 * wpart + h) * 8]) = hi;
+      *reinterpret_cast<u32x4*>(&wl[buf][wcn][(2 * wpart + h) * 8]) = lo;
+    }
+  };
+
+  f32x4_t acc[MT][NT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[i][t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+  fetch(0);
+  publish(0);
+  for (int g = 0; g < G; ++g) {
+    const int buf = g & 1;
+    __syncthreads();  // buffer g&1 is complete; buffer (g+1)&1 is no longer read
+    if (g + 1 < G) fetch(g + 1);
+    bf16x8_t av[MT][2];
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+      const int row = wm * 64 + i * 16 + l16;
+      av[i][0] = *reinterpret_cast<const bf16x8_t*>(&xs[buf][row][(2 * lg) * 8]);
+      av[i][1] = *reinterpret_cast<const bf16x8_t*>(&xs[buf][row][(2 * lg + 1) * 8]);
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const int col = wn * 64 + t * 16 + l16;
+      const bf16x8_t h0 = *reinterpret_cast<const bf16x8_t*>(&wh[buf][col][(2 * lg) * 8]);
+      const bf16x8_t h1 = *reinterpret_cast<const bf16x8_t*>(&wh[buf][col][(2 * lg + 1) * 8]);
+      const bf16x8_t o0 = *reinterpret_cast<const bf16x8_t*>(&wl[buf][col][(2 * lg) * 8]);
+      const bf16x8_t o1 = *reinterpret_cast<const bf16x8_t*>(&wl[buf][col][(2 * lg + 1) * 8]);
+#pragma unroll
+      for (int i = 0; i < MT; ++i) {
+        acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[i][0], h0, acc[i][t], 0, 0, 0);
+        acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[i][1], h1, acc[i][t], 0, 0, 0);
+        acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[i][0], o0, acc[i][t], 0, 0, 0);
+        acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[i][1], o1, acc[i][t], 0, 0, 0);
+      }
+    }
+    if (g + 1 < G) publish(buf ^ 1);
+  }
+
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t m = m0 + wm * 64 + i * 16 + 4 * lg + r;
+      if (m >= a.M) continue;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const int64_t n = n0 + wn * 64 + t * 16 + l16;
+        if (n < a.N) a.y[m * a.ys + n] = (uint16_t)(BF16::pack(acc[i][t][r], 0.0f) & 0xffffu);
+      }
+    }
+}
+
 bool skinny_launch(const QgemmArgs& a, hipStream_t s) {
   if (a.K % (64 * kSkCG)) return false;
   const dim3 grid((unsigned)((a.N + 63) / 64));
@@ -368,7 +504,7 @@ void qgemm_launch(const QgemmArgs& a, hipStream_t s) {
   } else if (a.M <= 512) {
     hipLaunchKernelGGL(qgemm_kernel<64>, dim3(gx, (unsigned)((a.M + 63) / 64)), dim3(256), 0, s, a);
   } else {
-    hipLaunchKernelGGL(qgemm_kernel<128>, dim3(gx, (unsigned)((a.M + 127) / 128)), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(qgemm_hl_kernel, dim3(gx, (unsigned)((a.M + kHlBM - 1) / kHlBM)), dim3(512), 0, s, a);
   }
 }
 
