@@ -363,40 +363,53 @@ __device__ inline uint32_t pack_hi(float a, float b) {
   return (f2u(a) >> 16) | (f2u(b) & 0xffff0000u);
 }
 
-__global__ __launch_bounds__(512) void qgemm_hl_kernel(QgemmArgs a) {
-  constexpr int MT = 4, NT = 4;
+// WM x 2 waves, each (16 MT) x 64: WM * 16 * MT = 256 rows.
+template <int WM, int MT>
+__global__ __launch_bounds__(WM * 128) void qgemm_hl_kernel(QgemmArgs a) {
+  constexpr int NT = 4, T = WM * 128;
+  static_assert(WM * 16 * MT == kHlBM, "256-row blocks");
+  constexpr int XP = kHlBM * 8 / T;   // 16-byte x pieces per thread per group
+  constexpr int WPT = kHlBN * 8 / T;  // code words per thread per group (2 or 4)
   __shared__ __align__(16) uint16_t xs[2][kHlBM][kQgPitch];
   __shared__ __align__(16) uint16_t wh[2][kHlBN][kQgPitch];
   __shared__ __align__(16) uint16_t wl[2][kHlBN][kQgPitch];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;   // 4 x 2 waves
+  const int wm = wave >> 1, wn = wave & 1;
   const int l16 = lane & 15, lg = lane >> 4;
   const int64_t m0 = (int64_t)blockIdx.y * kHlBM, n0 = (int64_t)blockIdx.x * kHlBN;
   const int KW = (int)(a.K / 8), G = (int)(a.K / 64);
 
-  // x: 256 rows x 8 pieces of 16 B per group; piece c = tid + 512 i
-  const uint16_t* xrow[4];
+  // x: 256 rows x 8 pieces of 16 B per group; piece c = tid + T i
+  const uint16_t* xrow[XP];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int c = tid + 512 * i;
+  for (int i = 0; i < XP; ++i) {
+    const int c = tid + T * i;
     const int64_t r = m0 + c / 8;
     xrow[i] = a.x + (r < a.M ? r : a.M - 1) * a.xs + (c & 7) * 8;
   }
-  // weights: column tid / 4 of the tile, words 2 (tid % 4) and 2 (tid % 4) + 1
-  const int wcn = tid >> 2, wpart = tid & 3;
+  // weights: column tid / (8 / WPT) of the tile, WPT consecutive words
+  const int wcn = tid / (8 / WPT), wpart = tid % (8 / WPT);
   const int64_t wn_ = n0 + wcn < a.N ? n0 + wcn : a.N - 1;
-  const uint32_t* wsrc = a.w + wn_ * KW + 2 * wpart;
+  const uint32_t* wsrc = a.w + wn_ * KW + WPT * wpart;
   const uint16_t* ssrc = a.sc + wn_ * G;
   const uint16_t* bsrc = a.bi + wn_ * G;
 
-  u32x4 xr[4];
-  u32x2_t wr;
+  u32x4 xr[XP];
+  uint32_t wr[WPT];
   uint32_t sr, br;
   auto fetch = [&](int g) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) xr[i] = *reinterpret_cast<const u32x4*>(xrow[i] + g * 64);
-    wr = *reinterpret_cast<const u32x2_t*>(wsrc + g * 8);
+    for (int i = 0; i < XP; ++i) xr[i] = *reinterpret_cast<const u32x4*>(xrow[i] + g * 64);
+    if constexpr (WPT == 4) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(wsrc + g * 8);
+#pragma unroll
+      for (int h = 0; h < 4; ++h) wr[h] = v[h];
+    } else {
+      const u32x2_t v = *reinterpret_cast<const u32x2_t*>(wsrc + g * 8);
+      wr[0] = v[0];
+      wr[1] = v[1];
+    }
     sr = ssrc[g];
     br = bsrc[g];
   };
@@ -404,13 +417,13 @@ __global__ __launch_bounds__(512) void qgemm_hl_kernel(QgemmArgs a) {
   // the hi and lo planes of s * q + b
   auto publish = [&](int buf) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int c = tid + 512 * i;
+    for (int i = 0; i < XP; ++i) {
+      const int c = tid + T * i;
       *reinterpret_cast<u32x4*>(&xs[buf][c / 8][(c & 7) * 8]) = xr[i];
     }
     const float sc = BF16::lo(sr), bi = BF16::lo(br);
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    for (int h = 0; h < WPT; ++h) {
       const uint32_t c = wr[h];
       float w[8];
 #pragma unroll
@@ -422,8 +435,8 @@ __global__ __launch_bounds__(512) void qgemm_hl_kernel(QgemmArgs a) {
         const float h0 = u2f(f2u(w[2 * k]) & 0xffff0000u), h1 = u2f(f2u(w[2 * k + 1]) & 0xffff0000u);
         lo[k] = BF16::pack(w[2 * k] - h0, w[2 * k + 1] - h1);
       }
-      *reinterpret_cast<u32x4*>(&wh[buf][wcn][(2 * wpart + h) * 8]) = hi;
-      *reinterpret_cast<u32x4*>(&wl[buf][wcn][(2 * wpart + h) * 8]) = lo;
+      *reinterpret_cast<u32x4*>(&wh[buf][wcn][(WPT * wpart + h) * 8]) = hi;
+      *reinterpret_cast<u32x4*>(&wl[buf][wcn][(WPT * wpart + h) * 8]) = lo;
     }
   };
 
@@ -442,7 +455,7 @@ __global__ __launch_bounds__(512) void qgemm_hl_kernel(QgemmArgs a) {
     bf16x8_t av[MT][2];
 #pragma unroll
     for (int i = 0; i < MT; ++i) {
-      const int row = wm * 64 + i * 16 + l16;
+      const int row = wm * 16 * MT + i * 16 + l16;
       av[i][0] = *reinterpret_cast<const bf16x8_t*>(&xs[buf][row][(2 * lg) * 8]);
       av[i][1] = *reinterpret_cast<const bf16x8_t*>(&xs[buf][row][(2 * lg + 1) * 8]);
     }
@@ -468,7 +481,7 @@ __global__ __launch_bounds__(512) void qgemm_hl_kernel(QgemmArgs a) {
   for (int i = 0; i < MT; ++i)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int64_t m = m0 + wm * 64 + i * 16 + 4 * lg + r;
+      const int64_t m = m0 + wm * 16 * MT + i * 16 + 4 * lg + r;
       if (m >= a.M) continue;
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
@@ -504,7 +517,9 @@ void qgemm_launch(const QgemmArgs& a, hipStream_t s) {
   } else if (a.M <= 512) {
     hipLaunchKernelGGL(qgemm_kernel<64>, dim3(gx, (unsigned)((a.M + 63) / 64)), dim3(256), 0, s, a);
   } else {
-    hipLaunchKernelGGL(qgemm_hl_kernel, dim3(gx, (unsigned)((a.M + kHlBM - 1) / kHlBM)), dim3(512), 0, s, a);
+    // 8 waves of 64 x 64 measured faster than 4 waves of 128 x 64
+    hipLaunchKernelGGL((qgemm_hl_kernel<4, 4>), dim3(gx, (unsigned)((a.M + kHlBM - 1) / kHlBM)),
+                       dim3(512), 0, s, a);
   }
 }
 

@@ -799,6 +799,40 @@ Array gather_qmm(const Array& x, const Array& w, const Array& scales, const Arra
   return y;
 }
 
+Array quantized_matmul(const Array& x, const Array& w, const Array& scales, const Array& biases,
+                       bool transpose, int group_size, int bits) {
+  const char* op = "quantized_matmul";
+  Operands ops = {{"x", &x}, {"w", &w}, {"scales", &scales}, {"biases", &biases}};
+  if (!transpose) fail(op, "only transpose = true (weights stored [N, K]) is implemented", ops);
+  if (x.ndim() < 1) fail(op, "x must have at least one axis", ops);
+  if (w.ndim() != 2 || w.dtype() != Dtype::Uint32 || !w.is_contiguous() || scales.ndim() != 2 ||
+      scales.shape() != biases.shape() || !scales.is_contiguous() || !biases.is_contiguous())
+    fail(op, "w must be contiguous Uint32 [N, K/8]; scales/biases [N, K/group]", ops);
+  const int64_t K = x.dim(-1), N = w.dim(0);
+  if (bits <= 0 || w.dim(1) * 32 / bits != K) fail(op, "w's packed width does not match x's K", ops);
+  Shape lead(x.shape().begin(), x.shape().end() - 1);
+  int64_t M = 1;
+  for (int64_t d : lead) M *= d;
+  // rows of x: [M, K] with a unit-stride last axis (a 2-d strided view is
+  // taken as it is; more leading axes must merge without a copy)
+  if (K > 1 && x.strides().back() != 1) fail(op, "x's last axis must have unit stride", ops);
+  Array x2 = x.ndim() == 2 ? x : x.reshape({M, K});
+  Shape oshape = lead;
+  oshape.push_back(N);
+  Array y = Array::empty(oshape, x.dtype());
+  if (M == 0) return y;
+  check(hgk_quantized_matmul(static_cast<int>(x.dtype()), x2.data(), M, x2.strides()[0],
+                             static_cast<const uint32_t*>(w.data()), scales.data(), biases.data(),
+                             static_cast<int>(scales.dtype()), N, K, group_size, bits, y.data(), N,
+                             stream_arg()),
+        op, ops);
+  return y;
+}
+
+Array nn::QLinear::forward(const Array& x) const {
+  return quantized_matmul(x, weight, scales, biases, true, group_size, bits);
+}
+
 Array nn::SwitchMlpWeights::forward_gather(const Array& x, const Array& indices) const {
   if (x.ndim() != 2 || indices.ndim() != 2 || indices.dim(0) != x.dim(0))
     throw Exception::custom("forward_gather input must be [T, D] with indices [T, top_k] " +

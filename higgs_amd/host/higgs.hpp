@@ -248,6 +248,10 @@ struct QLinear {
   Array weight, scales, biases;
   int group_size = 64;
   int bits = 4;
+  // QLinear::forward (qwen3_next.rs:210-220): quantized_matmul(x, weight,
+  // scales, biases, transpose = true, group_size, bits) over the last axis
+  // of x (any leading dims; weight [N, K*bits/32] for this form).
+  Array forward(const Array& x) const;
 };
 
 // Stacked expert weights of a switch MLP (qwen3_next.rs:824-904).
@@ -258,6 +262,13 @@ struct SwitchMlpWeights {
   Array forward_gather(const Array& x, const Array& indices) const;
 };
 }  // namespace nn
+
+// ops::quantized_matmul(x, w, scales, biases, transpose, group_size, bits)
+// (quantized_forward, qwen3_next.rs:174-183): x [..., K] with a unit-stride
+// last axis, w [N, K*bits/32] Uint32, scales/biases [N, K/group_size];
+// returns [..., N]. Only transpose = true (weights stored [N, K]).
+Array quantized_matmul(const Array& x, const Array& w, const Array& scales, const Array& biases,
+                       bool transpose, int group_size, int bits);
 
 // gather_qmm(x, w, scales, biases, rhs_indices, transpose = true, group_size,
 // bits) with one row of x per (token, expert) pair (qwen3_next.rs:294-363):

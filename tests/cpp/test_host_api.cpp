@@ -558,6 +558,44 @@ TEST(test_switch_mlp_forward_gather) {
   check_close(y.to_bits(), want_d, "down");
 }
 
+// QLinear::forward = quantized_matmul (qwen3_next.rs:174-221): decode (8
+// rows, the per-row path), a batch of 64 rows (the matrix-core path for few
+// rows) and 600 rows as [2, 300, K] (the prefill path), against the oracle
+// within 1 bf16 ulp (or 1e-3 next to zero), >= 99% bit-identical.
+TEST(test_qlinear_forward_matches_oracle) {
+  const int64_t N = 320, K = 1024, G = 64;
+  std::vector<uint32_t> w(N * K / 8);
+  or_fill_u32(9600, w.data(), static_cast<int64_t>(w.size()));
+  auto sb = bits_of(uniform(9601, N * K / G, 0.005f, 0.02f), OR_BF16);
+  auto bb = bits_of(uniform(9602, N * K / G, -0.1f, 0.1f), OR_BF16);
+  higgs::nn::QLinear lin{Array::from_slice(w, {N, K / 8}), dev16(sb, {N, K / G}, Dtype::Bfloat16),
+                         dev16(bb, {N, K / G}, Dtype::Bfloat16), 64, 4};
+  std::vector<int32_t> zeros_idx;
+  for (int64_t M : {8, 64, 600}) {
+    auto xb = bits_of(normal(9610 + M, M * K), OR_BF16);
+    Array x = M == 600 ? dev16(xb, {2, 300, K}, Dtype::Bfloat16) : dev16(xb, {M, K}, Dtype::Bfloat16);
+    Array y = lin.forward(x);
+    ASSERT(y.ndim() == x.ndim() && y.dim(-1) == N, "%s", y.describe().c_str());
+    zeros_idx.assign(M, 0);
+    std::vector<uint16_t> want(M * N);
+    ASSERT(or_gather_qmm(OR_BF16, xb.data(), M, K, 1, nullptr, w.data(), sb.data(), bb.data(), OR_BF16, 1, N, K, 64,
+                         zeros_idx.data(), M, want.data(), N) == 0,
+           "oracle");
+    auto got = y.to_bits();
+    std::vector<float> gf(got.size()), wf(want.size());
+    or_convert_to_f32(OR_BF16, got.data(), gf.data(), static_cast<int64_t>(got.size()));
+    or_convert_to_f32(OR_BF16, want.data(), wf.data(), static_cast<int64_t>(want.size()));
+    int64_t exact = 0;
+    for (size_t i = 0; i < got.size(); ++i) {
+      ASSERT(ulp16(got[i], want[i]) <= 1 || std::fabs(gf[i] - wf[i]) <= 1e-3f, "M=%lld y[%zu] %g vs %g",
+             (long long)M, i, gf[i], wf[i]);
+      exact += got[i] == want[i];
+    }
+    ASSERT(exact >= 0.99 * static_cast<double>(got.size()), "M=%lld: %lld of %zu bit-identical", (long long)M,
+           (long long)exact, got.size());
+  }
+}
+
 // The reference's gated-delta kernel tests (qwen3_next.rs:1700-1722,
 // 2421-2450): all-ones q, k, v and a, zero a_log, dt_bias, b and state, Hk 2,
 // Hv 4, Dk = Dv = 32, f32. One step gives delta = 1/2, s = 1/2 everywhere and

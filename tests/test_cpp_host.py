@@ -25,7 +25,7 @@ EXPECTED = {
     "test_ops_run_on_the_scoped_stream", "test_add_rms_norm_block_boundaries",
     "test_quantized_embedding_forward_rms_norm",
     "test_load_quantized_checkpoint_drives_embedding_and_norm", "test_switch_mlp_forward_gather",
-    "test_gated_delta_reference_cases_and_decode",
+    "test_gated_delta_reference_cases_and_decode", "test_qlinear_forward_matches_oracle",
 }
 
 
@@ -50,7 +50,8 @@ def test_host_library_exports_the_mlx_shaped_api():
                 "higgs::nn::RmsNorm::forward(", "higgs::nn::Rope::forward(",
                 "higgs::nn::QuantizedEmbedding::forward(", "higgs::nn::silu_mul(",
                 "higgs::nn::gelu_approximate_mul(", "higgs::apply_rope(", "higgs::swiglu(",
-                "higgs::gated_delta(", "higgs::gdn_qk_norm_weights(",
+                "higgs::gated_delta(", "higgs::gdn_qk_norm_weights(", "higgs::quantized_matmul(",
+                "higgs::nn::QLinear::forward(",
                 "higgs::gated_rms_norm(", "higgs::qk_norm_rope(", "higgs::Array::from_slice(",
                 "higgs::add_rms_norm(", "higgs::nn::QuantizedEmbedding::forward_rms_norm(",
                 "higgs::gather_qmm(", "higgs::nn::SwitchMlpWeights::forward_gather("):
