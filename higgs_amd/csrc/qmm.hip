@@ -44,6 +44,7 @@ struct QmmArgs {
   int64_t E, N, K;
   int group;
   int64_t pairs;
+  int64_t p0;       // first pair of this launch (launches cover <= 65535 pairs)
   void* y;
   int64_t ys;
 };
@@ -82,7 +83,7 @@ __global__ __launch_bounds__(256) void qmv_bf16_kernel(QmmArgs a) {
   constexpr int K = STEPS * 128;
   __shared__ __attribute__((aligned(16))) uint32_t xs_perm[K / 2];  // bf16 pairs in dot order
   __shared__ float hsum[K / 32];       // sum of x over each 32-code half group
-  const int64_t p = blockIdx.y;
+  const int64_t p = a.p0 + blockIdx.y;
   const int64_t e = pair_expert(a, p);
   const int64_t xr0 = pair_row(a, p);
   const bool valid = e >= 0 && e < a.E && xr0 >= 0;
@@ -191,14 +192,24 @@ __global__ __launch_bounds__(256) void qmv_generic_kernel(QmmArgs a) {
 
 namespace {
 
+template <class S, int STEPS>
+void launch_bf16_k(QmmArgs a, hipStream_t s) {
+  // one launch per 65535 pairs (the grid's y extent)
+  for (int64_t p0 = 0; p0 < a.pairs; p0 += 65535) {
+    a.p0 = p0;
+    const int64_t np = a.pairs - p0 < 65535 ? a.pairs - p0 : 65535;
+    const dim3 grid((unsigned)((a.N + 63) / 64), (unsigned)np);
+    hipLaunchKernelGGL((qmv_bf16_kernel<S, STEPS>), grid, dim3(256), 0, s, a);
+  }
+}
+
 template <class S>
 bool launch_bf16(const QmmArgs& a, hipStream_t s) {
-  const dim3 grid((unsigned)((a.N + 63) / 64), (unsigned)a.pairs);
   switch (a.K) {
-    case 512: hipLaunchKernelGGL((qmv_bf16_kernel<S, 4>), grid, dim3(256), 0, s, a); return true;
-    case 1024: hipLaunchKernelGGL((qmv_bf16_kernel<S, 8>), grid, dim3(256), 0, s, a); return true;
-    case 2048: hipLaunchKernelGGL((qmv_bf16_kernel<S, 16>), grid, dim3(256), 0, s, a); return true;
-    case 4096: hipLaunchKernelGGL((qmv_bf16_kernel<S, 32>), grid, dim3(256), 0, s, a); return true;
+    case 512: launch_bf16_k<S, 4>(a, s); return true;
+    case 1024: launch_bf16_k<S, 8>(a, s); return true;
+    case 2048: launch_bf16_k<S, 16>(a, s); return true;
+    case 4096: launch_bf16_k<S, 32>(a, s); return true;
     default: return false;
   }
 }
@@ -243,8 +254,8 @@ extern "C" int hgk_gather_qmm(int dtype, const void* x, int64_t x_rows, int64_t 
     return fail(HGK_ERR_ARG, "%s: row strides (%lld, %lld) smaller than K=%lld / N=%lld", fn,
                 (long long)x_row_stride, (long long)y_row_stride, (long long)k, (long long)n);
   if (!x || !w || !scales || !biases || !rhs_indices || !y) return fail(HGK_ERR_ARG, "%s: null pointer", fn);
-  if (pairs > 65535 || n_experts * n * k >= ((int64_t)1 << 42))
-    return fail(HGK_ERR_UNSUPPORTED, "%s: problem too large (pairs <= 65535)", fn);
+  if (n_experts * n * k >= ((int64_t)1 << 42) || pairs * n >= ((int64_t)1 << 32) || pairs >= ((int64_t)1 << 31))
+    return fail(HGK_ERR_UNSUPPORTED, "%s: problem too large", fn);
   if (pairs == 0) return HGK_OK;
   QmmArgs a{};
   a.x = x; a.xrows = x_rows; a.xs = x_row_stride; a.xdiv = x_row_div > 0 ? x_row_div : 1; a.lhs = lhs_indices;
@@ -294,9 +305,9 @@ extern "C" int hgk_quantized_matmul(int dtype, const void* x, int64_t m, int64_t
     qgemm_launch(g, s);
     return launch_status(fn);
   }
-  if (m > 65535)
-    return fail(HGK_ERR_UNSUPPORTED, "%s: M=%lld rows need the MFMA path (bf16, group 64, aligned x)",
-                fn, (long long)m);
+  if (m * n >= ((int64_t)1 << 32))
+    return fail(HGK_ERR_UNSUPPORTED, "%s: M=%lld x N=%lld too large for the per-row path", fn,
+                (long long)m, (long long)n);
   // one GEMV per row: the gather kernel with a single weight matrix
   QmmArgs a{};
   a.x = x; a.xrows = m; a.xs = x_row_stride; a.xdiv = 1; a.lhs = nullptr;

@@ -239,7 +239,7 @@ int hgk_quantized_embedding_rms_norm(const void* ids, int ids_dtype, int64_t n_i
  * given, else p / x_row_div (forward_gather's broadcast of one token row over
  * its top_k experts: x_row_div = top_k for gate/up, 1 for down). y [pairs, n]
  * in x's dtype, f32 accumulation. Rows or experts out of range give zero
- * rows. pairs <= 65535.
+ * rows.
  */
 int hgk_gather_qmm(int dtype, const void* x, int64_t x_rows, int64_t x_row_stride,
                    int64_t x_row_div, const int32_t* lhs_indices, const uint32_t* w,
@@ -255,7 +255,7 @@ int hgk_gather_qmm(int dtype, const void* x, int64_t x_rows, int64_t x_row_strid
  * in scales_dtype; y [M, N] (row stride y_row_stride). bits = 4,
  * group_size 32, 64 or 128, bf16 or f16 with scales of the same dtype. With
  * bf16, group 64 and M >= 16 the matrix cores run it (exact products, f32
- * sums, one rounding); otherwise one GEMV per row (M <= 65535).
+ * sums, one rounding); otherwise one GEMV per row.
  */
 int hgk_quantized_matmul(int dtype, const void* x, int64_t m, int64_t x_row_stride,
                          const uint32_t* w, const void* scales, const void* biases,

@@ -119,3 +119,19 @@ def test_swiglu_expert_block_end_to_end(dev):
     # three roundings deep, the end-to-end bar widens to 4 ulps
     assert_close(to_host(d), d_ref, O.BF16, max_ulp=4, what="expert block end to end")
 
+
+
+def test_more_pairs_than_one_grid_holds(dev):
+    """81,920 pairs (an 8192-token prefill at top-10) exceed the 65535 pairs
+    one launch covers; the pairs around each launch boundary and at both ends
+    are checked against the oracle."""
+    P, E, N, K = 81920, 6, 64, 512
+    x = O.from_f32(O.normal(2381, (P, K)), O.BF16)
+    w = O.u32(2382, (E, N, K // 8))
+    s = O.from_f32(O.uniform(2383, (E, N, K // 64), 0.005, 0.02), O.BF16)
+    b = O.from_f32(O.uniform(2384, (E, N, K // 64), -0.1, 0.1), O.BF16)
+    ex = (O.u32(2385, (P,)) % np.uint32(E)).astype(np.int32)
+    got = _run(dev, x, w, s, b, ex, O.BF16)
+    for lo, hi in ((0, 48), (65500, 65580), (P - 48, P)):
+        ref = O.gather_qmm(x[lo:hi], O.BF16, w, s, b, O.BF16, ex[lo:hi])
+        _check(got[lo:hi], ref, O.BF16, f"pairs {lo}..{hi}")
