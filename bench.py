@@ -380,6 +380,40 @@ def wl_qwen3_next_qlinear(cx):
     return Workload("qwen3_next_qlinear", cfg, ks, nd, 64 + 4096)
 
 
+def wl_qwen3_next_moe_prefill(cx):
+    """Qwen3-Next-80B-A3B routed experts over a 4096-token prefill: top-10 of
+    512 experts (40,960 pairs, ~80 per expert), gate and up (512 x 2048)
+    gather_qmm, SwiGLU, down (2048 x 512) gather_qmm, 4-bit group 64 -- the
+    expert-grouped matrix-core path; flops = 2 x pairs x N x K per
+    projection."""
+    torch = cx.torch
+    T, top_k, E, D, I = 4096, 10, 512, 2048, 512
+    P = T * top_k
+    tab = {nm: cx.qtable_experts(E, N, K) for nm, N, K in
+           (("gate", I, D), ("up", I, D), ("down", D, I))}
+    ns = 2
+    g = torch.Generator().manual_seed(6)
+    exs = [torch.stack([torch.randperm(E, generator=g)[:top_k] for _ in range(T)]).reshape(-1)
+           .to(torch.int32) for _ in range(ns)]
+    exd = [ex.to(cx.dev) for ex in exs]
+    xs = [cx.randn((T, D), torch.bfloat16) for _ in range(ns)]
+    acts = [cx.randn((P, I), torch.bfloat16) for _ in range(ns)]
+    ks, outs = [], {}
+    for nm, N, K, xdiv in (("gate", I, D, top_k), ("up", I, D, top_k), ("down", D, I, 1)):
+        outs[nm] = [cx.empty((P, N), torch.bfloat16) for _ in range(ns)]
+        sets = [((xs[si] if nm != "down" else acts[si]), exs[si], exd[si], outs[nm][si])
+                for si in range(ns)]
+        k = k_qmm(cx, f"qmm_{nm}_prefill", sets, tab[nm], E, N, K, T, top_k, xdiv)
+        k.flops = 2 * P * N * K
+        ks.append(k)
+    act = [(outs["gate"][si], outs["up"][si], cx.empty((P, I), torch.bfloat16)) for si in range(ns)]
+    ks.insert(2, k_glu(cx, "swiglu_moe_prefill", act, P, I, SILU))
+    cfg = {"workload": "qwen3-next-80b-a3b routed experts, 4096-token prefill", "tokens": T,
+           "experts": E, "top_k": top_k, "hidden": D, "expert_dim": I, "quant": "4-bit g64",
+           "buffer_sets": ns}
+    return Workload("qwen3_next_moe_prefill", cfg, ks, ns, T)
+
+
 def k_gdn(cx, name, sets, wq, wk, alog, dtb, B, T, Hk, Dk, Hv, Dv):
     """Gated-delta recurrence with the fused q/k norm; bytes = state read and
     written once + q, k, v, a, b read + y written."""
@@ -540,6 +574,7 @@ WORKLOADS = {
     "qwen3_next_moe_decode": wl_qwen3_next_moe_decode,
     "qwen3_next_gdn": wl_qwen3_next_gdn,
     "qwen3_next_qlinear": wl_qwen3_next_qlinear,
+    "qwen3_next_moe_prefill": wl_qwen3_next_moe_prefill,
 }
 
 

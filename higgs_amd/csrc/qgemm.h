@@ -18,6 +18,30 @@ struct QgemmArgs {
   int64_t ys;         // y row stride (elements)
 };
 
+// gather_qmm over many (token, expert) pairs, grouped by expert on the matrix
+// cores: y[p, :] = x[row(p), :] . W[e_p]^T, row(p) = lhs[p] or p / xdiv.
+struct GatherArgs {
+  const uint16_t* x;
+  int64_t xrows, xs, xdiv;
+  const int32_t* lhs;
+  const uint32_t* w;   // [E, N, K/8]
+  const uint16_t* sc;  // [E, N, K/64]
+  const uint16_t* bi;
+  const void* experts;
+  int experts_i32;
+  int64_t E, N, K, pairs;
+  uint16_t* y;
+  int64_t ys;
+};
+
+// Pairs per expert (on average) from which the grouped kernel runs.
+constexpr int64_t kGatherMinPairsPerExpert = 16;
+
+// bf16, group 64, 4 bits, x 16-byte aligned rows, w 16-byte aligned, K % 64.
+bool gather_grouped_supported(int dtype, int sdt, int group_size, int bits, const void* x,
+                              int64_t xs, const void* w, int64_t k);
+void gather_grouped_launch(const GatherArgs& a, hipStream_t s);
+
 // Rows of x at or above which the MFMA kernel runs (below: one GEMV per row).
 constexpr int64_t kQgemmMinRows = 16;
 

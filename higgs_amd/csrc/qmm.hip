@@ -65,7 +65,7 @@ __device__ inline int64_t pair_expert(const QmmArgs& a, int64_t p) {
   return (int64_t)reinterpret_cast<const uint32_t*>(a.experts)[p];
 }
 
-// x row of pair p, or -1 when it is outside x (pairs < 2^16, so the
+// x row of pair p, or -1 when it is outside x (pairs < 2^31, so the
 // division is done in 32 bits)
 __device__ inline int64_t pair_row(const QmmArgs& a, int64_t p) {
   int64_t r = a.lhs ? (int64_t)a.lhs[p] : (int64_t)((uint32_t)p / (uint32_t)a.xdiv);
@@ -263,6 +263,18 @@ extern "C" int hgk_gather_qmm(int dtype, const void* x, int64_t x_rows, int64_t 
   a.E = n_experts; a.N = n; a.K = k; a.group = group_size; a.pairs = pairs; a.y = y;
   a.ys = y_row_stride;
   const hipStream_t s = as_stream(stream);
+  // many pairs per expert (prefill): grouped by expert on the matrix cores
+  if (pairs >= kGatherMinPairsPerExpert * n_experts && n_experts < 65535 &&
+      gather_grouped_supported(dtype, scales_dtype, group_size, bits, x, x_row_stride, w, k)) {
+    GatherArgs g{};
+    g.x = static_cast<const uint16_t*>(x); g.xrows = x_rows; g.xs = x_row_stride;
+    g.xdiv = x_row_div > 0 ? x_row_div : 1; g.lhs = lhs_indices; g.w = w;
+    g.sc = static_cast<const uint16_t*>(scales); g.bi = static_cast<const uint16_t*>(biases);
+    g.experts = rhs_indices; g.experts_i32 = rhs_dtype == DT_I32; g.E = n_experts; g.N = n; g.K = k;
+    g.pairs = pairs; g.y = static_cast<uint16_t*>(y); g.ys = y_row_stride;
+    gather_grouped_launch(g, s);
+    return launch_status(fn);
+  }
   const bool vec_ok = dtype == DT_BF16 && aligned16(x) && x_row_stride % 8 == 0 && aligned16(w) &&
                       (reinterpret_cast<uintptr_t>(scales) & 1) == 0;
   if (vec_ok && launch_bf16<BF16>(a, s)) return launch_status(fn);

@@ -239,7 +239,9 @@ int hgk_quantized_embedding_rms_norm(const void* ids, int ids_dtype, int64_t n_i
  * given, else p / x_row_div (forward_gather's broadcast of one token row over
  * its top_k experts: x_row_div = top_k for gate/up, 1 for down). y [pairs, n]
  * in x's dtype, f32 accumulation. Rows or experts out of range give zero
- * rows.
+ * rows. With at least 16 pairs per expert on average (prefill; bf16, group
+ * 64) the pairs are grouped by expert inside the kernel and run on the matrix
+ * cores; otherwise one GEMV per pair.
  */
 int hgk_gather_qmm(int dtype, const void* x, int64_t x_rows, int64_t x_row_stride,
                    int64_t x_row_div, const int32_t* lhs_indices, const uint32_t* w,

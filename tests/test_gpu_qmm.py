@@ -122,10 +122,11 @@ def test_swiglu_expert_block_end_to_end(dev):
 
 
 def test_more_pairs_than_one_grid_holds(dev):
-    """81,920 pairs (an 8192-token prefill at top-10) exceed the 65535 pairs
-    one launch covers; the pairs around each launch boundary and at both ends
-    are checked against the oracle."""
-    P, E, N, K = 81920, 6, 64, 512
+    """81,920 pairs exceed the 65535 pairs one launch of the per-pair kernel
+    covers (6000 experts keep them below the grouped kernel's 16 pairs per
+    expert); the pairs around the launch boundary and at both ends are
+    checked against the oracle."""
+    P, E, N, K = 81920, 6000, 16, 512
     x = O.from_f32(O.normal(2381, (P, K)), O.BF16)
     w = O.u32(2382, (E, N, K // 8))
     s = O.from_f32(O.uniform(2383, (E, N, K // 64), 0.005, 0.02), O.BF16)
@@ -135,3 +136,42 @@ def test_more_pairs_than_one_grid_holds(dev):
     for lo, hi in ((0, 48), (65500, 65580), (P - 48, P)):
         ref = O.gather_qmm(x[lo:hi], O.BF16, w, s, b, O.BF16, ex[lo:hi])
         _check(got[lo:hi], ref, O.BF16, f"pairs {lo}..{hi}")
+
+
+def test_grouped_prefill_path_matches_oracle(dev):
+    """Many pairs per expert (a 512-token prefill at top-8 of 32 experts, 128
+    pairs per expert on average) take the expert-grouped matrix-core kernel;
+    gate/up style (x row = pair // top_k) and down style (one row per pair)."""
+    T, top_k, E, N, K = 512, 8, 32, 256, 1024
+    P = T * top_k
+    w = O.u32(2401, (E, N, K // 8))
+    s = O.from_f32(O.uniform(2402, (E, N, K // 64), 0.005, 0.02), O.BF16)
+    b = O.from_f32(O.uniform(2403, (E, N, K // 64), -0.1, 0.1), O.BF16)
+    ex = (O.u32(2404, (P,)) % np.uint32(E)).astype(np.int32)
+    x = O.from_f32(O.normal(2405, (T, K)), O.BF16)
+    got = _run(dev, x, w, s, b, ex, O.BF16, x_div=top_k)
+    ref = O.gather_qmm(x, O.BF16, w, s, b, O.BF16, ex, x_div=top_k)
+    _check(got, ref, O.BF16, "grouped gate/up")
+    xd = O.from_f32(O.normal(2406, (P, K)), O.BF16)
+    got = _run(dev, xd, w, s, b, ex, O.BF16)
+    ref = O.gather_qmm(xd, O.BF16, w, s, b, O.BF16, ex)
+    _check(got, ref, O.BF16, "grouped down")
+
+
+def test_grouped_path_routing_and_out_of_range(dev):
+    """The grouped kernel keeps gather_qmm's routing rules: lhs rows, -1
+    wrapping to the last expert, out-of-range experts and rows giving zero
+    rows; one expert with more pairs than one scan pass lists (the list is
+    drained and the scan resumes)."""
+    P, R, E, N, K = 10000, 40, 4, 128, 512
+    x, w, s, b, ex = _case(2411, P, R, E, N, K)
+    ex = ex.copy()
+    ex[:9000] = 1                  # 9000 pairs on one expert: the list fills and drains
+    ex[[5, 2300]] = [E + 2, -1]    # out of range -> zero row; -1 wraps to E - 1
+    lhs = (np.arange(P) * 13) % R
+    lhs[7] = R                     # row out of range -> zero row
+    lhs[9] = -1                    # wraps to the last row
+    got = _run(dev, x, w, s, b, ex, O.BF16, lhs=lhs)
+    ref = O.gather_qmm(x, O.BF16, w, s, b, O.BF16, ex, lhs=lhs)
+    _check(got, ref, O.BF16, "grouped routing")
+    assert not got[5].any() and not got[7].any() and got[2300].any() and got[9].any()
