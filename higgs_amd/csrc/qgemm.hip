@@ -357,6 +357,9 @@ __global__ __launch_bounds__(1024) void qgemm_skinny_kernel(QgemmArgs a) {
 // one barrier per group, and the next group's x, codes, scales and biases
 // are loaded while the current group's MFMAs run.
 constexpr int kHlBM = 256, kHlBN = 128;
+// groups of loads in flight (4 measured no faster than 2: this kernel is
+// bound by LDS traffic and issue, not by load latency)
+constexpr int kHlDepth = 2;
 
 // two f32 -> packed bf16 pair by truncation (the hi plane) and by rounding
 __device__ inline uint32_t pack_hi(float a, float b) {
@@ -395,36 +398,40 @@ __global__ __launch_bounds__(WM * 128) void qgemm_hl_kernel(QgemmArgs a) {
   const uint16_t* ssrc = a.sc + wn_ * G;
   const uint16_t* bsrc = a.bi + wn_ * G;
 
-  u32x4 xr[XP];
-  uint32_t wr[WPT];
-  uint32_t sr, br;
-  auto fetch = [&](int g) {
+  // a ring of kHlDepth groups' loads in registers (slot g % kHlDepth)
+  struct Stage {
+    u32x4 x[XP];
+    uint32_t w[WPT];
+    uint32_t s, b;
+  };
+  Stage st[kHlDepth];
+  auto fetch = [&](Stage& q, int g) {
 #pragma unroll
-    for (int i = 0; i < XP; ++i) xr[i] = *reinterpret_cast<const u32x4*>(xrow[i] + g * 64);
+    for (int i = 0; i < XP; ++i) q.x[i] = *reinterpret_cast<const u32x4*>(xrow[i] + g * 64);
     if constexpr (WPT == 4) {
       const u32x4 v = *reinterpret_cast<const u32x4*>(wsrc + g * 8);
 #pragma unroll
-      for (int h = 0; h < 4; ++h) wr[h] = v[h];
+      for (int h = 0; h < 4; ++h) q.w[h] = v[h];
     } else {
       const u32x2_t v = *reinterpret_cast<const u32x2_t*>(wsrc + g * 8);
-      wr[0] = v[0];
-      wr[1] = v[1];
+      q.w[0] = v[0];
+      q.w[1] = v[1];
     }
-    sr = ssrc[g];
-    br = bsrc[g];
+    q.s = ssrc[g];
+    q.b = bsrc[g];
   };
-  // write the fetched group into LDS buffer `buf`: x as it is, weights as
-  // the hi and lo planes of s * q + b
-  auto publish = [&](int buf) {
+  // write a fetched group into LDS buffer `buf`: x as it is, weights as the
+  // hi and lo planes of s * q + b
+  auto publish = [&](const Stage& q, int buf) {
 #pragma unroll
     for (int i = 0; i < XP; ++i) {
       const int c = tid + T * i;
-      *reinterpret_cast<u32x4*>(&xs[buf][c / 8][(c & 7) * 8]) = xr[i];
+      *reinterpret_cast<u32x4*>(&xs[buf][c / 8][(c & 7) * 8]) = q.x[i];
     }
-    const float sc = BF16::lo(sr), bi = BF16::lo(br);
+    const float sc = BF16::lo(q.s), bi = BF16::lo(q.b);
 #pragma unroll
     for (int h = 0; h < WPT; ++h) {
-      const uint32_t c = wr[h];
+      const uint32_t c = q.w[h];
       float w[8];
 #pragma unroll
       for (int k = 0; k < 8; ++k) w[k] = __builtin_fmaf(sc, (float)((c >> (4 * k)) & 15u), bi);
@@ -446,12 +453,7 @@ __global__ __launch_bounds__(WM * 128) void qgemm_hl_kernel(QgemmArgs a) {
 #pragma unroll
     for (int t = 0; t < NT; ++t) acc[i][t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-  fetch(0);
-  publish(0);
-  for (int g = 0; g < G; ++g) {
-    const int buf = g & 1;
-    __syncthreads();  // buffer g&1 is complete; buffer (g+1)&1 is no longer read
-    if (g + 1 < G) fetch(g + 1);
+  auto compute = [&](int buf) {
     bf16x8_t av[MT][2];
 #pragma unroll
     for (int i = 0; i < MT; ++i) {
@@ -474,7 +476,24 @@ __global__ __launch_bounds__(WM * 128) void qgemm_hl_kernel(QgemmArgs a) {
         acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[i][1], o1, acc[i][t], 0, 0, 0);
       }
     }
-    if (g + 1 < G) publish(buf ^ 1);
+  };
+
+  // every fetch is unconditional (past the last group it re-reads the last
+  // group), so the count of loads in flight is the same on every path and a
+  // publish waits only for its own group's loads
+#pragma unroll
+  for (int d = 0; d < kHlDepth; ++d) fetch(st[d], d < G ? d : G - 1);
+  publish(st[0], 0);
+  for (int g0 = 0; g0 < G; g0 += kHlDepth) {
+#pragma unroll
+    for (int d = 0; d < kHlDepth; ++d) {
+      const int g = g0 + d;
+      if (g >= G) break;
+      __syncthreads();  // buffer g&1 is complete; buffer (g+1)&1 is no longer read
+      fetch(st[d], g + kHlDepth < G ? g + kHlDepth : G - 1);
+      compute(g & 1);
+      if (g + 1 < G) publish(st[(d + 1) % kHlDepth], (g + 1) & 1);
+    }
   }
 
 #pragma unroll
