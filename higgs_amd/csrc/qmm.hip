@@ -20,9 +20,12 @@
 //
 // Decode touches ~1.25 pairs per expert, so reading an expert's tile once per
 // pair costs ~1.75x the distinct-expert bytes; grouping the pairs by expert
-// (sorted order, or one block walking an expert's pairs) measured slower on
+// (sorted order, one block walking an expert's pairs, or a block that lists
+// its expert's pairs itself and holds the weights in registers across them:
+// 98 against 67 us at 64 sequences x top-10 of 512) measured slower on
 // MI355X -- the pairs of one expert run at the same time on different CUs,
-// and serialising them costs more than the re-read.
+// and serialising them costs more than the re-read. At prefill (16 or more
+// pairs per expert) the grouped matrix-core kernel in qgemm.hip runs instead.
 #include "../../include/higgs_hip.h"
 #include "hgk_common.h"
 #include "hgk_host.h"
@@ -73,6 +76,64 @@ __device__ inline int64_t pair_row(const QmmArgs& a, int64_t p) {
   return (r >= 0 && r < a.xrows) ? r : -1;
 }
 
+// Stage one bf16 x row of K elements in LDS in dot order (the codes of a
+// word pair as (0,4) (1,5) (2,6) (3,7)) with its 32-element half-group sums.
+// Contains the block's barriers: every thread of the block calls it.
+template <int K>
+__device__ inline void qmv_stage_x(const uint16_t* xrow, uint32_t* xs_perm, float* hsum) {
+  // thread t handles one word's worth (8 elements) of the row
+  for (int wd = threadIdx.x; wd < K / 8; wd += 256) {
+    const u32x4 v = *reinterpret_cast<const u32x4*>(xrow + wd * 8);
+    // elements 0..7 as lo/hi halves of v[0..3]: e0=v0.lo e1=v0.hi e2=v1.lo ...
+    // dot order pairs (e0,e4) (e1,e5) (e2,e6) (e3,e7)
+    xs_perm[wd * 4 + 0] = (v[0] & 0xffffu) | (v[2] << 16);
+    xs_perm[wd * 4 + 1] = (v[0] >> 16) | (v[2] & 0xffff0000u);
+    xs_perm[wd * 4 + 2] = (v[1] & 0xffffu) | (v[3] << 16);
+    xs_perm[wd * 4 + 3] = (v[1] >> 16) | (v[3] & 0xffff0000u);
+  }
+  __syncthreads();
+  for (int h = threadIdx.x; h < K / 32; h += 256) {
+    float sacc = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) sacc = dot2_bf16(xs_perm[h * 16 + q], 0x3f803f80u, sacc);
+    hsum[h] = sacc;
+  }
+  __syncthreads();
+}
+
+// This lane's share of one output row: its 32 codes per step against the
+// staged x, the affine part applied per half group.
+template <class S, int STEPS>
+__device__ inline float qmv_dot(const u32x4* codes, const uint32_t* sraw, const uint32_t* braw,
+                                const uint32_t* xs_perm, const float* hsum, int j) {
+  float acc = 0.0f;
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s) {
+    const u32x4 cs = codes[s];
+    const int h = s * 4 + j;  // half group index
+    const u32x4 xq0 = *reinterpret_cast<const u32x4*>(&xs_perm[h * 16 + 0]);
+    const u32x4 xq1 = *reinterpret_cast<const u32x4*>(&xs_perm[h * 16 + 4]);
+    const u32x4 xq2 = *reinterpret_cast<const u32x4*>(&xs_perm[h * 16 + 8]);
+    const u32x4 xq3 = *reinterpret_cast<const u32x4*>(&xs_perm[h * 16 + 12]);
+    const u32x4 xw[4] = {xq0, xq1, xq2, xq3};
+    float d = 0.0f;
+#pragma unroll
+    for (int wi = 0; wi < 4; ++wi) {
+      const uint32_t c = cs[wi];
+      // (128 + q_i, 128 + q_{i+4}) as packed bf16, i = 0..3
+      d = dot2_bf16(xw[wi][0], (c & 0x000f000fu) | 0x43004300u, d);
+      d = dot2_bf16(xw[wi][1], ((c >> 4) & 0x000f000fu) | 0x43004300u, d);
+      d = dot2_bf16(xw[wi][2], ((c >> 8) & 0x000f000fu) | 0x43004300u, d);
+      d = dot2_bf16(xw[wi][3], ((c >> 12) & 0x000f000fu) | 0x43004300u, d);
+    }
+    const float hs = hsum[h];
+    const float sv = S::lo(sraw[s]), bv = S::lo(braw[s]);
+    acc = __builtin_fmaf(sv, d - 128.0f * hs, acc);
+    acc = __builtin_fmaf(bv, hs, acc);
+  }
+  return acc;
+}
+
 // bf16 x: one block = one pair x 64 output rows (4 waves x 16 rows); a row
 // is split over 4 lanes, lane j reading 16 bytes (32 codes) per step of 128
 // codes, so a wave's load covers 16 rows x 64 contiguous bytes. STEPS = K/128.
@@ -115,48 +176,8 @@ __global__ __launch_bounds__(256) void qmv_bf16_kernel(QmmArgs a) {
     braw[s] = brow[g];
   }
 
-  // stage x: thread t handles one word's worth (8 elements) of the row
-  for (int wd = threadIdx.x; wd < K / 8; wd += 256) {
-    const u32x4 v = *reinterpret_cast<const u32x4*>(xrow + wd * 8);
-    // elements 0..7 as lo/hi halves of v[0..3]: e0=v0.lo e1=v0.hi e2=v1.lo ...
-    // dot order pairs (e0,e4) (e1,e5) (e2,e6) (e3,e7)
-    xs_perm[wd * 4 + 0] = (v[0] & 0xffffu) | (v[2] << 16);
-    xs_perm[wd * 4 + 1] = (v[0] >> 16) | (v[2] & 0xffff0000u);
-    xs_perm[wd * 4 + 2] = (v[1] & 0xffffu) | (v[3] << 16);
-    xs_perm[wd * 4 + 3] = (v[1] >> 16) | (v[3] & 0xffff0000u);
-  }
-  __syncthreads();
-  for (int h = threadIdx.x; h < K / 32; h += 256) {
-    float sacc = 0.0f;
-#pragma unroll
-    for (int q = 0; q < 16; ++q) sacc = dot2_bf16(xs_perm[h * 16 + q], 0x3f803f80u, sacc);
-    hsum[h] = sacc;
-  }
-  __syncthreads();
-  float acc = 0.0f;
-#pragma unroll
-  for (int s = 0; s < STEPS; ++s) {
-    const int h = s * 4 + j;  // half group index
-    const u32x4 xq0 = *reinterpret_cast<const u32x4*>(&xs_perm[h * 16 + 0]);
-    const u32x4 xq1 = *reinterpret_cast<const u32x4*>(&xs_perm[h * 16 + 4]);
-    const u32x4 xq2 = *reinterpret_cast<const u32x4*>(&xs_perm[h * 16 + 8]);
-    const u32x4 xq3 = *reinterpret_cast<const u32x4*>(&xs_perm[h * 16 + 12]);
-    const u32x4 xw[4] = {xq0, xq1, xq2, xq3};
-    float d = 0.0f;
-#pragma unroll
-    for (int wi = 0; wi < 4; ++wi) {
-      const uint32_t c = codes[s][wi];
-      // (128 + q_i, 128 + q_{i+4}) as packed bf16, i = 0..3
-      d = dot2_bf16(xw[wi][0], (c & 0x000f000fu) | 0x43004300u, d);
-      d = dot2_bf16(xw[wi][1], ((c >> 4) & 0x000f000fu) | 0x43004300u, d);
-      d = dot2_bf16(xw[wi][2], ((c >> 8) & 0x000f000fu) | 0x43004300u, d);
-      d = dot2_bf16(xw[wi][3], ((c >> 12) & 0x000f000fu) | 0x43004300u, d);
-    }
-    const float hs = hsum[h];
-    const float sv = S::lo(sraw[s]), bv = S::lo(braw[s]);
-    acc = __builtin_fmaf(sv, d - 128.0f * hs, acc);
-    acc = __builtin_fmaf(bv, hs, acc);
-  }
+  qmv_stage_x<K>(xrow, xs_perm, hsum);
+  float acc = qmv_dot<S, STEPS>(codes, sraw, braw, xs_perm, hsum, j);
   // the row's 4 lanes are adjacent: reduce within the quad
   acc += __shfl_xor(acc, 1, 64);
   acc += __shfl_xor(acc, 2, 64);
