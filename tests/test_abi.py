@@ -112,7 +112,42 @@ def test_error_paths_return_status_and_message():
     st, msg = _status(L.hgk_quantized_embedding, fake, 1, 4, fake, fake, fake, 1, 10, 2048,
                       64, 4, 0.0, fake, 2048, None)
     assert st == _lib.ERR_ARG and "ids" in msg
+    # add + norm, gather_qmm, quantized_matmul, gated delta
+    st, msg = _status(L.hgk_add_rms_norm, 1, fake, 8, None, 8, fake, 1, 0, 1e-5, fake, 8,
+                      fake, 1, 8, 4, 8, None)
+    assert st == _lib.ERR_ARG and "null" in msg
+    st, msg = _status(L.hgk_gather_qmm, 1, fake, 4, 64, 1, None, fake, fake, fake, 1, 2, 64, 64,
+                      64, 8, fake, 4, 4, fake, 64, None)
+    assert st == _lib.ERR_UNSUPPORTED and "bits" in msg
+    st, msg = _status(L.hgk_gather_qmm, 1, fake, 4, 64, 1, None, fake, fake, fake, 1, 2, 64, 64,
+                      64, 4, fake, 0, 4, fake, 64, None)
+    assert st == _lib.ERR_ARG and "indices" in msg
+    st, msg = _status(L.hgk_gather_qmm, 1, fake, 2, 64, 1, None, fake, fake, fake, 1, 2, 64, 64,
+                      64, 4, fake, 4, 4, fake, 64, None)
+    assert st == _lib.ERR_ARG and "rows" in msg
+    st, msg = _status(L.hgk_quantized_matmul, 1, fake, 4, 64, fake, fake, fake, 1, 64, 96, 64, 4,
+                      fake, 64, None)
+    assert st == _lib.ERR_ARG and "K" in msg
+    st, msg = _status(L.hgk_quantized_matmul, 1, fake, 4, 64, fake, fake, fake, 2, 64, 64, 64, 4,
+                      fake, 64, None)
+    assert st == _lib.ERR_UNSUPPORTED and "scales" in msg
+    st, msg = _status(L.hgk_quantized_matmul, 0, fake, 4, 64, fake, fake, fake, 0, 64, 64, 64, 4,
+                      fake, 64, None)
+    assert st == _lib.ERR_UNSUPPORTED and "bf16 or f16" in msg
+    gd = lambda **kw: _status(L.hgk_gated_delta, 1, fake, fake, fake, fake, fake, fake, fake, 0,
+                              None, kw.get("qw"), kw.get("kw"), 1e-6, 1, 1, kw.get("hk", 2),
+                              kw.get("dk", 128), kw.get("hv", 4), 128, fake, fake, None)
+    st, msg = gd(dk=96)
+    assert st == _lib.ERR_UNSUPPORTED and "head_k_dim" in msg
+    st, msg = gd(hk=3)
+    assert st == _lib.ERR_ARG and "multiple" in msg
+    st, msg = gd(qw=fake)
+    assert st == _lib.ERR_ARG and "both" in msg
     # empty problems succeed without launching anything
+    assert L.hgk_quantized_matmul(1, fake, 0, 64, fake, fake, fake, 1, 64, 64, 64, 4, fake, 64,
+                                  None) == 0
+    assert L.hgk_gated_delta(1, fake, fake, fake, fake, fake, fake, fake, 0, None, None, None,
+                             1e-6, 0, 1, 2, 128, 4, 128, fake, fake, None) == 0
     assert L.hgk_rms_norm(fake, 1, 8, None, 1, 0, 1e-5, fake, 1, 8, 0, 8, None) == 0
     assert L.hgk_glu(0, 1, fake, 8, fake, 8, fake, 1, 8, 0, 8, None) == 0
     assert L.hgk_quantized_embedding(fake, 4, 0, fake, fake, fake, 1, 10, 2048, 64, 4, 0.0,

@@ -506,6 +506,25 @@ def test_gather_qmm_matches_torch_f64_dequant_matmul():
     assert exact_frac(y, ref_bits, O.BF16) >= 0.999
 
 
+def test_quantized_matmul_matches_torch_f64_and_groups():
+    """quantized_matmul (QLinear::forward): torch f64 dequantize-then-matmul
+    rounded once to bf16 agrees; groups 32 and 128 dequantize with their own
+    scale spans; f16 activations too."""
+    for dt, group, M, N, K in ((O.BF16, 64, 9, 80, 512), (O.BF16, 32, 5, 48, 256),
+                               (O.BF16, 128, 5, 48, 512), (O.F16, 64, 7, 40, 256)):
+        x = O.from_f32(O.normal(2250 + group, (M, K)), dt)
+        w = O.u32(2251 + group, (N, K // 8))
+        s = O.from_f32(O.uniform(2252 + group, (N, K // group), 0.005, 0.02), dt)
+        b = O.from_f32(O.uniform(2253 + group, (N, K // group), -0.1, 0.1), dt)
+        y = O.quantized_matmul(x, dt, w, s, b, dt, group=group)
+        wd = torch.from_numpy(_dequant_f64(w[None], s[None], b[None], dt, group)[0])
+        xd = torch.from_numpy(O.to_f32(x, dt).astype(np.float64))
+        ref = (xd @ wd.T).to(torch.bfloat16 if dt == O.BF16 else torch.float16)
+        ref_bits = ref.view(torch.int16).numpy().view(np.uint16)
+        assert_close(y, ref_bits, dt, max_ulp=1, what=f"quantized_matmul g{group}")
+        assert exact_frac(y, ref_bits, dt) >= 0.99
+
+
 def test_gather_qmm_closed_forms():
     """Unit scales, zero biases and one-hot x return the raw codes; all-zero
     codes return sum_g b_g * sum_{k in g} x_k."""
