@@ -23,6 +23,7 @@ _f32p = C.POINTER(C.c_float)
 PROTOTYPES = {
     "hgk_last_error": (C.c_char_p, []),
     "hgk_abi_version": (_int, []),
+    "hgk_sync": (_int, [_vp]),
     "hgk_rms_norm": (_int, [_vp, _int, _i64, _vp, _int, _int, _f32, _vp, _int, _i64,
                             _i64, _i64, _vp]),
     "hgk_rope_inv_freq": (_int, [_f32, _int, _f32p, _f32p]),

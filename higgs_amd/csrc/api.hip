@@ -39,6 +39,17 @@ extern "C" const char* hgk_last_error(void) { return g_last_error; }
 
 extern "C" int hgk_abi_version(void) { return HGK_ABI_VERSION; }
 
+// The one blocking call of the library: waits for the work queued on
+// `stream` (NULL = the device's null stream) and reports an asynchronous
+// error raised by it. Stands where the engine forces evaluation with
+// mlx_rs::transforms::eval (crates/higgs-engine/src/simple.rs:399).
+extern "C" int hgk_sync(void* stream) {
+  clear_error();
+  hipError_t e = hipStreamSynchronize(static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(HGK_ERR_HIP, "hgk_sync: %s", hipGetErrorString(e));
+  return HGK_OK;
+}
+
 // Frequencies as fast::rope derives them: explicit freqs -> 1/freqs (f32
 // reciprocal); otherwise exp(arange(0, -half, -1) * f32(log(base) / half))
 // with MLX's polynomial exp (mlx_exp), evaluated in f32 on the host so the

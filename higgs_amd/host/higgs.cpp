@@ -189,7 +189,7 @@ Stream Stream::create() {
 
 Stream Stream::task_local_or_default() { return t_current; }
 
-void Stream::synchronize() const { hip_check(hipStreamSynchronize(s_), "hipStreamSynchronize"); }
+void Stream::synchronize() const { check(hgk_sync(reinterpret_cast<void*>(s_)), "synchronize", {}); }
 
 StreamScope::StreamScope(const Stream& s) : prev_(t_current) { t_current = s; }
 StreamScope::~StreamScope() { t_current = prev_; }

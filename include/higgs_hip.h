@@ -54,6 +54,13 @@ const char* hgk_last_error(void);
 /* HGK_ABI_VERSION of the loaded library. */
 int hgk_abi_version(void);
 
+/* Blocks until the work queued on `stream` (NULL = null stream) has finished
+ * and returns HGK_ERR_HIP with the runtime's message if that work failed.
+ * It is the only entry point that waits on the device; every other call only
+ * enqueues. Replaces the forced evaluation mlx_rs::transforms::eval at
+ * crates/higgs-engine/src/simple.rs:399 (and constrained.rs:275). */
+int hgk_sync(void* stream);
+
 /*
  * RMSNorm over the last axis of x[rows, n]:
  *   y = w' * round_T(x * rsqrt(mean(x^2) + eps)),  T = promote(x, w')

@@ -61,7 +61,8 @@ def test_host_library_exports_the_mlx_shaped_api():
                          text=True, check=True).stdout
     for fn in ("hgk_rms_norm", "hgk_rope", "hgk_qk_norm_rope", "hgk_glu", "hgk_gated_rms_norm",
                "hgk_quantized_embedding", "hgk_last_error", "hgk_add_rms_norm",
-               "hgk_quantized_embedding_rms_norm", "hgk_gather_qmm"):
+               "hgk_quantized_embedding_rms_norm", "hgk_gather_qmm", "hgk_quantized_matmul",
+               "hgk_gated_delta", "hgk_sync"):
         assert fn in dyn, fn
 
 

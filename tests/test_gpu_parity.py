@@ -10,6 +10,7 @@ difference of two rounded products cancels).
 """
 from __future__ import annotations
 
+import ctypes as C
 import math
 
 import numpy as np
@@ -385,3 +386,24 @@ def test_qembed_codes_bitexact_and_variants(dev):
     got, ref = _qemb(dev, 50, 256, 0, ids=ids, key=1860)
     assert np.array_equal(got, ref)
     assert not got[3].any() and not got[4].any()
+
+
+# ------------------------------------------------------------------ hgk_sync
+def test_sync_waits_for_the_stream_it_names(dev):
+    """hgk_sync is the only blocking entry: after it returns for a side stream,
+    everything queued there has finished (the stream reports idle) and the
+    result is the one the oracle gives."""
+    from higgs_amd import _lib
+    rows, n = 4096, 4096
+    x = O.from_f32(O.normal(1901, (rows, n)), O.BF16)
+    w = O.from_f32(O.normal(1902, (n,), 1.0, 0.02), O.BF16)
+    xd, wd = to_dev(x, O.BF16, dev), to_dev(w, O.BF16, dev)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        outs = [H.rms_norm(xd, wd, 1e-5) for _ in range(8)]
+    _lib.check(_lib.lib().hgk_sync(C.c_void_p(side.cuda_stream)))
+    assert side.query()
+    _lib.check(_lib.lib().hgk_sync(None))
+    ref = O.rms_norm(x, O.BF16, w, O.BF16, 1e-5)
+    assert np.array_equal(to_host(outs[-1]), ref) or ulp_dist(to_host(outs[-1]), ref, O.BF16).max() <= 1
