@@ -990,6 +990,12 @@ def main(argv=None):
                             "traffic": traffic_for(dom["kernel"], wl.name),
                             "bytes_per_launch": dom["bytes"],
                             "avg_launch_us": round(dom["avg_us"], 3)}
+        if dom.get("frac_of_mfma_peak", 0.0) > dom["frac_of_peak"]:
+            # a matrix-core-bound kernel (e.g. a prefill projection): priced
+            # against the dense bf16 MFMA peak
+            line["roofline"].update({"bound": "mfma", "achieved": round(dom["tflops"], 2),
+                                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                                     "frac": round(dom["frac_of_mfma_peak"], 4)})
     if args.table:
         rows = []
         for name in WORKLOADS:

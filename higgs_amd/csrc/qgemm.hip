@@ -4,8 +4,9 @@
 // with w [N, K/8] u32 (8 codes per word, low nibble first) and scales/biases
 // [N, K/64] in the activation dtype (bf16).
 //
-// Three kernels: the exact-product kernel below (16 < M <= 512), the skinny
-// kernel for M <= 64 and the hi/lo-plane kernel for M > 512 (further down).
+// Three kernels: the exact-product kernel below (M <= 512), the decode kernel
+// for M <= 64 with K a multiple of 512 and the hi/lo-plane kernel for M > 512
+// (further down).
 //
 // Exact products, one group at a time. A code q enters the matrix core as
 // the bf16 number 128 + q (two bit operations per pair of codes), x as
@@ -41,6 +42,7 @@ typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
 constexpr int kQgBN = 128;   // output columns per block
 constexpr int kQgPitch = 72; // LDS row pitch of the x tile (64 + 8 elements)
+constexpr int kCUs = 256;     // compute units of an MI355X
 
 // 8 codes of one word (code i at bits 4i) -> the 8 bf16 values 128 + q_i in
 // order: the low and high nibbles of each byte are split apart, v_perm_b32
@@ -198,151 +200,209 @@ __global__ __launch_bounds__(256) void qgemm_kernel(QgemmArgs a) {
   }
 }
 
-// ---------------------------------------------------------------- skinny
-// Few rows (M <= 64, the decode step of a batch): the weights are the whole
-// cost. A block is 16 waves over 64 columns: wave w takes column tile w % 4
-// and, of every 512-wide K chunk (8 groups), the two groups 2 (w / 4) and
-// 2 (w / 4) + 1, so a wave's share of the weights is small and all of it for
-// two chunks is in flight at once. x is staged in LDS per chunk, double
-// buffered (one barrier per chunk; the next chunk's x is loaded into
-// registers before the next weights and written to the other buffer after
-// the current chunk's MFMAs). The four group slices' partial sums meet in LDS
-// at the end.
-constexpr int kSkCG = 8;     // groups per chunk
-constexpr int kSkPitch = kSkCG * 64 + 8;
-
-// Per-lane weights of one chunk: codes of this wave's two groups for this
-// lane's column, and their two scales and biases.
-struct SkW {
-  u32x2_t w[2];
-  uint32_t s, b;
-};
+// ---------------------------------------------------------------- decode
+// Few rows (M <= 64, the decode step of a batch; K a multiple of 512): the
+// weights are read once and x (at most 64 rows) is read by every block. A
+// block is 8 waves over 16 NT columns and all rows, and walks K in chunks of
+// 32 groups, each split into 4 sub-chunks of 8 groups. All 512 threads load
+// the chunk's codes, scales and biases with coalesced loads (512 contiguous
+// bytes of codes per wave instruction), sub-chunk by sub-chunk in issue
+// order, and publish each sub-chunk to LDS as it lands (one barrier per
+// sub-chunk), so the MFMAs of sub-chunk s run while later sub-chunks are
+// still arriving. Wave w takes group 8 s + w of sub-chunk s and reads its x
+// straight from global memory into its MFMA A registers (the waves read
+// disjoint slices of x; each A fragment serves NT column tiles). Per group a
+// wave runs the exact-product MFMAs C_g = x . (128 + q) of its MT x NT tiles
+// (B from LDS) and, against a B of ones, the row sums Sx_g, which come out in
+// the accumulator layout (lane l gets rows 4 (l / 16) + r); then
+// acc += s C_g + (b - 128 s) Sx_g. The partial sums of the 8 waves meet in
+// LDS at the end and are added in wave order.
+//
+// Global loads are buffer loads (a uniform descriptor, a fixed 32-bit offset
+// per lane), all unconditional: a sub-chunk past the last group loads through
+// a descriptor of zero size, which returns zeros without touching memory. So
+// the sequence of loads is the same on every path and the waits stay exact.
+constexpr int kDecWaves = 8;
+constexpr int kDecThreads = 64 * kDecWaves;
+constexpr int kDecSubs = 4;                       // sub-chunks of 8 groups per chunk
+constexpr int kDecCG = 8 * kDecSubs;              // groups per chunk
+constexpr int kDecPitch = kDecCG * 32 + 16;       // LDS bytes per code row (conflict-free reads)
+constexpr int kBufWord3 = 0x00020000;             // raw buffer, 32-bit data format
 
 template <int MT>
-__global__ __launch_bounds__(1024) void qgemm_skinny_kernel(QgemmArgs a) {
-  constexpr int ROWS = 16 * MT;
-  constexpr int XCH = ROWS * 64 / 1024;  // 16-byte x pieces per thread per chunk
-  __shared__ __align__(16) uint16_t xs[2][ROWS][kSkPitch];
-  __shared__ __align__(16) float sx[2][kSkCG][ROWS];
+struct DecX {
+  u32x4 x[MT][2];
+};
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int nt = wave & 3, sl = wave >> 2;
+__device__ inline __amdgpu_buffer_rsrc_t buf_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, kBufWord3);
+}
+
+template <int MT, int NT>
+__global__ __launch_bounds__(kDecThreads) void qgemm_decode_kernel(QgemmArgs a) {
+  constexpr int ROWS = 16 * NT;
+  constexpr int WB = ROWS * kDecPitch;             // codes of a chunk
+  constexpr int SB = ROWS * kDecCG * 2;            // scales of a chunk (biases again)
+  constexpr int E = MT * NT * 256;                 // partial sums per wave
+  constexpr int RB = kDecWaves * E * 4;
+  constexpr int LB = WB + 2 * SB > RB ? WB + 2 * SB : RB;
+  constexpr int WP = ROWS * 32 / kDecThreads;      // 8-byte code pieces per thread per sub-chunk
+  static_assert(WP * kDecThreads == ROWS * 32, "even split");
+  __shared__ __align__(16) unsigned char lds[LB];
+  unsigned char* const sct = lds + WB;
+  unsigned char* const bit = lds + WB + SB;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l16 = lane & 15, lg = lane >> 4;
-  const int64_t n = (int64_t)blockIdx.x * 64 + nt * 16 + l16;
-  const int64_t nc = n < a.N ? n : a.N - 1;
-  const int KW = (int)(a.K / 8), G = (int)(a.K / 64), NC = G / kSkCG;
-  const uint32_t* wcol = a.w + nc * KW + 2 * lg;
-  const uint16_t* scol = a.sc + nc * G;
-  const uint16_t* bcol = a.bi + nc * G;
+  const int64_t n0 = (int64_t)blockIdx.x * ROWS;
+  const int KW = (int)(a.K / 8), G = (int)(a.K / 64);
 
-  auto fetch_w = [&](SkW& r, int c) {
-    const int g0 = c * kSkCG + 2 * sl;
-    r.w[0] = *reinterpret_cast<const u32x2_t*>(wcol + g0 * 8);
-    r.w[1] = *reinterpret_cast<const u32x2_t*>(wcol + (g0 + 1) * 8);
-    r.s = *reinterpret_cast<const uint32_t*>(scol + g0);
-    r.b = *reinterpret_cast<const uint32_t*>(bcol + g0);
-  };
-  // x pieces of one chunk: piece q = tid + 1024 i -> row q / 64, word q % 64
-  u32x4 xr[XCH];
-  auto load_x = [&](int c) {
-#pragma unroll
-    for (int i = 0; i < XCH; ++i) {
-      const int q = tid + 1024 * i, row = q >> 6, wd = q & 63;
-      const int64_t rr = row < a.M ? row : a.M - 1;
-      xr[i] = *reinterpret_cast<const u32x4*>(a.x + rr * a.xs + c * kSkCG * 64 + wd * 8);
-    }
-  };
-  auto stage = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < XCH; ++i) {
-      const int q = tid + 1024 * i, row = q >> 6, wd = q & 63;
-      *reinterpret_cast<u32x4*>(&xs[buf][row][wd * 8]) = xr[i];
-      const float s8 = sum8_lanes(sum8_bf16(xr[i]));
-      if ((wd & 7) == 0) sx[buf][wd >> 3][row] = s8;
-    }
-  };
+  const uint32_t xbytes = (uint32_t)(((int64_t)(a.M - 1) * a.xs + a.K) * 2);
+  const uint32_t wbytes = (uint32_t)(a.N * a.K / 2), sbytes = (uint32_t)(a.N * G * 2);
 
-  f32x4_t acc[MT];
+  // lane (l16, lg) supplies row l16 of each 16-row tile and, to the group's
+  // two MFMAs f = 0, 1, k = 32 f + 8 lg .. 32 f + 8 lg + 7 (code words lg and
+  // 4 + lg), so the four lanes of a row read 64 contiguous bytes of x per load
+  uint32_t xo[MT];
 #pragma unroll
-  for (int i = 0; i < MT; ++i) acc[i] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-
-  auto compute = [&](const SkW& r, int buf) {
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int gi = 2 * sl + h;
-      uint32_t w0 = r.w[h][0], w1 = r.w[h][1];
-      asm volatile("" : "+v"(w0), "+v"(w1));
-      const bf16x8_t b0 = expand_codes(w0);
-      const bf16x8_t b1 = expand_codes(w1);
-      const float s = h ? BF16::hi(r.s) : BF16::lo(r.s);
-      const float bp = (h ? BF16::hi(r.b) : BF16::lo(r.b)) - 128.0f * s;
-      f32x4_t cc[MT];
-#pragma unroll
-      for (int i = 0; i < MT; ++i) {
-        const bf16x8_t a0 = *reinterpret_cast<const bf16x8_t*>(&xs[buf][i * 16 + l16][gi * 64 + (2 * lg) * 8]);
-        const bf16x8_t a1 = *reinterpret_cast<const bf16x8_t*>(&xs[buf][i * 16 + l16][gi * 64 + (2 * lg + 1) * 8]);
-        cc[i] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-        cc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b0, cc[i], 0, 0, 0);
-        cc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1, cc[i], 0, 0, 0);
-      }
-#pragma unroll
-      for (int i = 0; i < MT; ++i) {
-        const f32x4_t sxr = *reinterpret_cast<const f32x4_t*>(&sx[buf][gi][i * 16 + 4 * lg]);
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr)
-          acc[i][rr] = __builtin_fmaf(s, cc[i][rr], __builtin_fmaf(bp, sxr[rr], acc[i][rr]));
-      }
-      // the group's update completes here: without it the MFMAs of every
-      // group are issued first and all their results held at once
-#pragma unroll
-      for (int i = 0; i < MT; ++i) asm volatile("" : "+v"(acc[i]));
-    }
-  };
-
-  SkW ra, rb;
-  fetch_w(ra, 0);
-  if (NC > 1) fetch_w(rb, 1);
-  load_x(0);
-  stage(0);
-  for (int c = 0; c < NC; c += 2) {
-    // chunk c (buffer 0, weights ra)
-    __syncthreads();
-    if (c + 1 < NC) load_x(c + 1);
-    compute(ra, 0);
-    if (c + 2 < NC) fetch_w(ra, c + 2);
-    if (c + 1 < NC) stage(1);
-    if (c + 1 >= NC) break;
-    // chunk c + 1 (buffer 1, weights rb)
-    __syncthreads();
-    if (c + 2 < NC) load_x(c + 2);
-    compute(rb, 1);
-    if (c + 3 < NC) fetch_w(rb, c + 3);
-    if (c + 2 < NC) stage(0);
+  for (int i = 0; i < MT; ++i) {
+    const int r = i * 16 + l16;
+    xo[i] = (uint32_t)((r < a.M ? r : a.M - 1) * a.xs * 2) + 16u * lg;
   }
-
-  // the four group slices' partial sums: slices 1..3 through LDS to slice 0
-  __syncthreads();
-  float* red = reinterpret_cast<float*>(&xs[0][0][0]);  // 3 x 4 x MT*4 x 64 floats
-  static_assert(3 * 4 * MT * 4 * 64 * 4 <= (int)sizeof(xs), "reduction fits the x buffers");
-  if (sl > 0) {
+  // this thread's share of a sub-chunk: code piece c = tid + 512 i is row
+  // c / 32, bytes 8 (c % 32) of the sub-chunk's 256; lane l < ROWS of wave 0
+  // loads the 16 bytes of scales of row l, of wave 1 those of biases
+  uint32_t wgo[WP];
 #pragma unroll
-    for (int i = 0; i < MT; ++i)
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr)
-        red[(((sl - 1) * 4 + nt) * MT * 4 + i * 4 + rr) * 64 + lane] = acc[i][rr];
+  for (int i = 0; i < WP; ++i) {
+    const int c = tid + kDecThreads * i;
+    const int64_t n = n0 + c / 32 < a.N ? n0 + c / 32 : a.N - 1;
+    wgo[i] = (uint32_t)(n * KW * 4) + 8u * (c % 32);
   }
-  __syncthreads();
-  if (sl > 0 || n >= a.N) return;
+  const bool sbl = wave < 2 && lane < ROWS;
+  const uint32_t sgo = (uint32_t)((n0 + lane < a.N ? n0 + lane : a.N - 1) * G * 2);
+
+  f32x4_t acc[MT][NT];
 #pragma unroll
   for (int i = 0; i < MT; ++i)
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      float v = acc[i][rr];
+    for (int t = 0; t < NT; ++t) acc[i][t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  const bf16x8_t ones = __builtin_bit_cast(bf16x8_t, u32x4{0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u});
+
+  for (int c0 = 0; c0 < G; c0 += kDecCG) {
+    if (c0 > 0) __syncthreads();  // the previous chunk's readers are done
+
+    // sub-chunk s covers groups c0 + 8 s .. c0 + 8 s + 7 (live when c0 + 8 s < G)
+    u32x2_t wv[kDecSubs][WP];
+    u32x4 sbv[kDecSubs];
+    auto load_sub = [&](int s) {
+      const uint32_t live = c0 + 8 * s < G ? 0xffffffffu : 0u;
+      const int g0 = (c0 + 8 * s) & (int)live;
+      const __amdgpu_buffer_rsrc_t bw = buf_rsrc(a.w, wbytes & live);
 #pragma unroll
-      for (int k = 0; k < 3; ++k) v += red[((k * 4 + nt) * MT * 4 + i * 4 + rr) * 64 + lane];
-      const int64_t m = i * 16 + 4 * lg + rr;
-      if (m < a.M) a.y[m * a.ys + n] = (uint16_t)(BF16::pack(v, 0.0f) & 0xffffu);
+      for (int i = 0; i < WP; ++i)
+        wv[s][i] = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(bw, wgo[i], g0 * 32, 0));
+      const __amdgpu_buffer_rsrc_t bs = buf_rsrc(wave == 0 ? a.sc : a.bi, wave < 2 ? sbytes & live : 0u);
+      sbv[s] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(bs, sgo, g0 * 2, 0));
+      asm volatile("" ::: "memory");
+    };
+    auto publish_sub = [&](int s) {
+#pragma unroll
+      for (int i = 0; i < WP; ++i) {
+        const int c = tid + kDecThreads * i;
+        *reinterpret_cast<u32x2_t*>(lds + (c / 32) * kDecPitch + s * 256 + 8 * (c % 32)) = wv[s][i];
+      }
+      if (sbl) *reinterpret_cast<u32x4*>((wave == 0 ? sct : bit) + lane * (kDecCG * 2) + s * 16) = sbv[s];
+    };
+    // this wave's group of sub-chunk s: x (zeros, without a memory access,
+    // past the last group)
+    auto fetch_x = [&](DecX<MT>& q, int s) {
+      const bool live = c0 + 8 * s < G;
+      const int g = live ? c0 + 8 * s + wave : 0;
+      const __amdgpu_buffer_rsrc_t bx = buf_rsrc(a.x, live ? xbytes : 0u);
+#pragma unroll
+      for (int i = 0; i < MT; ++i) {
+        q.x[i][0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(bx, xo[i], g * 128, 0));
+        q.x[i][1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(bx, xo[i] + 64, g * 128, 0));
+      }
+      asm volatile("" ::: "memory");
+    };
+    auto compute = [&](const DecX<MT>& q, int s) {
+      const int gl = 8 * s + wave;  // group within the chunk
+      bf16x8_t bw[NT][2];
+      float sc[NT], bp[NT];
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const int row = t * 16 + l16;
+        const unsigned char* wp = lds + row * kDecPitch + gl * 32 + lg * 4;
+        uint32_t w0 = *reinterpret_cast<const uint32_t*>(wp), w1 = *reinterpret_cast<const uint32_t*>(wp + 16);
+        asm volatile("" : "+v"(w0), "+v"(w1));
+        bw[t][0] = expand_codes(w0);
+        bw[t][1] = expand_codes(w1);
+        sc[t] = BF16::lo(*reinterpret_cast<const uint16_t*>(sct + row * (kDecCG * 2) + gl * 2));
+        bp[t] = BF16::lo(*reinterpret_cast<const uint16_t*>(bit + row * (kDecCG * 2) + gl * 2)) - 128.0f * sc[t];
+      }
+#pragma unroll
+      for (int i = 0; i < MT; ++i) {
+        const bf16x8_t a0 = __builtin_bit_cast(bf16x8_t, q.x[i][0]);
+        const bf16x8_t a1 = __builtin_bit_cast(bf16x8_t, q.x[i][1]);
+        f32x4_t sx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, ones, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+        sx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, ones, sx, 0, 0, 0);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          f32x4_t c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, bw[t][0], f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+          c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, bw[t][1], c, 0, 0, 0);
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            acc[i][t][r] = __builtin_fmaf(sc[t], c[r], __builtin_fmaf(bp[t], sx[r], acc[i][t][r]));
+        }
+        // the tile row's update completes here (otherwise every MFMA result
+        // of the group is held at once)
+#pragma unroll
+        for (int t = 0; t < NT; ++t) asm volatile("" : "+v"(acc[i][t]));
+      }
+    };
+
+    // two sub-chunks in flight: sub-chunk s + 2 is requested once the MFMAs
+    // of sub-chunk s are done, so those run while s + 1 is still arriving
+    DecX<MT> xr[2];
+    load_sub(0);
+    fetch_x(xr[0], 0);
+    load_sub(1);
+    fetch_x(xr[1], 1);
+#pragma unroll
+    for (int s = 0; s < kDecSubs; ++s) {
+      publish_sub(s);
+      __syncthreads();
+      if (c0 + 8 * s < G) compute(xr[s & 1], s);
+      if (s + 2 < kDecSubs) {
+        load_sub(s + 2);
+        fetch_x(xr[s & 1], s + 2);
+      }
     }
+  }
+
+  // partial sums -> LDS (over the chunk buffers); element e = ((i NT + t) 4 + r) 64 + lane
+  __syncthreads();
+  float* red = reinterpret_cast<float*>(lds);
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) red[wave * E + ((i * NT + t) * 4 + r) * 64 + lane] = acc[i][t][r];
+  __syncthreads();
+  for (int e = tid; e < E; e += kDecThreads) {
+    float v = red[e];
+#pragma unroll
+    for (int w = 1; w < kDecWaves; ++w) v += red[w * E + e];
+    const int ln = e & 63, r = (e >> 6) & 3, it = e >> 8;
+    const int t = it % NT, i = it / NT;
+    const int64_t m = i * 16 + 4 * (ln >> 4) + r;
+    const int64_t n = n0 + t * 16 + (ln & 15);
+    if (m < a.M && n < a.N) a.y[m * a.ys + n] = (uint16_t)(BF16::pack(v, 0.0f) & 0xffffu);
+  }
 }
 
 // ---------------------------------------------------------------- hi/lo
@@ -769,14 +829,35 @@ void gather_grouped_launch(const GatherArgs& a, hipStream_t s) {
   hipLaunchKernelGGL((gather_hl_kernel<8>), grid, dim3(512), 0, s, a);
 }
 
-bool skinny_launch(const QgemmArgs& a, hipStream_t s) {
-  if (a.K % (64 * kSkCG)) return false;
-  const dim3 grid((unsigned)((a.N + 63) / 64));
+template <int MT>
+void decode_launch_mt(const QgemmArgs& a, int nt, hipStream_t s) {
+  const dim3 grid((unsigned)((a.N + 16 * nt - 1) / (16 * nt))), block(kDecThreads);
+  switch (nt) {
+    case 1: hipLaunchKernelGGL((qgemm_decode_kernel<MT, 1>), grid, block, 0, s, a); break;
+    case 2: hipLaunchKernelGGL((qgemm_decode_kernel<MT, 2>), grid, block, 0, s, a); break;
+    default: hipLaunchKernelGGL((qgemm_decode_kernel<MT, 3>), grid, block, 0, s, a); break;
+  }
+}
+
+// The decode kernel takes K in sub-chunks of 512 and addresses x, the codes,
+// scales and biases with 32-bit buffer offsets.
+bool decode_fits(const QgemmArgs& a) {
+  const int64_t lim = (int64_t)1 << 31;
+  return a.K % 512 == 0 && ((a.M - 1) * a.xs + a.K) * 2 < lim && a.N * a.K / 2 < lim &&
+         a.N * (a.K / 64) * 2 < lim;
+}
+
+void decode_launch(const QgemmArgs& a, hipStream_t s) {
+  // the widest column tile (16 NT columns per block) that still gives every
+  // CU a block
+  // (three tiles at most: four hold more registers than a wave has at 64 rows)
+  int nt = 3;
+  while (nt > 1 && (a.N + 16 * nt - 1) / (16 * nt) < kCUs) --nt;
   switch ((a.M + 15) / 16) {
-    case 1: hipLaunchKernelGGL(qgemm_skinny_kernel<1>, grid, dim3(1024), 0, s, a); return true;
-    case 2: hipLaunchKernelGGL(qgemm_skinny_kernel<2>, grid, dim3(1024), 0, s, a); return true;
-    case 3: hipLaunchKernelGGL(qgemm_skinny_kernel<3>, grid, dim3(1024), 0, s, a); return true;
-    default: hipLaunchKernelGGL(qgemm_skinny_kernel<4>, grid, dim3(1024), 0, s, a); return true;
+    case 1: decode_launch_mt<1>(a, nt, s); break;
+    case 2: decode_launch_mt<2>(a, nt, s); break;
+    case 3: decode_launch_mt<3>(a, nt, s); break;
+    default: decode_launch_mt<4>(a, nt, s); break;
   }
 }
 
@@ -789,9 +870,8 @@ bool qgemm_supported(int dtype, int sdt, int group_size, int bits, const void* x
 
 void qgemm_launch(const QgemmArgs& a, hipStream_t s) {
   const unsigned gx = (unsigned)((a.N + kQgBN - 1) / kQgBN);
-  if (a.M <= 64 && skinny_launch(a, s)) return;
-  if (a.M <= 64) {
-    hipLaunchKernelGGL(qgemm_kernel<32>, dim3(gx, (unsigned)((a.M + 31) / 32)), dim3(256), 0, s, a);
+  if (a.M <= 64 && decode_fits(a)) {
+    decode_launch(a, s);
   } else if (a.M <= 512) {
     hipLaunchKernelGGL(qgemm_kernel<64>, dim3(gx, (unsigned)((a.M + 63) / 64)), dim3(256), 0, s, a);
   } else {
