@@ -213,10 +213,14 @@ __global__ __launch_bounds__(256) void qgemm_kernel(QgemmArgs a) {
 // straight from global memory into its MFMA A registers (the waves read
 // disjoint slices of x; each A fragment serves NT column tiles). Per group a
 // wave runs the exact-product MFMAs C_g = x . (128 + q) of its MT x NT tiles
-// (B from LDS) and, against a B of ones, the row sums Sx_g, which come out in
-// the accumulator layout (lane l gets rows 4 (l / 16) + r); then
-// acc += s C_g + (b - 128 s) Sx_g. The partial sums of the 8 waves meet in
-// LDS at the end and are added in wave order.
+// (B from LDS) and acc += s C_g; two more MFMAs of ones against x^T give the
+// row sums Sx_g (every output of lane (l16, lg) is the sum of row l16). The
+// bias term sum_g (b - 128 s)[n, g] Sx_g[m] of a chunk's four sub-chunks is
+// one f32 MFMA (16 x 16 x 4) per tile, with k = the sub-chunk. The partial
+// sums of the 8 waves meet in LDS at the end and are added in wave order.
+// (Staging x through LDS as well, with contiguous 1 KB loads, measured no
+// faster: the per-sub-chunk load volume, mostly x re-read by every CU, and
+// not the access pattern, sets the pace.)
 //
 // Global loads are buffer loads (a uniform descriptor, a fixed 32-bit offset
 // per lane), all unconditional: a sub-chunk past the last group loads through
@@ -243,8 +247,7 @@ __global__ __launch_bounds__(kDecThreads) void qgemm_decode_kernel(QgemmArgs a) 
   constexpr int ROWS = 16 * NT;
   constexpr int WB = ROWS * kDecPitch;             // codes of a chunk
   constexpr int SB = ROWS * kDecCG * 2;            // scales of a chunk (biases again)
-  constexpr int E = MT * NT * 256;                 // partial sums per wave
-  constexpr int RB = kDecWaves * E * 4;
+  constexpr int RB = kDecWaves * MT * NT * 256 * 4;  // partial sums of the 8 waves
   constexpr int LB = WB + 2 * SB > RB ? WB + 2 * SB : RB;
   constexpr int WP = ROWS * 32 / kDecThreads;      // 8-byte code pieces per thread per sub-chunk
   static_assert(WP * kDecThreads == ROWS * 32, "even split");
@@ -328,10 +331,13 @@ __global__ __launch_bounds__(kDecThreads) void qgemm_decode_kernel(QgemmArgs a) 
       }
       asm volatile("" ::: "memory");
     };
+    // the row sums of this wave's group in each sub-chunk, row l16 of each
+    // 16-row tile (the bias term is applied once per chunk, below)
+    float sxs[kDecSubs][MT];
     auto compute = [&](const DecX<MT>& q, int s) {
       const int gl = 8 * s + wave;  // group within the chunk
       bf16x8_t bw[NT][2];
-      float sc[NT], bp[NT];
+      float sc[NT];
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
         const int row = t * 16 + l16;
@@ -341,21 +347,21 @@ __global__ __launch_bounds__(kDecThreads) void qgemm_decode_kernel(QgemmArgs a) 
         bw[t][0] = expand_codes(w0);
         bw[t][1] = expand_codes(w1);
         sc[t] = BF16::lo(*reinterpret_cast<const uint16_t*>(sct + row * (kDecCG * 2) + gl * 2));
-        bp[t] = BF16::lo(*reinterpret_cast<const uint16_t*>(bit + row * (kDecCG * 2) + gl * 2)) - 128.0f * sc[t];
       }
 #pragma unroll
       for (int i = 0; i < MT; ++i) {
         const bf16x8_t a0 = __builtin_bit_cast(bf16x8_t, q.x[i][0]);
         const bf16x8_t a1 = __builtin_bit_cast(bf16x8_t, q.x[i][1]);
-        f32x4_t sx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, ones, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-        sx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, ones, sx, 0, 0, 0);
+        // ones . x^T: every output of lane (l16, lg) is the row sum of row l16
+        f32x4_t sx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, a0, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+        sx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, a1, sx, 0, 0, 0);
+        sxs[s][i] = sx[0];
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
           f32x4_t c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, bw[t][0], f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
           c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, bw[t][1], c, 0, 0, 0);
 #pragma unroll
-          for (int r = 0; r < 4; ++r)
-            acc[i][t][r] = __builtin_fmaf(sc[t], c[r], __builtin_fmaf(bp[t], sx[r], acc[i][t][r]));
+          for (int r = 0; r < 4; ++r) acc[i][t][r] = __builtin_fmaf(sc[t], c[r], acc[i][t][r]);
         }
         // the tile row's update completes here (otherwise every MFMA result
         // of the group is held at once)
@@ -375,33 +381,61 @@ __global__ __launch_bounds__(kDecThreads) void qgemm_decode_kernel(QgemmArgs a) 
     for (int s = 0; s < kDecSubs; ++s) {
       publish_sub(s);
       __syncthreads();
-      if (c0 + 8 * s < G) compute(xr[s & 1], s);
+      if (c0 + 8 * s < G) {
+        compute(xr[s & 1], s);
+      } else {
+#pragma unroll
+        for (int i = 0; i < MT; ++i) sxs[s][i] = 0.0f;
+      }
       if (s + 2 < kDecSubs) {
         load_sub(s + 2);
         fetch_x(xr[s & 1], s + 2);
       }
     }
+    // bias term of the wave's 4 groups, sum_g (b - 128 s)[n, g] Sx_g[m], as one
+    // f32 MFMA (16 x 16 x 4) per tile: k = the sub-chunk, lane (l16, lg)
+    // supplies Sx of row l16 and (b - 128 s) of column l16 for sub-chunk lg
+    // (zero past the last group: x and the scales read zeros there)
+    const int glb = 8 * lg + wave;
+    float bsel[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const int row = t * 16 + l16;
+      const float sv = BF16::lo(*reinterpret_cast<const uint16_t*>(sct + row * (kDecCG * 2) + glb * 2));
+      bsel[t] = BF16::lo(*reinterpret_cast<const uint16_t*>(bit + row * (kDecCG * 2) + glb * 2)) - 128.0f * sv;
+    }
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+      const float asel = lg == 0 ? sxs[0][i] : lg == 1 ? sxs[1][i] : lg == 2 ? sxs[2][i] : sxs[3][i];
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+        acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x4f32(asel, bsel[t], acc[i][t], 0, 0, 0);
+    }
   }
 
-  // partial sums -> LDS (over the chunk buffers); element e = ((i NT + t) 4 + r) 64 + lane
+  // partial sums -> LDS (over the chunk buffers), one 16-byte tile fragment
+  // per lane: fragment f = (i NT + t) 64 + lane
   __syncthreads();
-  float* red = reinterpret_cast<float*>(lds);
+  f32x4_t* red = reinterpret_cast<f32x4_t*>(lds);
+  constexpr int F = MT * NT * 64;
 #pragma unroll
   for (int i = 0; i < MT; ++i)
 #pragma unroll
-    for (int t = 0; t < NT; ++t)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) red[wave * E + ((i * NT + t) * 4 + r) * 64 + lane] = acc[i][t][r];
+    for (int t = 0; t < NT; ++t) red[wave * F + (i * NT + t) * 64 + lane] = acc[i][t];
   __syncthreads();
-  for (int e = tid; e < E; e += kDecThreads) {
-    float v = red[e];
+  for (int f = tid; f < F; f += kDecThreads) {
+    f32x4_t v = red[f];
 #pragma unroll
-    for (int w = 1; w < kDecWaves; ++w) v += red[w * E + e];
-    const int ln = e & 63, r = (e >> 6) & 3, it = e >> 8;
+    for (int w = 1; w < kDecWaves; ++w) v += red[w * F + f];
+    const int ln = f & 63, it = f >> 6;
     const int t = it % NT, i = it / NT;
-    const int64_t m = i * 16 + 4 * (ln >> 4) + r;
     const int64_t n = n0 + t * 16 + (ln & 15);
-    if (m < a.M && n < a.N) a.y[m * a.ys + n] = (uint16_t)(BF16::pack(v, 0.0f) & 0xffffu);
+    if (n >= a.N) continue;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t m = i * 16 + 4 * (ln >> 4) + r;
+      if (m < a.M) a.y[m * a.ys + n] = (uint16_t)(BF16::pack(v[r], 0.0f) & 0xffffu);
+    }
   }
 }
 
