@@ -4,11 +4,13 @@
 //   w_q    [vocab, hidden/8]          u32, 8 codes per word, low nibble first
 //   scales [vocab, hidden/group]      bf16 or f16
 //   biases [vocab, hidden/group]      same dtype as scales
-// One wave64 owns one token: each lane reads 16 bytes of packed codes (32
-// codes) per step and its group's scale/bias, and writes 64 bytes of output,
-// so a token's row (hidden/2 bytes of codes) is one coalesced burst and the
-// write (4x larger) is fully vectorised. The table is never dequantized as a
-// whole (QEmbedding::forward does that on every call in the reference).
+// One wave64 owns one token: at step s lane i reads packed word s*64 + i
+// (8 codes) and its group's scale/bias and writes those 8 outputs, so every
+// load instruction reads 256 contiguous bytes of the row and every store
+// writes 1 KB contiguous (a lane owning 16 contiguous bytes of codes and
+// 64 bytes of output measured 2.5x slower: each instruction then touched
+// every line of the row). The table is never dequantized as a whole
+// (QEmbedding::forward does that on every call in the reference).
 //
 // Arithmetic (MLX dequantize, S = scales dtype):
 //   v = round_S(round_S(q * s) + b);  optionally v = round_S(v * round_S(scale))
