@@ -37,9 +37,12 @@ struct GatherArgs {
 // Pairs per expert (on average) from which the grouped kernel runs.
 constexpr int64_t kGatherMinPairsPerExpert = 16;
 
-// bf16, group 64, 4 bits, x 16-byte aligned rows, w 16-byte aligned, K % 64.
+// bf16, group 64, 4 bits, x 16-byte aligned rows, w 16-byte aligned, K % 64,
+// the expert ids 16-byte aligned and a multiple of 4 (read 4 at a time: a
+// partly out-of-range 16-byte buffer load is not relied on) and under 2 GiB.
 bool gather_grouped_supported(int dtype, int sdt, int group_size, int bits, const void* x,
-                              int64_t xs, const void* w, int64_t k);
+                              int64_t xs, const void* w, int64_t k, const void* experts,
+                              int64_t pairs);
 void gather_grouped_launch(const GatherArgs& a, hipStream_t s);
 
 // Rows of x at or above which the MFMA kernel runs (below: one GEMV per row).

@@ -703,25 +703,46 @@ __global__ __launch_bounds__(WAVES * 64) void gather_hl_kernel(GatherArgs a) {
   }
   const int wcn = tid / (8 / WPT), wpart = tid % (8 / WPT);
 
+  // the expert ids as stored (converted where compared); thread tid reads ids
+  // base + RND tid .. + RND - 1 of a round with 16-byte buffer loads (ids past
+  // the last pair read zeros and are never listed)
+  auto id_of = [&](uint32_t raw) -> int64_t {
+    if (a.experts_i32) {
+      const int64_t v = (int32_t)raw;
+      return v < 0 ? v + a.E : v;
+    }
+    return (int64_t)raw;
+  };
+  static_assert(RND % 4 == 0, "whole 16-byte id loads");
+  const __amdgpu_buffer_rsrc_t rid = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<void*>(a.experts), (short)0, (int)(a.pairs * 4), 0x00020000);
+  // one round's ids, kept raw; the next round's are requested before the
+  // current round is compared, so the scan pays the load latency once
+  uint32_t cur[RND], nxt[RND];
+  auto load_round = [&](uint32_t (&r)[RND], int64_t base) {
+    const bool live = base < a.pairs;
+#pragma unroll
+    for (int c = 0; c < RND / 4; ++c) {
+      const uint32_t off = live ? (uint32_t)((base + RND * tid + 4 * c) * 4) : 0x80000000u;
+      const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rid, off, 0, 0));
+#pragma unroll
+      for (int k = 0; k < 4; ++k) r[4 * c + k] = v[k];
+    }
+  };
   int64_t scan = 0;
+  load_round(cur, 0);
   while (scan < a.pairs) {
-    // ---- fill the list from `scan` (1024 ids per round, stop before overflow)
+    // ---- fill the list from `scan` (kGaRoundIds ids per round, stop before overflow)
     __syncthreads();
     if (tid == 0) cnt = 0;
     __syncthreads();
     while (scan < a.pairs) {
       if (cnt > kGaCap - kGaRoundIds) break;  // uniform: read after the round's barrier
-      // all of the round's id loads go out before any is compared
-      int64_t ep[RND];
+      load_round(nxt, scan + kGaRoundIds);
 #pragma unroll
       for (int i = 0; i < RND; ++i) {
-        const int64_t p = scan + i * T + tid;
-        ep[i] = ga_expert(a, p < a.pairs ? p : a.pairs - 1);
-      }
-#pragma unroll
-      for (int i = 0; i < RND; ++i) {
-        const int64_t p = scan + i * T + tid;
-        const bool m = p < a.pairs && ep[i] == e;
+        const int64_t p = scan + RND * tid + i;
+        const bool m = p < a.pairs && id_of(cur[i]) == e;
         const uint64_t mask = __ballot(m);
         if (mask) {  // uniform per wave
           int base = 0;
@@ -730,6 +751,8 @@ __global__ __launch_bounds__(WAVES * 64) void gather_hl_kernel(GatherArgs a) {
           if (m) list[base + __popcll(mask & ((1ull << lane) - 1ull))] = (int32_t)p;
         }
       }
+#pragma unroll
+      for (int i = 0; i < RND; ++i) cur[i] = nxt[i];
       scan += kGaRoundIds;
       __syncthreads();
     }
@@ -875,10 +898,13 @@ __global__ __launch_bounds__(WAVES * 64) void gather_hl_kernel(GatherArgs a) {
 }
 
 bool gather_grouped_supported(int dtype, int sdt, int group_size, int bits, const void* x,
-                              int64_t xs, const void* w, int64_t k) {
+                              int64_t xs, const void* w, int64_t k, const void* experts,
+                              int64_t pairs) {
   return dtype == DT_BF16 && sdt == DT_BF16 && group_size == 64 && bits == 4 && k % 64 == 0 &&
          (reinterpret_cast<uintptr_t>(x) & 15) == 0 && xs % 8 == 0 &&
-         (reinterpret_cast<uintptr_t>(w) & 15) == 0;
+         (reinterpret_cast<uintptr_t>(w) & 15) == 0 &&
+         (reinterpret_cast<uintptr_t>(experts) & 15) == 0 && pairs % 4 == 0 &&
+         pairs * 4 < ((int64_t)1 << 31);
 }
 
 void gather_grouped_launch(const GatherArgs& a, hipStream_t s) {
@@ -887,6 +913,9 @@ void gather_grouped_launch(const GatherArgs& a, hipStream_t s) {
   const int64_t ntiles = (a.N + kHlBN - 1) / kHlBN;
   int64_t gx = 2048 / (a.E + 1);
   gx = gx < 1 ? 1 : (gx > ntiles ? ntiles : gx);
+  // no block without a column tile (it would scan for nothing)
+  const int64_t tpg = (ntiles + gx - 1) / gx;
+  gx = (ntiles + tpg - 1) / tpg;
   const dim3 grid((unsigned)gx, (unsigned)(a.E + 1));
   // 8 waves (2 per SIMD) measured 1.44x faster than 4 waves of 64 x 64 tiles
   hipLaunchKernelGGL((gather_hl_kernel<8>), grid, dim3(512), 0, s, a);

@@ -286,7 +286,8 @@ extern "C" int hgk_gather_qmm(int dtype, const void* x, int64_t x_rows, int64_t 
   const hipStream_t s = as_stream(stream);
   // many pairs per expert (prefill): grouped by expert on the matrix cores
   if (pairs >= kGatherMinPairsPerExpert * n_experts && n_experts < 65535 &&
-      gather_grouped_supported(dtype, scales_dtype, group_size, bits, x, x_row_stride, w, k)) {
+      gather_grouped_supported(dtype, scales_dtype, group_size, bits, x, x_row_stride, w, k,
+                               rhs_indices, pairs)) {
     GatherArgs g{};
     g.x = static_cast<const uint16_t*>(x); g.xrows = x_rows; g.xs = x_row_stride;
     g.xdiv = x_row_div > 0 ? x_row_div : 1; g.lhs = lhs_indices; g.w = w;

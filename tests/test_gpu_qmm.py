@@ -175,3 +175,15 @@ def test_grouped_path_routing_and_out_of_range(dev):
     ref = O.gather_qmm(x, O.BF16, w, s, b, O.BF16, ex, lhs=lhs)
     _check(got, ref, O.BF16, "grouped routing")
     assert not got[5].any() and not got[7].any() and got[2300].any() and got[9].any()
+
+
+def test_grouped_size_with_unaligned_pair_count(dev):
+    """A pair count that is not a multiple of 4 (the grouped kernel reads the
+    expert ids 16 bytes at a time, so it leaves such a call to the per-pair
+    kernel) gives the oracle's result, including the last pairs."""
+    P, R, E, N, K = 4098, 600, 8, 128, 512
+    x, w, s, b, ex = _case(2421, P, R, E, N, K)
+    got = _run(dev, x, w, s, b, ex, O.BF16, x_div=7)
+    ref = O.gather_qmm(x, O.BF16, w, s, b, O.BF16, ex, x_div=7)
+    _check(got, ref, O.BF16, "unaligned pair count")
+    _check(got[-2:], ref[-2:], O.BF16, "last pairs")
