@@ -297,8 +297,10 @@ void launch_fast(RopeArgs& a, hipStream_t s) {
   // as many tokens per block as keep every lane group's rows in one batch of
   // loads, but enough blocks to fill the chip
   const int slots = 256 / LPR;
+  // (stepping down one token at a time: halving from 6 to 3 at the Llama
+  // chain's 4096 tokens x 40 heads measured 8% slower than 4)
   int tpb = std::max(1, std::min((slots * kRopeBatch) / a.hsum, kMaxTpb));
-  while (tpb > 1 && (a.tokens + tpb - 1) / tpb < 1024u) tpb = (tpb + 1) / 2;
+  while (tpb > 1 && (a.tokens + tpb - 1) / tpb < 1024u) --tpb;
   a.tpb = tpb;
   const unsigned blocks = (a.tokens + tpb - 1) / tpb;
   const size_t shmem = 2u * tpb * a.half * sizeof(float);
