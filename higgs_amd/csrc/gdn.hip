@@ -684,6 +684,392 @@ __global__ __launch_bounds__(256) void gated_delta_token_kernel(GdnArgs a) {
   }
 }
 
+// ---------------------------------------------------------------- WY chunks
+// bf16 prefill with the fused q/k norm at Dk = 128: the chunked (WY) form of
+// the same recurrence, on the matrix cores. Per chunk of C = 64 steps with
+// lam_t = sum_{u <= t} log g_u (log g = -exp(a_log) * softplus(a + dt_bias),
+// the exponent of the reference's g) and the block's 64 state rows S (f32):
+//   L = strictly_lower(beta_i e^{lam_i - lam_j} k_i.k_j)
+//   R = beta * (V - e^lam * (K S^T))
+//   Delta = (I + L)^{-1} R
+//   Y = e^lam * (Q S^T) + lower(e^{lam_i - lam_j} q_i.k_j) Delta
+//   S <- e^{lam_C} S + (e^{lam_C - lam} * Delta)^T K
+// which unrolls the per-step update s = s*g; d = (v - s.k)*beta; s += k*d;
+// y = s.q exactly (in exact arithmetic). Step by step this is the
+// reference's recurrence; only the rounding differs, as for the other kernels.
+// Products: k.k and q.k on v_mfma_f32_16x16x32_bf16 (the normalised q and k
+// are bf16, so every product is exact in the f32 accumulator); K S^T, Q S^T
+// and the state update on the same instruction with the f32 operand split
+// into bf16 hi + lo (relative error ~2^-17); the triangular solve and M Delta
+// on v_mfma_f32_16x16x4_f32 (f32 throughout): 16 x 16 diagonal blocks of
+// (I + L) inverted by forward substitution, the rest by blocked substitution.
+// A block owns (b, v-head, 64 state rows), 8 waves, the state in LDS for the
+// whole sequence; the next chunk's q, k, v, a, b are loaded during the current
+// chunk's products. Steps past T in the last chunk are zero rows (k = q = v =
+// beta = 0, log g = 0), which leave S unchanged.
+typedef __bf16 wy_bf8 __attribute__((ext_vector_type(8)));
+typedef float wy_f4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWyC = 64;             // steps per chunk
+constexpr int kWyDK = 128;           // head_k_dim
+constexpr int kWyRows = 64;          // state rows per block
+constexpr int kWySP = kWyDK + 4;     // f32 pitch of the state rows
+constexpr int kWyKP = kWyDK + 8;     // bf16 pitch of k / q rows
+constexpr int kWyTP = kWyC + 8;      // bf16 pitch of k^T rows and of the v / y staging rows
+constexpr int kWyLP = kWyC + 4;      // f32 pitch of L, M and R^T / Delta^T rows
+constexpr int64_t kWyMinSteps = 64;  // shorter sequences take the chunk kernel
+
+struct WyLds {
+  float S[kWyRows][kWySP];
+  uint16_t Kh[kWyC][kWyKP];
+  uint16_t Qh[kWyC][kWyKP];
+  uint16_t KT[kWyDK][kWyTP];
+  float L[kWyC][kWyLP];     // after the solve: the y staging rows (bf16, pitch kWyTP)
+  float M[kWyC][kWyLP];
+  float RD[kWyRows][kWyLP];  // R^T, overwritten block by block with Delta^T ([row][step])
+  float Td[4][16][20];       // inverses of the 16 x 16 diagonal blocks of I + L
+  uint16_t V[kWyC][kWyTP];
+  float lam[kWyC], beta[kWyC], eL[kWyC], eC[kWyC];
+};
+
+// One chunk's raw global loads of one thread.
+struct WyRaw {
+  u32x4 qk[4];  // 32 elements of a k row (threads 0..255) or a q row (256..511)
+  u32x4 v;      // 8 elements of a v row
+  uint32_t a, b;  // wave 0: step (lane)'s a and b
+};
+
+__device__ inline void wy_fetch(const GdnArgs& g, WyRaw& r, int64_t bi, int64_t hk, int64_t hv,
+                                int64_t dv0, int64_t t0, int tid, bool wave0) {
+  const int64_t last = g.T - 1;
+  {
+    const int row = tid >> 2, part = tid & 3;
+    const int64_t t = t0 + (row & 63) < last ? t0 + (row & 63) : last;
+    const void* src = row < 64 ? g.k : g.q;
+    const u32x4* p = reinterpret_cast<const u32x4*>(
+        reinterpret_cast<const uint16_t*>(src) + ((bi * g.T + t) * g.Hk + hk) * kWyDK + 32 * part);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) r.qk[c] = p[c];
+  }
+  {
+    const int s = tid >> 3, part = tid & 7;
+    const int64_t t = t0 + s < last ? t0 + s : last;
+    r.v = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(g.v) +
+                                          ((bi * g.T + t) * g.Hv + hv) * g.Dv + dv0 + 8 * part);
+  }
+  if (wave0) {
+    const int lane = tid & 63;
+    const int64_t t = t0 + lane < last ? t0 + lane : last;
+    r.a = ldraw<BF16>(g.a, (bi * g.T + t) * g.Hv + hv);
+    r.b = ldraw<BF16>(g.b, (bi * g.T + t) * g.Hv + hv);
+  }
+}
+
+// Eight f32 values as bf16 hi and lo parts (x = hi + lo + O(2^-17 |x|)).
+__device__ inline void wy_split(const float* x, wy_bf8& hi, wy_bf8& lo) {
+  u32x4 h, l;
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    h[p] = BF16::pack(x[2 * p], x[2 * p + 1]);
+    l[p] = BF16::pack(x[2 * p] - BF16::lo(h[p]), x[2 * p + 1] - BF16::hi(h[p]));
+  }
+  hi = __builtin_bit_cast(wy_bf8, h);
+  lo = __builtin_bit_cast(wy_bf8, l);
+}
+
+__device__ inline wy_f4 wy_ld4(const float* p) { return *reinterpret_cast<const wy_f4*>(p); }
+__device__ inline wy_bf8 wy_ld8(const uint16_t* p) { return *reinterpret_cast<const wy_bf8*>(p); }
+
+__device__ inline void wy_wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__global__ __launch_bounds__(512) void gated_delta_wy_kernel(GdnArgs g) {
+  __shared__ __align__(16) WyLds sm;
+  const int tid = threadIdx.x;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63, l16 = lane & 15, lg = lane >> 4;
+  const int64_t hv = blockIdx.y, bi = blockIdx.z;
+  const int64_t hk = (int)blockIdx.y / g.hgrp;
+  const int64_t dv0 = (int64_t)blockIdx.x * kWyRows;
+  const int64_t srow0 = (bi * g.Hv + hv) * g.Dv + dv0;
+
+  // the state rows, f32 in LDS
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int c = tid + 512 * h, row = c >> 4, part = c & 15;
+    float x[8];
+    if (g.state_in) {
+      const u32x4 raw = *reinterpret_cast<const u32x4*>(
+          reinterpret_cast<const uint16_t*>(g.state_in) + (srow0 + row) * kWyDK + 8 * part);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = elem<BF16>(raw, e);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = 0.0f;
+    }
+    *reinterpret_cast<wy_f4*>(&sm.S[row][8 * part]) = wy_f4{x[0], x[1], x[2], x[3]};
+    *reinterpret_cast<wy_f4*>(&sm.S[row][8 * part + 4]) = wy_f4{x[4], x[5], x[6], x[7]};
+  }
+  // this thread's norm weights (k for rows 0..63, q for 64..127)
+  const int nrow = tid >> 2, npart = tid & 3;
+  const bool isk = nrow < 64;
+  u32x4 wraw[4];
+  {
+    const u32x4* p = reinterpret_cast<const u32x4*>(
+        reinterpret_cast<const uint16_t*>(isk ? g.kw : g.qw) + 32 * npart);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) wraw[c] = p[c];
+  }
+  const float A = expf(load_param(g.a_log, g.pdt, hv));
+  const float dtb = load_param(g.dt_bias, g.pdt, hv);
+
+  WyRaw raw;
+  wy_fetch(g, raw, bi, hk, hv, dv0, 0, tid, w == 0);
+  const int64_t nch = (g.T + kWyC - 1) / kWyC;
+  const int rt = w & 3;                  // this wave's 16-row tile of the state rows
+  const int tA = w < 4 ? 0 : 1, tB = w < 4 ? 3 : 2;  // its two step tiles (balanced for M Delta)
+
+  for (int64_t ch = 0; ch < nch; ++ch) {
+    const int64_t t0 = ch * kWyC;
+    const int n = (int)(g.T - t0 < kWyC ? g.T - t0 : kWyC);
+
+    // ---- A: normalised k / q rows (bf16) and k^T, v, gates into LDS
+    {
+      const int t = nrow & 63;
+      float x[32];
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[8 * c + e] = elem<BF16>(raw.qk[c], e);
+      double ss = 0.0;
+#pragma unroll
+      for (int i = 0; i < 32; ++i) ss = __builtin_fma((double)x[i], (double)x[i], ss);
+      ss = group_sum<4>(ss);
+      const float rs = rms_scale(ss, g.inv_dk, g.eps);
+      const bool live = t < n;
+#pragma unroll
+      for (int i = 0; i < 32; ++i)
+        x[i] = live ? BF16::round(BF16::round(x[i] * rs) * elem<BF16>(wraw[i >> 3], i & 7)) : 0.0f;
+      uint16_t* dst = isk ? &sm.Kh[t][32 * npart] : &sm.Qh[t][32 * npart];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        u32x4 o;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) o[p] = BF16::pack(x[8 * c + 2 * p], x[8 * c + 2 * p + 1]);
+        *reinterpret_cast<u32x4*>(dst + 8 * c) = o;
+      }
+      if (isk) {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) sm.KT[32 * npart + i][t] = (uint16_t)(f2u(x[i]) >> 16);
+      }
+    }
+    {
+      const int s = tid >> 3, part = tid & 7;
+      *reinterpret_cast<u32x4*>(&sm.V[s][8 * part]) = s < n ? raw.v : u32x4{0u, 0u, 0u, 0u};
+    }
+    if (w == 0) {
+      const bool live = lane < n;
+      const float x = BF16::lo(raw.a) + dtb;
+      const float sp = fmaxf(x, 0.0f) + log1pf(expf(-fabsf(x)));
+      float lg_ = live ? -A * sp : 0.0f;
+      const float be = live ? 1.0f / (1.0f + expf(-BF16::lo(raw.b))) : 0.0f;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const float u = __shfl_up(lg_, o, 64);
+        if (lane >= o) lg_ += u;
+      }
+      const float lamC = __shfl(lg_, 63, 64);
+      sm.lam[lane] = lg_;
+      sm.beta[lane] = be;
+      sm.eL[lane] = expf(lg_);
+      sm.eC[lane] = expf(lamC - lg_);
+    }
+    __syncthreads();
+
+    // the next chunk's loads fly during this chunk's products (the last chunk
+    // reloads its own steps, clamped into range)
+    wy_fetch(g, raw, bi, hk, hv, dv0, ch + 1 < nch ? t0 + kWyC : t0, tid, w == 0);
+
+    // ---- B1: k.k and q.k tiles on or below the diagonal -> L, M
+    for (int job = w; job < 20; job += 8) {
+      const bool isq = job >= 10;
+      const int jj = isq ? job - 10 : job;
+      const int i = jj >= 6 ? 3 : jj >= 3 ? 2 : jj >= 1 ? 1 : 0;
+      const int j = jj - i * (i + 1) / 2;
+      const uint16_t* X = isq ? &sm.Qh[16 * i + l16][0] : &sm.Kh[16 * i + l16][0];
+      const uint16_t* Kr = &sm.Kh[16 * j + l16][0];
+      wy_f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wy_ld8(X + 32 * ks + 8 * lg),
+                                                      wy_ld8(Kr + 32 * ks + 8 * lg), acc, 0, 0, 0);
+      const int tj = 16 * j + l16;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int ti = 16 * i + 4 * lg + r;
+        const float dec = expf(sm.lam[ti] - sm.lam[tj]);
+        if (isq) sm.M[ti][tj] = tj <= ti ? dec * acc[r] : 0.0f;
+        else sm.L[ti][tj] = tj < ti ? sm.beta[ti] * dec * acc[r] : 0.0f;
+      }
+    }
+
+    // ---- B2: K S^T -> R^T, and e^lam * Q S^T kept for y
+    wy_f4 yacc[2];
+    {
+      wy_bf8 sh[4], sl[4];
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const float* sp = &sm.S[16 * rt + l16][32 * ks + 8 * lg];
+        const wy_f4 a0 = wy_ld4(sp), a1 = wy_ld4(sp + 4);
+        const float x[8] = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+        wy_split(x, sh[ks], sl[ks]);
+      }
+#pragma unroll
+      for (int ts = 0; ts < 2; ++ts) {
+        const int tt = ts ? tB : tA;
+        wy_f4 p = {0.0f, 0.0f, 0.0f, 0.0f}, qs = p;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          const wy_bf8 ak = wy_ld8(&sm.Kh[16 * tt + l16][32 * ks + 8 * lg]);
+          const wy_bf8 aq = wy_ld8(&sm.Qh[16 * tt + l16][32 * ks + 8 * lg]);
+          p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak, sh[ks], p, 0, 0, 0);
+          p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak, sl[ks], p, 0, 0, 0);
+          qs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aq, sh[ks], qs, 0, 0, 0);
+          qs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aq, sl[ks], qs, 0, 0, 0);
+        }
+        const int rr = 16 * rt + l16;
+        wy_f4 rv;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int t = 16 * tt + 4 * lg + r;
+          const float vv = BF16::lo((uint32_t)sm.V[t][rr]);
+          rv[r] = sm.beta[t] * (vv - sm.eL[t] * p[r]);
+          yacc[ts][r] = sm.eL[t] * qs[r];
+        }
+        *reinterpret_cast<wy_f4*>(&sm.RD[rr][16 * tt + 4 * lg]) = rv;
+      }
+    }
+    __syncthreads();
+
+    // ---- C: Delta = (I + L)^{-1} R, waves 0..3, one 16-row tile of the state each
+    if (w < 4) {
+      {
+        // column l16 of the inverse of diagonal block lg, by forward substitution;
+        // every wave computes all four blocks and writes the same values
+        float x[16];
+        const int o = 16 * lg;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+          float s = k == l16 ? 1.0f : 0.0f;
+#pragma unroll
+          for (int m = 0; m < k; ++m) s = __builtin_fmaf(-sm.L[o + k][o + m], x[m], s);
+          x[k] = s;
+        }
+#pragma unroll
+        for (int k = 0; k < 16; ++k) sm.Td[lg][k][l16] = x[k];
+      }
+      wy_wave_sync();
+      const int rr = 16 * rt + l16;
+      wy_f4 dl[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        wy_f4 s = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int j = 0; j < i; ++j) {
+          const wy_f4 a4 = wy_ld4(&sm.L[16 * i + l16][16 * j + 4 * lg]);
+#pragma unroll
+          for (int m = 0; m < 4; ++m) s = __builtin_amdgcn_mfma_f32_16x16x4f32(a4[m], dl[j][m], s, 0, 0, 0);
+        }
+        const wy_f4 acc = wy_ld4(&sm.RD[rr][16 * i + 4 * lg]) - s;
+        const wy_f4 td = wy_ld4(&sm.Td[i][l16][4 * lg]);
+        wy_f4 d = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int m = 0; m < 4; ++m) d = __builtin_amdgcn_mfma_f32_16x16x4f32(td[m], acc[m], d, 0, 0, 0);
+        dl[i] = d;
+        *reinterpret_cast<wy_f4*>(&sm.RD[rr][16 * i + 4 * lg]) = d;
+      }
+    }
+    __syncthreads();
+
+    // ---- D1: y = e^lam * Q S^T + M Delta, staged as bf16 in L's space
+    uint16_t* ys = reinterpret_cast<uint16_t*>(&sm.L[0][0]);
+    {
+      const int rr = 16 * rt + l16;
+#pragma unroll
+      for (int ts = 0; ts < 2; ++ts) {
+        const int tt = ts ? tB : tA;
+        wy_f4 y = yacc[ts];
+        for (int j = 0; j <= tt; ++j) {
+          const wy_f4 a4 = wy_ld4(&sm.M[16 * tt + l16][16 * j + 4 * lg]);
+          const wy_f4 b4 = wy_ld4(&sm.RD[rr][16 * j + 4 * lg]);
+#pragma unroll
+          for (int m = 0; m < 4; ++m) y = __builtin_amdgcn_mfma_f32_16x16x4f32(a4[m], b4[m], y, 0, 0, 0);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          ys[(16 * tt + 4 * lg + r) * kWyTP + rr] = (uint16_t)(BF16::pack(y[r], 0.0f) & 0xffffu);
+      }
+    }
+    // ---- D2: S <- e^{lam_C} S + (e^{lam_C - lam} * Delta)^T K, four 16 x 16 tiles per wave
+    {
+      wy_bf8 wh[2], wl[2];
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const int tb = 32 * ks + 8 * lg;
+        const wy_f4 d0 = wy_ld4(&sm.RD[16 * rt + l16][tb]), d1 = wy_ld4(&sm.RD[16 * rt + l16][tb + 4]);
+        const wy_f4 e0 = wy_ld4(&sm.eC[tb]), e1 = wy_ld4(&sm.eC[tb + 4]);
+        const float x[8] = {d0[0] * e0[0], d0[1] * e0[1], d0[2] * e0[2], d0[3] * e0[3],
+                            d1[0] * e1[0], d1[1] * e1[1], d1[2] * e1[2], d1[3] * e1[3]};
+        wy_split(x, wh[ks], wl[ks]);
+      }
+      const float dec = sm.eL[kWyC - 1];
+#pragma unroll
+      for (int dd = 0; dd < 4; ++dd) {
+        const int dt = (w >> 2) * 4 + dd;
+        wy_f4 acc;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[r] = dec * sm.S[16 * rt + 4 * lg + r][16 * dt + l16];
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          const wy_bf8 b = wy_ld8(&sm.KT[16 * dt + l16][32 * ks + 8 * lg]);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wh[ks], b, acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wl[ks], b, acc, 0, 0, 0);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sm.S[16 * rt + 4 * lg + r][16 * dt + l16] = acc[r];
+      }
+    }
+    __syncthreads();
+
+    // ---- D3: y rows of the live steps
+    {
+      const int s = tid >> 3, part = tid & 7;
+      if (s < n) {
+        const u32x4 o = *reinterpret_cast<const u32x4*>(&ys[s * kWyTP + 8 * part]);
+        *reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(g.y) +
+                                  ((bi * g.T + t0 + s) * g.Hv + hv) * g.Dv + dv0 + 8 * part) = o;
+      }
+    }
+  }
+
+  // the state rows back, in bf16 (every wave's last state update is behind the
+  // final barrier of the loop)
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int c = tid + 512 * h, row = c >> 4, part = c & 15;
+    const wy_f4 a0 = wy_ld4(&sm.S[row][8 * part]), a1 = wy_ld4(&sm.S[row][8 * part + 4]);
+    u32x4 o;
+    o[0] = BF16::pack(a0[0], a0[1]);
+    o[1] = BF16::pack(a0[2], a0[3]);
+    o[2] = BF16::pack(a1[0], a1[1]);
+    o[3] = BF16::pack(a1[2], a1[3]);
+    *reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(g.state_out) + (srow0 + row) * kWyDK + 8 * part) = o;
+  }
+}
+
 namespace {
 
 template <class X, bool NORM>
@@ -749,11 +1135,28 @@ bool launch_chunks(const GdnArgs& a, hipStream_t s) {
 // Steps per call up to which the barrier-free decode kernel runs.
 constexpr int64_t kDecodeMaxSteps = 2;
 
+// The WY kernel's shape: bf16 with the fused norm, Dk = 128, whole 64-row
+// state tiles, 16-byte rows of v and y, and sequences long enough to fill
+// its chunks.
+bool wy_fits(const GdnArgs& a) {
+  auto al = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
+  return a.Dk == kWyDK && a.Dv % kWyRows == 0 && a.T >= kWyMinSteps && al(a.v) && al(a.y) &&
+         al(a.qw) && al(a.kw);
+}
+
 template <class X, bool NORM>
 bool launch_x(const GdnArgs& a, hipStream_t s, bool aligned) {
   if (!aligned) return launch_rows<X, NORM>(a, s);
   if (a.T == 1) return launch_token<X, NORM>(a, s);
-  return a.T <= kDecodeMaxSteps ? launch_decode<X, NORM>(a, s) : launch_chunks<X, NORM>(a, s);
+  if (a.T <= kDecodeMaxSteps) return launch_decode<X, NORM>(a, s);
+  if constexpr (X::kCode == DT_BF16 && NORM) {
+    if (wy_fits(a)) {
+      const dim3 grid((unsigned)(a.Dv / kWyRows), (unsigned)a.Hv, (unsigned)a.B);
+      hipLaunchKernelGGL(gated_delta_wy_kernel, grid, dim3(512), 0, s, a);
+      return true;
+    }
+  }
+  return launch_chunks<X, NORM>(a, s);
 }
 
 }  // namespace

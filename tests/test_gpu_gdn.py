@@ -157,6 +157,37 @@ def test_prefill_head_dims_and_ragged_dv(dev, Dk, Dv):
     _check(s, rs, O.BF16, f"prefill state Dk={Dk} Dv={Dv}")
 
 
+@pytest.mark.parametrize("B,T,Hk,Hv,Dv,state", [(2, 200, 4, 8, 128, True), (1, 64, 2, 4, 64, False),
+                                               (1, 512, 16, 32, 128, True), (2, 130, 1, 2, 192, True)],
+                         ids=["ragged last chunk", "one chunk, zero state", "model heads T=512",
+                              "three row tiles"])
+def test_wy_chunked_prefill_bf16(dev, B, T, Hk, Hv, Dv, state):
+    """bf16 prefill with the fused q/k norm at Dk = 128, Dv a multiple of 64
+    and T >= 64 runs the chunked (WY) matrix-core form of the recurrence: a
+    ragged last chunk, exactly one chunk, the model's head counts and several
+    64-row state tiles, at the bf16 bar against the step-by-step oracle."""
+    shape = (B, T, Hk, 128, Hv, Dv)
+    inp = _inputs(2800 + T + Hv + Dv, *shape, O.BF16)
+    y, s = _run(dev, inp, O.BF16, norm=True, state=state)
+    ry, rs = _oracle(inp, O.BF16, norm=True, state=state)
+    _check(y, ry, O.BF16, f"wy y B={B} T={T} Hv={Hv} Dv={Dv}")
+    _check(s, rs, O.BF16, f"wy state B={B} T={T} Hv={Hv} Dv={Dv}")
+
+
+def test_wy_in_place_state(dev):
+    shape = (1, 96, 2, 128, 4, 128)
+    inp = _inputs(2851, *shape, O.BF16)
+    d = _dev(inp, O.BF16, dev)
+    wq, wk = H.gdn_qk_norm_weights(128, torch.bfloat16, dev)
+    st = d["state"]
+    y, s2 = H.gated_delta(d["q"], d["k"], d["v"], d["a_log"], d["a"], d["dt_bias"], d["b"], st,
+                          state_out=st, q_norm_w=wq, k_norm_w=wk)
+    assert s2.data_ptr() == st.data_ptr()
+    ry, rs = _oracle(inp, O.BF16, norm=True)
+    _check(to_host(y), ry, O.BF16, "wy in-place y")
+    _check(to_host(s2), rs, O.BF16, "wy in-place state")
+
+
 def test_zero_state_and_in_place_state(dev):
     shape = (2, 4, 2, 128, 4, 32)
     inp = _inputs(2731, *shape, O.BF16)
