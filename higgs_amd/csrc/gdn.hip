@@ -729,39 +729,82 @@ struct WyLds {
   float RD[kWyRows][kWyLP];  // R^T, overwritten block by block with Delta^T ([row][step])
   float Td[4][16][20];       // inverses of the 16 x 16 diagonal blocks of I + L
   uint16_t V[kWyC][kWyTP];
-  float lam[kWyC], beta[kWyC], eL[kWyC], eC[kWyC];
+  float lam2[kWyC], beta[kWyC], eL[kWyC], eC[kWyC];  // lam2 = lam * log2(e)
+  uint16_t wk[kWyDK], wq[kWyDK];                       // the norm weights
 };
 
-// One chunk's raw global loads of one thread.
-struct WyRaw {
-  u32x4 qk[4];  // 32 elements of a k row (threads 0..255) or a q row (256..511)
-  u32x4 v;      // 8 elements of a v row
-  uint32_t a, b;  // wave 0: step (lane)'s a and b
+// Raw global loads of one chunk. Waves 4..7 own the q/k rows: thread
+// u = tid - 256 holds 32 elements (part u & 3) of k row u >> 2 and of q row
+// u >> 2. Waves 0..3 own v: thread tid holds 16 elements (part tid & 3) of
+// v row tid >> 2; wave 0 also holds step (lane)'s a and b.
+struct WyRawQK {
+  u32x4 k[4], q[4];
+};
+struct WyRawV {
+  u32x4 v[2];
+  uint32_t a, b;
 };
 
-__device__ inline void wy_fetch(const GdnArgs& g, WyRaw& r, int64_t bi, int64_t hk, int64_t hv,
-                                int64_t dv0, int64_t t0, int tid, bool wave0) {
+__device__ inline void wy_fetch_qk(const GdnArgs& g, WyRawQK& r, int64_t bi, int64_t hk, int64_t t0,
+                                   int u) {
+  const int64_t last = g.T - 1;
+  const int row = u >> 2, part = u & 3;
+  const int64_t t = t0 + row < last ? t0 + row : last;
+  const int64_t e = ((bi * g.T + t) * g.Hk + hk) * kWyDK + 32 * part;
+  const u32x4* pk = reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(g.k) + e);
+  const u32x4* pq = reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(g.q) + e);
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    r.k[c] = pk[c];
+    r.q[c] = pq[c];
+  }
+}
+
+__device__ inline void wy_fetch_v(const GdnArgs& g, WyRawV& r, int64_t bi, int64_t hv, int64_t dv0,
+                                  int64_t t0, int tid, bool wave0) {
   const int64_t last = g.T - 1;
   {
-    const int row = tid >> 2, part = tid & 3;
-    const int64_t t = t0 + (row & 63) < last ? t0 + (row & 63) : last;
-    const void* src = row < 64 ? g.k : g.q;
-    const u32x4* p = reinterpret_cast<const u32x4*>(
-        reinterpret_cast<const uint16_t*>(src) + ((bi * g.T + t) * g.Hk + hk) * kWyDK + 32 * part);
-#pragma unroll
-    for (int c = 0; c < 4; ++c) r.qk[c] = p[c];
-  }
-  {
-    const int s = tid >> 3, part = tid & 7;
+    const int s = tid >> 2, part = tid & 3;
     const int64_t t = t0 + s < last ? t0 + s : last;
-    r.v = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(g.v) +
-                                          ((bi * g.T + t) * g.Hv + hv) * g.Dv + dv0 + 8 * part);
+    const u32x4* p = reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(g.v) +
+                                                    ((bi * g.T + t) * g.Hv + hv) * g.Dv + dv0 + 16 * part);
+    r.v[0] = p[0];
+    r.v[1] = p[1];
   }
   if (wave0) {
     const int lane = tid & 63;
     const int64_t t = t0 + lane < last ? t0 + lane : last;
     r.a = ldraw<BF16>(g.a, (bi * g.T + t) * g.Hv + hv);
     r.b = ldraw<BF16>(g.b, (bi * g.T + t) * g.Hv + hv);
+  }
+}
+
+// 32 elements (part u & 3) of one q or k row normalised as rms_norm(x, w, eps)
+// in bf16 (n = round(x * r), out = round(n * w), sum of squares in f64 over
+// the row's four lanes), packed; rows past the chunk's live steps are zero.
+__device__ inline void wy_norm(const u32x4 (&raw)[4], const uint16_t* w, float inv_dk, float eps,
+                               bool live, u32x4 (&out)[4]) {
+  float x[32];
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[8 * c + e] = elem<BF16>(raw[c], e);
+  double ss = 0.0;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) ss = __builtin_fma((double)x[i], (double)x[i], ss);
+  ss = group_sum<4>(ss);
+  const float rs = rms_scale(ss, inv_dk, eps);
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const u32x4 wr = *reinterpret_cast<const u32x4*>(w + 8 * c);
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      float a0 = x[8 * c + 2 * p] * rs, a1 = x[8 * c + 2 * p + 1] * rs;
+      round2<BF16>(a0, a1);
+      a0 = a0 * BF16::lo(wr[p]);
+      a1 = a1 * BF16::hi(wr[p]);
+      out[c][p] = live ? BF16::pack(a0, a1) : 0u;
+    }
   }
 }
 
@@ -795,8 +838,10 @@ __global__ __launch_bounds__(512) void gated_delta_wy_kernel(GdnArgs g) {
   const int64_t hk = (int)blockIdx.y / g.hgrp;
   const int64_t dv0 = (int64_t)blockIdx.x * kWyRows;
   const int64_t srow0 = (bi * g.Hv + hv) * g.Dv + dv0;
+  const bool qk_wave = w >= 4;
+  const int u = tid - 256, urow = u >> 2, upart = u & 3;  // q/k role (waves 4..7)
 
-  // the state rows, f32 in LDS
+  // the state rows (f32) and the norm weights into LDS
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const int c = tid + 512 * h, row = c >> 4, part = c & 15;
@@ -813,85 +858,81 @@ __global__ __launch_bounds__(512) void gated_delta_wy_kernel(GdnArgs g) {
     *reinterpret_cast<wy_f4*>(&sm.S[row][8 * part]) = wy_f4{x[0], x[1], x[2], x[3]};
     *reinterpret_cast<wy_f4*>(&sm.S[row][8 * part + 4]) = wy_f4{x[4], x[5], x[6], x[7]};
   }
-  // this thread's norm weights (k for rows 0..63, q for 64..127)
-  const int nrow = tid >> 2, npart = tid & 3;
-  const bool isk = nrow < 64;
-  u32x4 wraw[4];
-  {
-    const u32x4* p = reinterpret_cast<const u32x4*>(
-        reinterpret_cast<const uint16_t*>(isk ? g.kw : g.qw) + 32 * npart);
-#pragma unroll
-    for (int c = 0; c < 4; ++c) wraw[c] = p[c];
+  if (tid < 32) {
+    const int part = tid & 15;
+    const void* src = tid < 16 ? g.kw : g.qw;
+    const u32x4 wv = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(src) + 8 * part);
+    *reinterpret_cast<u32x4*>(tid < 16 ? &sm.wk[8 * part] : &sm.wq[8 * part]) = wv;
   }
   const float A = expf(load_param(g.a_log, g.pdt, hv));
   const float dtb = load_param(g.dt_bias, g.pdt, hv);
-
-  WyRaw raw;
-  wy_fetch(g, raw, bi, hk, hv, dv0, 0, tid, w == 0);
   const int64_t nch = (g.T + kWyC - 1) / kWyC;
-  const int rt = w & 3;                  // this wave's 16-row tile of the state rows
+  const int rt = w & 3;                              // this wave's 16-row tile of the state rows
   const int tA = w < 4 ? 0 : 1, tB = w < 4 ? 3 : 2;  // its two step tiles (balanced for M Delta)
+
+  // chunk 0's loads; waves 4..7 normalise its q and k rows
+  WyRawQK rqk;
+  WyRawV rv;
+  u32x4 nk[4], nq[4];
+  if (qk_wave) wy_fetch_qk(g, rqk, bi, hk, 0, u);
+  else wy_fetch_v(g, rv, bi, hv, dv0, 0, tid, w == 0);
+  __syncthreads();  // the norm weights
+  if (qk_wave) {
+    const bool live = urow < g.T;
+    wy_norm(rqk.k, &sm.wk[32 * upart], g.inv_dk, g.eps, live, nk);
+    wy_norm(rqk.q, &sm.wq[32 * upart], g.inv_dk, g.eps, live, nq);
+  }
 
   for (int64_t ch = 0; ch < nch; ++ch) {
     const int64_t t0 = ch * kWyC;
     const int n = (int)(g.T - t0 < kWyC ? g.T - t0 : kWyC);
 
-    // ---- A: normalised k / q rows (bf16) and k^T, v, gates into LDS
-    {
-      const int t = nrow & 63;
-      float x[32];
+    // ---- A: normalised k / q rows and k^T (waves 4..7), v and the gates (waves 0..3)
+    if (qk_wave) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        *reinterpret_cast<u32x4*>(&sm.Kh[urow][32 * upart + 8 * c]) = nk[c];
+        *reinterpret_cast<u32x4*>(&sm.Qh[urow][32 * upart + 8 * c]) = nq[c];
+      }
 #pragma unroll
       for (int c = 0; c < 4; ++c)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) x[8 * c + e] = elem<BF16>(raw.qk[c], e);
-      double ss = 0.0;
+        for (int p = 0; p < 4; ++p) {
+          sm.KT[32 * upart + 8 * c + 2 * p][urow] = (uint16_t)(nk[c][p] & 0xffffu);
+          sm.KT[32 * upart + 8 * c + 2 * p + 1][urow] = (uint16_t)(nk[c][p] >> 16);
+        }
+    } else {
+      const int s = tid >> 2, part = tid & 3;
+      const bool live = s < n;
+      *reinterpret_cast<u32x4*>(&sm.V[s][16 * part]) = live ? rv.v[0] : u32x4{0u, 0u, 0u, 0u};
+      *reinterpret_cast<u32x4*>(&sm.V[s][16 * part + 8]) = live ? rv.v[1] : u32x4{0u, 0u, 0u, 0u};
+      if (w == 0) {
+        const bool lv = lane < n;
+        const float x = BF16::lo(rv.a) + dtb;
+        const float sp = fmaxf(x, 0.0f) + log1pf(expf(-fabsf(x)));
+        float lg_ = lv ? -A * sp : 0.0f;
+        const float be = lv ? 1.0f / (1.0f + expf(-BF16::lo(rv.b))) : 0.0f;
 #pragma unroll
-      for (int i = 0; i < 32; ++i) ss = __builtin_fma((double)x[i], (double)x[i], ss);
-      ss = group_sum<4>(ss);
-      const float rs = rms_scale(ss, g.inv_dk, g.eps);
-      const bool live = t < n;
-#pragma unroll
-      for (int i = 0; i < 32; ++i)
-        x[i] = live ? BF16::round(BF16::round(x[i] * rs) * elem<BF16>(wraw[i >> 3], i & 7)) : 0.0f;
-      uint16_t* dst = isk ? &sm.Kh[t][32 * npart] : &sm.Qh[t][32 * npart];
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        u32x4 o;
-#pragma unroll
-        for (int p = 0; p < 4; ++p) o[p] = BF16::pack(x[8 * c + 2 * p], x[8 * c + 2 * p + 1]);
-        *reinterpret_cast<u32x4*>(dst + 8 * c) = o;
+        for (int o = 1; o < 64; o <<= 1) {
+          const float t = __shfl_up(lg_, o, 64);
+          if (lane >= o) lg_ += t;
+        }
+        const float lamC = __shfl(lg_, 63, 64);
+        sm.lam2[lane] = lg_ * 1.4426950408889634f;
+        sm.beta[lane] = be;
+        sm.eL[lane] = expf(lg_);
+        sm.eC[lane] = expf(lamC - lg_);
       }
-      if (isk) {
-#pragma unroll
-        for (int i = 0; i < 32; ++i) sm.KT[32 * npart + i][t] = (uint16_t)(f2u(x[i]) >> 16);
-      }
-    }
-    {
-      const int s = tid >> 3, part = tid & 7;
-      *reinterpret_cast<u32x4*>(&sm.V[s][8 * part]) = s < n ? raw.v : u32x4{0u, 0u, 0u, 0u};
-    }
-    if (w == 0) {
-      const bool live = lane < n;
-      const float x = BF16::lo(raw.a) + dtb;
-      const float sp = fmaxf(x, 0.0f) + log1pf(expf(-fabsf(x)));
-      float lg_ = live ? -A * sp : 0.0f;
-      const float be = live ? 1.0f / (1.0f + expf(-BF16::lo(raw.b))) : 0.0f;
-#pragma unroll
-      for (int o = 1; o < 64; o <<= 1) {
-        const float u = __shfl_up(lg_, o, 64);
-        if (lane >= o) lg_ += u;
-      }
-      const float lamC = __shfl(lg_, 63, 64);
-      sm.lam[lane] = lg_;
-      sm.beta[lane] = be;
-      sm.eL[lane] = expf(lg_);
-      sm.eC[lane] = expf(lamC - lg_);
     }
     __syncthreads();
 
     // the next chunk's loads fly during this chunk's products (the last chunk
     // reloads its own steps, clamped into range)
-    wy_fetch(g, raw, bi, hk, hv, dv0, ch + 1 < nch ? t0 + kWyC : t0, tid, w == 0);
+    {
+      const int64_t tn = ch + 1 < nch ? t0 + kWyC : t0;
+      if (qk_wave) wy_fetch_qk(g, rqk, bi, hk, tn, u);
+      else wy_fetch_v(g, rv, bi, hv, dv0, tn, tid, w == 0);
+    }
 
     // ---- B1: k.k and q.k tiles on or below the diagonal -> L, M
     for (int job = w; job < 20; job += 8) {
@@ -901,18 +942,25 @@ __global__ __launch_bounds__(512) void gated_delta_wy_kernel(GdnArgs g) {
       const int j = jj - i * (i + 1) / 2;
       const uint16_t* X = isq ? &sm.Qh[16 * i + l16][0] : &sm.Kh[16 * i + l16][0];
       const uint16_t* Kr = &sm.Kh[16 * j + l16][0];
-      wy_f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+      wy_f4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = acc0;
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wy_ld8(X + 32 * ks + 8 * lg),
-                                                      wy_ld8(Kr + 32 * ks + 8 * lg), acc, 0, 0, 0);
-      const int tj = 16 * j + l16;
+      for (int ks = 0; ks < 4; ks += 2) {
+        acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wy_ld8(X + 32 * ks + 8 * lg),
+                                                       wy_ld8(Kr + 32 * ks + 8 * lg), acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wy_ld8(X + 32 * ks + 32 + 8 * lg),
+                                                       wy_ld8(Kr + 32 * ks + 32 + 8 * lg), acc1, 0, 0, 0);
+      }
+      const int tj = 16 * j + l16, ti0 = 16 * i + 4 * lg;
+      const float lj = sm.lam2[tj];
+      const wy_f4 li = wy_ld4(&sm.lam2[ti0]);
+      const wy_f4 bi4 = wy_ld4(&sm.beta[ti0]);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int ti = 16 * i + 4 * lg + r;
-        const float dec = expf(sm.lam[ti] - sm.lam[tj]);
-        if (isq) sm.M[ti][tj] = tj <= ti ? dec * acc[r] : 0.0f;
-        else sm.L[ti][tj] = tj < ti ? sm.beta[ti] * dec * acc[r] : 0.0f;
+        const int ti = ti0 + r;
+        const float dec = __builtin_amdgcn_exp2f(li[r] - lj);
+        const float v = acc0[r] + acc1[r];
+        if (isq) sm.M[ti][tj] = tj <= ti ? dec * v : 0.0f;
+        else sm.L[ti][tj] = tj < ti ? bi4[r] * dec * v : 0.0f;
       }
     }
 
@@ -991,6 +1039,11 @@ __global__ __launch_bounds__(512) void gated_delta_wy_kernel(GdnArgs g) {
         dl[i] = d;
         *reinterpret_cast<wy_f4*>(&sm.RD[rr][16 * i + 4 * lg]) = d;
       }
+    } else if (ch + 1 < nch) {
+      // meanwhile waves 4..7 normalise the next chunk's q and k rows
+      const bool live = t0 + kWyC + urow < g.T;
+      wy_norm(rqk.k, &sm.wk[32 * upart], g.inv_dk, g.eps, live, nk);
+      wy_norm(rqk.q, &sm.wq[32 * upart], g.inv_dk, g.eps, live, nq);
     }
     __syncthreads();
 
