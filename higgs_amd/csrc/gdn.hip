@@ -733,50 +733,64 @@ struct WyLds {
   uint16_t wk[kWyDK], wq[kWyDK];                       // the norm weights
 };
 
-// Raw global loads of one chunk. Waves 4..7 own the q/k rows: thread
-// u = tid - 256 holds 32 elements (part u & 3) of k row u >> 2 and of q row
-// u >> 2. Waves 0..3 own v: thread tid holds 16 elements (part tid & 3) of
-// v row tid >> 2; wave 0 also holds step (lane)'s a and b.
-struct WyRawQK {
-  u32x4 k[4], q[4];
-};
-struct WyRawV {
+// Raw global loads of one chunk. Thread u of a wave group of four holds 32
+// elements (part u & 3) of row u >> 2: q rows in waves 0..3 (u = tid), k rows
+// in waves 4..7 (u = tid - 256), which also hold 16 elements (part u & 3) of
+// v row u >> 2; wave 4 holds step (lane)'s a and b.
+struct WyRaw {
+  u32x4 x[4];
   u32x4 v[2];
   uint32_t a, b;
 };
 
-__device__ inline void wy_fetch_qk(const GdnArgs& g, WyRawQK& r, int64_t bi, int64_t hk, int64_t t0,
-                                   int u) {
+__device__ inline void wy_fetch(const GdnArgs& g, WyRaw& r, int64_t bi, int64_t hk, int64_t hv,
+                                int64_t dv0, int64_t t0, int u, bool kwave, bool wave4) {
   const int64_t last = g.T - 1;
   const int row = u >> 2, part = u & 3;
   const int64_t t = t0 + row < last ? t0 + row : last;
-  const int64_t e = ((bi * g.T + t) * g.Hk + hk) * kWyDK + 32 * part;
-  const u32x4* pk = reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(g.k) + e);
-  const u32x4* pq = reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(g.q) + e);
+  const u32x4* px = reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(kwave ? g.k : g.q) +
+                                                   ((bi * g.T + t) * g.Hk + hk) * kWyDK + 32 * part);
 #pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    r.k[c] = pk[c];
-    r.q[c] = pq[c];
+  for (int c = 0; c < 4; ++c) r.x[c] = px[c];
+  if (kwave) {
+    const u32x4* pv = reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(g.v) +
+                                                     ((bi * g.T + t) * g.Hv + hv) * g.Dv + dv0 + 16 * part);
+    r.v[0] = pv[0];
+    r.v[1] = pv[1];
+  }
+  if (wave4) {
+    const int lane = u & 63;
+    const int64_t ts = t0 + lane < last ? t0 + lane : last;
+    r.a = ldraw<BF16>(g.a, (bi * g.T + ts) * g.Hv + hv);
+    r.b = ldraw<BF16>(g.b, (bi * g.T + ts) * g.Hv + hv);
   }
 }
 
-__device__ inline void wy_fetch_v(const GdnArgs& g, WyRawV& r, int64_t bi, int64_t hv, int64_t dv0,
-                                  int64_t t0, int tid, bool wave0) {
-  const int64_t last = g.T - 1;
-  {
-    const int s = tid >> 2, part = tid & 3;
-    const int64_t t = t0 + s < last ? t0 + s : last;
-    const u32x4* p = reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(g.v) +
-                                                    ((bi * g.T + t) * g.Hv + hv) * g.Dv + dv0 + 16 * part);
-    r.v[0] = p[0];
-    r.v[1] = p[1];
+// The gates of one chunk on one wave, lane = step: lam2 = lam * log2(e) with
+// lam the inclusive prefix sum of log g = -A * softplus(a + dt_bias) over the
+// chunk, beta = sigmoid(b), e^lam and e^{lam_C - lam}; steps at or past n
+// have log g = 0 and beta = 0.
+struct WyGates {
+  float lam2, beta, eL, eC;
+};
+
+__device__ inline WyGates wy_gates(const WyRaw& r, float A, float dtb, int lane, int n) {
+  const bool lv = lane < n;
+  const float x = BF16::lo(r.a) + dtb;
+  const float sp = fmaxf(x, 0.0f) + log1pf(expf(-fabsf(x)));
+  float lam = lv ? -A * sp : 0.0f;
+  WyGates o;
+  o.beta = lv ? 1.0f / (1.0f + expf(-BF16::lo(r.b))) : 0.0f;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const float t = __shfl_up(lam, d, 64);
+    if (lane >= d) lam += t;
   }
-  if (wave0) {
-    const int lane = tid & 63;
-    const int64_t t = t0 + lane < last ? t0 + lane : last;
-    r.a = ldraw<BF16>(g.a, (bi * g.T + t) * g.Hv + hv);
-    r.b = ldraw<BF16>(g.b, (bi * g.T + t) * g.Hv + hv);
-  }
+  const float lamC = __shfl(lam, 63, 64);
+  o.lam2 = lam * 1.4426950408889634f;
+  o.eL = expf(lam);
+  o.eC = expf(lamC - lam);
+  return o;
 }
 
 // 32 elements (part u & 3) of one q or k row normalised as rms_norm(x, w, eps)
@@ -838,8 +852,8 @@ __global__ __launch_bounds__(512) void gated_delta_wy_kernel(GdnArgs g) {
   const int64_t hk = (int)blockIdx.y / g.hgrp;
   const int64_t dv0 = (int64_t)blockIdx.x * kWyRows;
   const int64_t srow0 = (bi * g.Hv + hv) * g.Dv + dv0;
-  const bool qk_wave = w >= 4;
-  const int u = tid - 256, urow = u >> 2, upart = u & 3;  // q/k role (waves 4..7)
+  const bool kwave = w >= 4;                  // k rows, v and gates; else q rows
+  const int u = kwave ? tid - 256 : tid, urow = u >> 2, upart = u & 3;
 
   // the state rows (f32) and the norm weights into LDS
 #pragma unroll
@@ -869,86 +883,66 @@ __global__ __launch_bounds__(512) void gated_delta_wy_kernel(GdnArgs g) {
   const int64_t nch = (g.T + kWyC - 1) / kWyC;
   const int rt = w & 3;                              // this wave's 16-row tile of the state rows
   const int tA = w < 4 ? 0 : 1, tB = w < 4 ? 3 : 2;  // its two step tiles (balanced for M Delta)
+  const uint16_t* wrow = kwave ? &sm.wk[32 * upart] : &sm.wq[32 * upart];
 
-  // chunk 0's loads; waves 4..7 normalise its q and k rows
-  WyRawQK rqk;
-  WyRawV rv;
-  u32x4 nk[4], nq[4];
-  if (qk_wave) wy_fetch_qk(g, rqk, bi, hk, 0, u);
-  else wy_fetch_v(g, rv, bi, hv, dv0, 0, tid, w == 0);
+  // chunk 0: loads, normalised q / k rows, gates
+  WyRaw raw;
+  u32x4 nx[4];
+  WyGates gt{};
+  wy_fetch(g, raw, bi, hk, hv, dv0, 0, u, kwave, w == 4);
   __syncthreads();  // the norm weights
-  if (qk_wave) {
-    const bool live = urow < g.T;
-    wy_norm(rqk.k, &sm.wk[32 * upart], g.inv_dk, g.eps, live, nk);
-    wy_norm(rqk.q, &sm.wq[32 * upart], g.inv_dk, g.eps, live, nq);
-  }
+  wy_norm(raw.x, wrow, g.inv_dk, g.eps, urow < g.T, nx);
+  if (w == 4) gt = wy_gates(raw, A, dtb, lane, (int)(g.T < kWyC ? g.T : kWyC));
 
   for (int64_t ch = 0; ch < nch; ++ch) {
     const int64_t t0 = ch * kWyC;
     const int n = (int)(g.T - t0 < kWyC ? g.T - t0 : kWyC);
 
-    // ---- A: normalised k / q rows and k^T (waves 4..7), v and the gates (waves 0..3)
-    if (qk_wave) {
+    // ---- A: this chunk's normalised q / k rows, k^T, v and gates into LDS
+    {
+      uint16_t* dst = kwave ? &sm.Kh[urow][32 * upart] : &sm.Qh[urow][32 * upart];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        *reinterpret_cast<u32x4*>(&sm.Kh[urow][32 * upart + 8 * c]) = nk[c];
-        *reinterpret_cast<u32x4*>(&sm.Qh[urow][32 * upart + 8 * c]) = nq[c];
-      }
+      for (int c = 0; c < 4; ++c) *reinterpret_cast<u32x4*>(dst + 8 * c) = nx[c];
+    }
+    if (kwave) {
 #pragma unroll
       for (int c = 0; c < 4; ++c)
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
-          sm.KT[32 * upart + 8 * c + 2 * p][urow] = (uint16_t)(nk[c][p] & 0xffffu);
-          sm.KT[32 * upart + 8 * c + 2 * p + 1][urow] = (uint16_t)(nk[c][p] >> 16);
+          sm.KT[32 * upart + 8 * c + 2 * p][urow] = (uint16_t)(nx[c][p] & 0xffffu);
+          sm.KT[32 * upart + 8 * c + 2 * p + 1][urow] = (uint16_t)(nx[c][p] >> 16);
         }
-    } else {
-      const int s = tid >> 2, part = tid & 3;
-      const bool live = s < n;
-      *reinterpret_cast<u32x4*>(&sm.V[s][16 * part]) = live ? rv.v[0] : u32x4{0u, 0u, 0u, 0u};
-      *reinterpret_cast<u32x4*>(&sm.V[s][16 * part + 8]) = live ? rv.v[1] : u32x4{0u, 0u, 0u, 0u};
-      if (w == 0) {
-        const bool lv = lane < n;
-        const float x = BF16::lo(rv.a) + dtb;
-        const float sp = fmaxf(x, 0.0f) + log1pf(expf(-fabsf(x)));
-        float lg_ = lv ? -A * sp : 0.0f;
-        const float be = lv ? 1.0f / (1.0f + expf(-BF16::lo(rv.b))) : 0.0f;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-          const float t = __shfl_up(lg_, o, 64);
-          if (lane >= o) lg_ += t;
-        }
-        const float lamC = __shfl(lg_, 63, 64);
-        sm.lam2[lane] = lg_ * 1.4426950408889634f;
-        sm.beta[lane] = be;
-        sm.eL[lane] = expf(lg_);
-        sm.eC[lane] = expf(lamC - lg_);
+      const bool live = urow < n;
+      *reinterpret_cast<u32x4*>(&sm.V[urow][16 * upart]) = live ? raw.v[0] : u32x4{0u, 0u, 0u, 0u};
+      *reinterpret_cast<u32x4*>(&sm.V[urow][16 * upart + 8]) = live ? raw.v[1] : u32x4{0u, 0u, 0u, 0u};
+      if (w == 4) {
+        sm.lam2[lane] = gt.lam2;
+        sm.beta[lane] = gt.beta;
+        sm.eL[lane] = gt.eL;
+        sm.eC[lane] = gt.eC;
       }
     }
     __syncthreads();
 
     // the next chunk's loads fly during this chunk's products (the last chunk
     // reloads its own steps, clamped into range)
-    {
-      const int64_t tn = ch + 1 < nch ? t0 + kWyC : t0;
-      if (qk_wave) wy_fetch_qk(g, rqk, bi, hk, tn, u);
-      else wy_fetch_v(g, rv, bi, hv, dv0, tn, tid, w == 0);
-    }
+    const int64_t tn = ch + 1 < nch ? t0 + kWyC : t0;
+    wy_fetch(g, raw, bi, hk, hv, dv0, tn, u, kwave, w == 4);
 
-    // ---- B1: k.k and q.k tiles on or below the diagonal -> L, M
-    for (int job = w; job < 20; job += 8) {
-      const bool isq = job >= 10;
-      const int jj = isq ? job - 10 : job;
+    // ---- B1: tiles (i, j), j <= i, of k.k and q.k together (one k operand,
+    // one decay factor) -> L, M
+    for (int jj = w; jj < 10; jj += 8) {
       const int i = jj >= 6 ? 3 : jj >= 3 ? 2 : jj >= 1 ? 1 : 0;
       const int j = jj - i * (i + 1) / 2;
-      const uint16_t* X = isq ? &sm.Qh[16 * i + l16][0] : &sm.Kh[16 * i + l16][0];
-      const uint16_t* Kr = &sm.Kh[16 * j + l16][0];
-      wy_f4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = acc0;
+      const uint16_t* Ki = &sm.Kh[16 * i + l16][8 * lg];
+      const uint16_t* Qi = &sm.Qh[16 * i + l16][8 * lg];
+      const uint16_t* Kj = &sm.Kh[16 * j + l16][8 * lg];
+      wy_f4 gk = {0.0f, 0.0f, 0.0f, 0.0f}, gq = gk;
 #pragma unroll
-      for (int ks = 0; ks < 4; ks += 2) {
-        acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wy_ld8(X + 32 * ks + 8 * lg),
-                                                       wy_ld8(Kr + 32 * ks + 8 * lg), acc0, 0, 0, 0);
-        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wy_ld8(X + 32 * ks + 32 + 8 * lg),
-                                                       wy_ld8(Kr + 32 * ks + 32 + 8 * lg), acc1, 0, 0, 0);
+      for (int ks = 0; ks < 4; ++ks) {
+        const wy_bf8 bk = wy_ld8(Kj + 32 * ks);
+        gk = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wy_ld8(Ki + 32 * ks), bk, gk, 0, 0, 0);
+        gq = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wy_ld8(Qi + 32 * ks), bk, gq, 0, 0, 0);
       }
       const int tj = 16 * j + l16, ti0 = 16 * i + 4 * lg;
       const float lj = sm.lam2[tj];
@@ -958,9 +952,8 @@ __global__ __launch_bounds__(512) void gated_delta_wy_kernel(GdnArgs g) {
       for (int r = 0; r < 4; ++r) {
         const int ti = ti0 + r;
         const float dec = __builtin_amdgcn_exp2f(li[r] - lj);
-        const float v = acc0[r] + acc1[r];
-        if (isq) sm.M[ti][tj] = tj <= ti ? dec * v : 0.0f;
-        else sm.L[ti][tj] = tj < ti ? bi4[r] * dec * v : 0.0f;
+        sm.M[ti][tj] = tj <= ti ? dec * gq[r] : 0.0f;
+        sm.L[ti][tj] = tj < ti ? bi4[r] * dec * gk[r] : 0.0f;
       }
     }
 
@@ -1003,6 +996,13 @@ __global__ __launch_bounds__(512) void gated_delta_wy_kernel(GdnArgs g) {
     __syncthreads();
 
     // ---- C: Delta = (I + L)^{-1} R, waves 0..3, one 16-row tile of the state each
+    // the next chunk's q rows (waves 0..3, interleaved with their solve) and k
+    // rows and gates (waves 4..7); on the last chunk the results are unused
+    {
+      const int nn = (int)(g.T - tn < kWyC ? g.T - tn : kWyC);
+      wy_norm(raw.x, wrow, g.inv_dk, g.eps, urow < nn, nx);
+      if (w == 4) gt = wy_gates(raw, A, dtb, lane, nn);
+    }
     if (w < 4) {
       {
         // column l16 of the inverse of diagonal block lg, by forward substitution;
@@ -1039,11 +1039,6 @@ __global__ __launch_bounds__(512) void gated_delta_wy_kernel(GdnArgs g) {
         dl[i] = d;
         *reinterpret_cast<wy_f4*>(&sm.RD[rr][16 * i + 4 * lg]) = d;
       }
-    } else if (ch + 1 < nch) {
-      // meanwhile waves 4..7 normalise the next chunk's q and k rows
-      const bool live = t0 + kWyC + urow < g.T;
-      wy_norm(rqk.k, &sm.wk[32 * upart], g.inv_dk, g.eps, live, nk);
-      wy_norm(rqk.q, &sm.wq[32 * upart], g.inv_dk, g.eps, live, nq);
     }
     __syncthreads();
 
