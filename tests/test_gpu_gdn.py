@@ -174,6 +174,17 @@ def test_wy_chunked_prefill_bf16(dev, B, T, Hk, Hv, Dv, state):
     _check(s, rs, O.BF16, f"wy state B={B} T={T} Hv={Hv} Dv={Dv}")
 
 
+def test_wy_long_sequence_no_drift(dev):
+    """4096 steps (64 chunks) through the WY kernel: the f32 state carried in
+    LDS across chunks stays at the bf16 bar against the step-by-step oracle."""
+    shape = (1, 4096, 1, 128, 2, 128)
+    inp = _inputs(2861, *shape, O.BF16)
+    y, s = _run(dev, inp, O.BF16, norm=True)
+    ry, rs = _oracle(inp, O.BF16, norm=True)
+    _check(y, ry, O.BF16, "wy long y")
+    _check(s, rs, O.BF16, "wy long state")
+
+
 def test_wy_in_place_state(dev):
     shape = (1, 96, 2, 128, 4, 128)
     inp = _inputs(2851, *shape, O.BF16)
