@@ -18,10 +18,12 @@
 // sums whose order differs from the reference's, within the stated bars):
 //  * token (T = 1, the decode step): no LDS and no barrier. A 16-lane group
 //    owns 8 consecutive state rows (Dk/16 columns per lane), so each dot
-//    product reduces inside a DPP row. Every load is issued up front, the small
-//    ones (gates, q, k, v, norm weights) before the state rows, so the q/k norm
-//    and the gates run while the state is in flight; each row is then
-//    converted, advanced, packed and stored on its own.
+//    product reduces inside a DPP row. The small loads (gates, q, k, v, norm
+//    weights) go first, then the first 4 state rows, so the q/k norm and the
+//    gates run while the state is in flight; each row is then waited on
+//    alone, advanced, packed and stored, and the row 4 ahead is requested
+//    (the state goes through buffer descriptors, so no load or store is
+//    under a branch and the waits stay per row).
 //  * decode (T = 2): as token, with the state held in f32 across the steps.
 //  * chunk (T > 2): stages 16 steps at a time in LDS -- q and k normalised
 //    once per step, g and beta once per step, v for the block's 32 rows -- and
@@ -474,6 +476,9 @@ __global__ __launch_bounds__(256) void gated_delta_chunk_kernel(GdnArgs a) {
 #ifndef HGK_GDN_RPL
 #define HGK_GDN_RPL 8
 #endif
+#ifndef HGK_GDN_WIN
+#define HGK_GDN_WIN 4  // state rows in flight per lane group (8: all, 3-4% slower)
+#endif
 #ifndef HGK_GDN_WPB
 #define HGK_GDN_WPB 4
 #endif
@@ -591,6 +596,44 @@ __device__ inline void load_row_raw(const void* base, int64_t e, uint32_t* w) {
   }
 }
 
+// NW 32-bit words at byte offset `off` of a buffer: offsets at or past the
+// buffer's size read zeros (a zero-size buffer reads zeros everywhere) and
+// drop stores, so the state rows need no branch around their loads or stores.
+typedef uint32_t gd_u32x2 __attribute__((ext_vector_type(2)));
+
+template <int NW>
+__device__ inline void buf_load_words(__amdgpu_buffer_rsrc_t rs, uint32_t off, uint32_t (&w)[NW]) {
+  if constexpr (NW == 1) {
+    w[0] = __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0);
+  } else if constexpr (NW == 2) {
+    const gd_u32x2 v = __builtin_bit_cast(gd_u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 0));
+    w[0] = v[0];
+    w[1] = v[1];
+  } else {
+    static_assert(NW % 4 == 0, "whole 16-byte pieces");
+#pragma unroll
+    for (int c = 0; c < NW / 4; ++c) {
+      const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16 * c, 0, 0));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) w[4 * c + i] = v[i];
+    }
+  }
+}
+
+template <int NW>
+__device__ inline void buf_store_words(__amdgpu_buffer_rsrc_t rs, uint32_t off, const uint32_t (&w)[NW]) {
+  if constexpr (NW == 1) {
+    __builtin_amdgcn_raw_buffer_store_b32(w[0], rs, off, 0, 0);
+  } else if constexpr (NW == 2) {
+    __builtin_amdgcn_raw_buffer_store_b64(gd_u32x2{w[0], w[1]}, rs, off, 0, 0);
+  } else {
+#pragma unroll
+    for (int c = 0; c < NW / 4; ++c)
+      __builtin_amdgcn_raw_buffer_store_b128(u32x4{w[4 * c], w[4 * c + 1], w[4 * c + 2], w[4 * c + 3]},
+                                             rs, off + 16 * c, 0, 0);
+  }
+}
+
 template <class X, class P, int NPT, bool NORM, int RPL>
 __global__ __launch_bounds__(256) void gated_delta_token_kernel(GdnArgs a) {
   constexpr int DK = 16 * NPT;
@@ -618,14 +661,23 @@ __global__ __launch_bounds__(256) void gated_delta_token_kernel(GdnArgs a) {
   }
 #pragma unroll
   for (int r = 0; r < RPL; ++r) vraw[r] = ldraw<X>(a.v, row * a.Dv + (r0 + r < a.Dv ? r0 + r : a.Dv - 1));
-  uint32_t raw[RPL][NW];
-  if (a.state_in) {
+  // the state rows through buffer descriptors (the launcher keeps the state
+  // under 2^31 bytes): no state reads zeros, rows past Dv read zeros and
+  // their stores are dropped, so no load or store sits under a branch and
+  // each row is waited on alone, its store issued while later rows load
+  const int64_t sbytes = a.B * a.Hv * a.Dv * DK * X::kBytes;
+  const __amdgpu_buffer_rsrc_t sin = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<void*>(a.state_in), (short)0, a.state_in ? (int)sbytes : 0, 0x00020000);
+  const __amdgpu_buffer_rsrc_t sout = __builtin_amdgcn_make_buffer_rsrc(a.state_out, (short)0, (int)sbytes, 0x00020000);
+  uint32_t soff[RPL];
 #pragma unroll
-    for (int r = 0; r < RPL; ++r) {
-      const int64_t dv = r0 + r < a.Dv ? r0 + r : a.Dv - 1;
-      load_row_raw<X, NPT>(a.state_in, (sbase + dv) * DK + (int64_t)j * NPT, raw[r]);
-    }
-  }
+  for (int r = 0; r < RPL; ++r)
+    soff[r] = r0 + r < a.Dv ? (uint32_t)(((sbase + r0 + r) * DK + (int64_t)j * NPT) * X::kBytes) : 0x80000000u;
+  uint32_t raw[RPL][NW];
+#pragma unroll
+  for (int r = 0; r < RPL; ++r)
+    if (r < HGK_GDN_WIN) buf_load_words<NW>(sin, soff[r], raw[r]);
+  __builtin_amdgcn_sched_barrier(0);  // every load above is issued before the first wait below
 
   const float g = gdn_gate(cvt<X>(araw), cvt<P>(dtb_raw), expf(cvt<P>(alog_raw)));
   const float beta = gdn_beta(cvt<X>(braw));
@@ -653,13 +705,8 @@ __global__ __launch_bounds__(256) void gated_delta_token_kernel(GdnArgs a) {
 #pragma unroll
   for (int r = 0; r < RPL; ++r) {
     float st[NPT];
-    if (a.state_in) {
 #pragma unroll
-      for (int i = 0; i < NPT; ++i) st[i] = elem<X>(raw[r], i);
-    } else {
-#pragma unroll
-      for (int i = 0; i < NPT; ++i) st[i] = 0.0f;
-    }
+    for (int i = 0; i < NPT; ++i) st[i] = elem<X>(raw[r], i);
     float kv = 0.0f;
 #pragma unroll
     for (int i = 0; i < NPT; ++i) {
@@ -675,7 +722,17 @@ __global__ __launch_bounds__(256) void gated_delta_token_kernel(GdnArgs a) {
       o = __builtin_fmaf(st[i], q[i], o);
     }
     out[r] = sum16(o);
-    if (r0 + r < a.Dv) store_row_part<X, NPT>(a.state_out, (sbase + r0 + r) * DK + (int64_t)j * NPT, st);
+    uint32_t w[NW];
+    if constexpr (X::kBytes == 2) {
+#pragma unroll
+      for (int i = 0; i < NW; ++i) w[i] = X::pack(st[2 * i], st[2 * i + 1]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < NW; ++i) w[i] = f2u(st[i]);
+    }
+    buf_store_words<NW>(sout, soff[r], w);
+    if (r + HGK_GDN_WIN < RPL) buf_load_words<NW>(sin, soff[r + HGK_GDN_WIN], raw[r + HGK_GDN_WIN]);
+    __builtin_amdgcn_sched_barrier(0);
   }
   if (j == 0) {
 #pragma unroll
@@ -1151,6 +1208,8 @@ bool launch_token_p(const GdnArgs& a, hipStream_t s) {
 // decode kernel, which reads them in any float dtype)
 template <class X, bool NORM>
 bool launch_token(const GdnArgs& a, hipStream_t s) {
+  // the token kernel addresses the state with 32-bit buffer offsets
+  if (a.B * a.Hv * a.Dv * a.Dk * X::kBytes >= ((int64_t)1 << 31)) return launch_decode<X, NORM>(a, s);
   if (a.pdt == DT_F32) return launch_token_p<X, F32, NORM>(a, s);
   if (a.pdt == X::kCode) return launch_token_p<X, X, NORM>(a, s);
   return launch_decode<X, NORM>(a, s);
