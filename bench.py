@@ -8,7 +8,7 @@ one batch of synthetic inputs already resident in HBM. The metric is achieved
 HBM bandwidth: algorithmic bytes (every input element read once, every output
 written once, weights/tables once; the gather gets no reuse credit) per second.
 
-    python bench.py [--steps K] [--warmup W] [--config NAME] [--table] [--no-cpu]
+    python bench.py [--steps K] [--warmup W] [--settle S] [--config NAME] [--table] [--no-cpu]
 
 Prints ONE JSON line. --table additionally measures every workload and writes
 gpurun_out/bench_table.json. Input/output buffer sets rotate so the bytes
@@ -691,7 +691,21 @@ def kernel_times(cx, wl, graph, per_group=20, groups=5):
     return per
 
 
-def measure(cx, wl, steps, warmup):
+def settle(cx, fn, seconds):
+    """Untimed whole steps until `seconds` of wall time have passed. The GPU's
+    clocks ramp up over its first ~10-20 ms of work (a 36 us kernel reads
+    38-39 us in its first ~10 ms on MI355X), which a warm-up counted in steps
+    of a sub-millisecond workload would leave inside the timed region."""
+    torch = cx.torch
+    t0, i = time.perf_counter(), 0
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(8):
+            fn(i)
+            i += 1
+        torch.cuda.synchronize()
+
+
+def measure(cx, wl, steps, warmup, settle_s=0.25):
     torch = cx.torch
     he = HipEvents()
     rec = he.h.hipEventRecord
@@ -702,6 +716,7 @@ def measure(cx, wl, steps, warmup):
         graphs = [_capture(cx, [_launcher(k, (si + r) % wl.nsets)
                                 for r in range(reps) for k in wl.kernels])
                   for si in range(wl.nsets)]
+        settle(cx, lambda i: graphs[i % wl.nsets].replay(), settle_s)
         for i in range(warmup):
             graphs[i % wl.nsets].replay()
         torch.cuda.synchronize()
@@ -718,6 +733,7 @@ def measure(cx, wl, steps, warmup):
         del graphs
         return {"ms_per_step": ms, "wall_ms_per_step": wall * 1e3 / (steps * reps),
                 "steps_per_graph": reps, "kernels": kernel_times(cx, wl, graph=True)}
+    settle(cx, wl.step, settle_s)
     for i in range(warmup):
         wl.step(i)
     torch.cuda.synchronize()
@@ -927,9 +943,9 @@ def traffic_for(kernel_name, workload):
         return None
 
 
-def run_one(cx, name, steps, warmup):
+def run_one(cx, name, steps, warmup, settle_s=0.25):
     wl = WORKLOADS[name](cx)
-    r = measure(cx, wl, steps, warmup)
+    r = measure(cx, wl, steps, warmup, settle_s)
     r["workload"] = wl
     return r
 
@@ -939,6 +955,8 @@ def main(argv=None):
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--settle", type=float, default=0.25,
+                    help="seconds of untimed steps before the warm-up, so the clocks are steady")
     ap.add_argument("--config", default="llama32_1b_chain", choices=sorted(WORKLOADS))
     ap.add_argument("--table", action="store_true", help="also measure every workload")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -966,7 +984,7 @@ def main(argv=None):
         torch.cuda.synchronize()
         del src, dst
     torch.cuda.synchronize()
-    res = run_one(cx, args.config, args.steps, args.warmup)
+    res = run_one(cx, args.config, args.steps, args.warmup, args.settle)
     wl = res["workload"]
     ms = res["ms_per_step"]
     gbs = wl.bytes / (ms * 1e-3) / 1e9
@@ -1002,7 +1020,7 @@ def main(argv=None):
             r = line if name == args.config else None
             if r is None:
                 torch.cuda.empty_cache()
-                rr = run_one(cx, name, max(10, args.steps // 2), args.warmup)
+                rr = run_one(cx, name, max(10, args.steps // 2), args.warmup, args.settle)
                 w2 = rr["workload"]
                 r = {"workload": name, "ms_per_step": rr["ms_per_step"], "bytes": w2.bytes,
                      "gbs": w2.bytes / (rr["ms_per_step"] * 1e-3) / 1e9,
