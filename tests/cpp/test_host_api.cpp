@@ -602,7 +602,7 @@ TEST(test_qlinear_forward_matches_oracle) {
 // y = 32 / 2 = 16 exactly; a second step from that state equals the oracle's,
 // and one two-step call equals two one-step calls (sequential dependence).
 // Then Qwen3-Next's decode shape in bf16 with the fused q/k norm against the
-// oracle (1 ulp, atol 1e-3).
+// oracle (1 ulp, atol 1e-3), and a 96-step prefill (>= 99% bit-identical).
 TEST(test_gated_delta_reference_cases_and_decode) {
   const int64_t B = 1, Hk = 2, Dk = 32, Hv = 4, Dv = 32;
   auto ones = [](int64_t n) { return std::vector<float>(n, 1.0f); };
@@ -667,6 +667,34 @@ TEST(test_gated_delta_reference_cases_and_decode) {
     or_convert_to_f32(OR_BF16, want.data(), wf.data(), static_cast<int64_t>(want.size()));
     for (size_t i = 0; i < got.size(); ++i)
       ASSERT(ulp16(got[i], want[i]) <= 1 || std::fabs(gf[i] - wf[i]) <= 1e-3f, "%s[%zu] %g vs %g", what, i, gf[i], wf[i]);
+  }
+  // a 96-step bf16 prefill with the fused norm (the chunked matrix-core form,
+  // a ragged last chunk), through the same call
+  const int64_t Tp = 96, Hkp = 2, Hvp = 4, Dvp = 64;
+  auto pq = bits_of(uniform(9510, Tp * Hkp * Dkd, -1, 1), OR_BF16), pk = bits_of(uniform(9511, Tp * Hkp * Dkd, -1, 1), OR_BF16);
+  auto pv = bits_of(uniform(9512, Tp * Hvp * Dvp, -1, 1), OR_BF16);
+  auto pa = bits_of(uniform(9513, Tp * Hvp, -1, 1), OR_BF16), pb = bits_of(uniform(9514, Tp * Hvp, -1, 1), OR_BF16);
+  auto ps = bits_of(uniform(9515, Hvp * Dvp * Dkd, -0.1f, 0.1f), OR_BF16);
+  auto palog = uniform(9516, Hvp, -1, 0), pdtb = uniform(9517, Hvp, -0.5f, 0.5f);
+  Array pst = dev16(ps, {1, Hvp, Dvp, Dkd}, Dtype::Bfloat16);
+  auto [py, pso] = higgs::gated_delta(dev16(pq, {1, Tp, Hkp, Dkd}, Dtype::Bfloat16), dev16(pk, {1, Tp, Hkp, Dkd}, Dtype::Bfloat16),
+                                      dev16(pv, {1, Tp, Hvp, Dvp}, Dtype::Bfloat16), f32(palog, {Hvp}),
+                                      dev16(pa, {1, Tp, Hvp}, Dtype::Bfloat16), f32(pdtb, {Hvp}),
+                                      dev16(pb, {1, Tp, Hvp}, Dtype::Bfloat16), &pst, &wq, &wk);
+  std::vector<uint16_t> opy(Tp * Hvp * Dvp), ops(ps.size());
+  ASSERT(or_gated_delta(OR_BF16, pq.data(), pk.data(), pv.data(), palog.data(), pa.data(), pdtb.data(), pb.data(), OR_F32,
+                        ps.data(), wqb.data(), wkb.data(), 1e-6f, 1, Tp, Hkp, Dkd, Hvp, Dvp, opy.data(), ops.data()) == 0,
+         "oracle prefill");
+  for (auto [got, want, what] : {std::tuple{py.to_bits(), opy, "prefill y"}, std::tuple{pso.to_bits(), ops, "prefill state"}}) {
+    std::vector<float> gf(got.size()), wf(want.size());
+    or_convert_to_f32(OR_BF16, got.data(), gf.data(), static_cast<int64_t>(got.size()));
+    or_convert_to_f32(OR_BF16, want.data(), wf.data(), static_cast<int64_t>(want.size()));
+    size_t same = 0;
+    for (size_t i = 0; i < got.size(); ++i) {
+      same += got[i] == want[i];
+      ASSERT(ulp16(got[i], want[i]) <= 1 || std::fabs(gf[i] - wf[i]) <= 1e-3f, "%s[%zu] %g vs %g", what, i, gf[i], wf[i]);
+    }
+    ASSERT(same >= got.size() * 99 / 100, "%s: %zu of %zu bit-identical", what, same, got.size());
   }
 }
 
