@@ -14,8 +14,9 @@
 // (1/Dk for q, 1/sqrt(Dk) for k, in the activation dtype; 1172-1173) when the
 // caller passes those weights.
 //
-// Kernels (all with the same per-row arithmetic; the dot products are f32
-// sums whose order differs from the reference's, within the stated bars):
+// Kernels (the step kernels share the per-row arithmetic; their dot products
+// are f32 sums whose order differs from the reference's, within the stated
+// bars):
 //  * token (T = 1, the decode step): no LDS and no barrier. A 16-lane group
 //    owns 8 consecutive state rows (Dk/16 columns per lane), so each dot
 //    product reduces inside a DPP row. The small loads (gates, q, k, v, norm
@@ -24,13 +25,16 @@
 //    alone, advanced, packed and stored, and the row 4 ahead is requested
 //    (the state goes through buffer descriptors, so no load or store is
 //    under a branch and the waits stay per row).
-//  * decode (T = 2): as token, with the state held in f32 across the steps.
+//  * decode (T = 2): the token kernel's layout (all loads up front, plain
+//    global addressing), with the state held in f32 across the steps.
 //  * chunk (T > 2): stages 16 steps at a time in LDS -- q and k normalised
 //    once per step, g and beta once per step, v for the block's 32 rows -- and
 //    every lane carries two state rows whose chains interleave; the next
 //    chunk's global loads are issued before the current chunk's recurrence,
 //    and y is staged in LDS and stored per step as one run of 32 rows.
 //  * row (any alignment): 32 lanes per row, step t+1 loaded during step t.
+//  * WY (bf16 prefill with the fused norm, Dk = 128, Dv a multiple of 64,
+//    T >= 64): the chunked matrix form on MFMA, below.
 #include <cmath>
 
 #include "../../include/higgs_hip.h"
@@ -762,8 +766,9 @@ __global__ __launch_bounds__(256) void gated_delta_token_kernel(GdnArgs a) {
 // (I + L) inverted by forward substitution, the rest by blocked substitution.
 // A block owns (b, v-head, 64 state rows), 8 waves, the state in LDS for the
 // whole sequence; the next chunk's q, k, v, a, b are loaded during the current
-// chunk's products. Steps past T in the last chunk are zero rows (k = q = v =
-// beta = 0, log g = 0), which leave S unchanged.
+// chunk's products, and its q/k rows are normalised (and its gates computed)
+// while waves 0..3 run the triangular solve. Steps past T in the last chunk
+// are zero rows (k = q = v = beta = 0, log g = 0), which leave S unchanged.
 typedef __bf16 wy_bf8 __attribute__((ext_vector_type(8)));
 typedef float wy_f4 __attribute__((ext_vector_type(4)));
 
