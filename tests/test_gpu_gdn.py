@@ -91,6 +91,19 @@ def test_qwen3_next_decode_bf16_with_norm(dev):
     _check(s, rs, O.BF16, "decode state")
 
 
+@pytest.mark.parametrize("Dk,Dv,state", [(64, 36, True), (256, 200, True), (128, 128, False)],
+                         ids=["Dk64 Dv36", "Dk256 Dv200", "no state"])
+def test_decode_step_ragged_rows_and_no_state(dev, Dk, Dv, state):
+    """The one-token kernel addresses the state through buffer ranges: rows
+    past Dv in a block's last tile read zeros and drop their stores, and no
+    state reads zeros; both at the bf16 bar."""
+    inp = _inputs(2711 + Dk + Dv, 3, 1, 2, Dk, 4, Dv, O.BF16)
+    y, s = _run(dev, inp, O.BF16, norm=True, state=state)
+    ry, rs = _oracle(inp, O.BF16, norm=True, state=state)
+    _check(y, ry, O.BF16, f"decode y Dk={Dk} Dv={Dv}")
+    _check(s, rs, O.BF16, f"decode state Dk={Dk} Dv={Dv}")
+
+
 def test_two_token_decode_bf16_with_norm(dev):
     """Two tokens per call (a speculative-decode shape) on the decode kernel,
     model dims, ragged Dv."""
