@@ -603,21 +603,24 @@ __device__ inline void load_row_raw(const void* base, int64_t e, uint32_t* w) {
 // NW 32-bit words at byte offset `off` of a buffer: offsets at or past the
 // buffer's size read zeros (a zero-size buffer reads zeros everywhere) and
 // drop stores, so the state rows need no branch around their loads or stores.
+// The state is read once and written once per call: both go with the
+// non-temporal cache policy (bit 1 of the buffer instructions' policy operand).
 typedef uint32_t gd_u32x2 __attribute__((ext_vector_type(2)));
+constexpr int kNt = 2;
 
 template <int NW>
 __device__ inline void buf_load_words(__amdgpu_buffer_rsrc_t rs, uint32_t off, uint32_t (&w)[NW]) {
   if constexpr (NW == 1) {
-    w[0] = __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0);
+    w[0] = __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, kNt);
   } else if constexpr (NW == 2) {
-    const gd_u32x2 v = __builtin_bit_cast(gd_u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 0));
+    const gd_u32x2 v = __builtin_bit_cast(gd_u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, kNt));
     w[0] = v[0];
     w[1] = v[1];
   } else {
     static_assert(NW % 4 == 0, "whole 16-byte pieces");
 #pragma unroll
     for (int c = 0; c < NW / 4; ++c) {
-      const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16 * c, 0, 0));
+      const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16 * c, 0, kNt));
 #pragma unroll
       for (int i = 0; i < 4; ++i) w[4 * c + i] = v[i];
     }
@@ -627,14 +630,14 @@ __device__ inline void buf_load_words(__amdgpu_buffer_rsrc_t rs, uint32_t off, u
 template <int NW>
 __device__ inline void buf_store_words(__amdgpu_buffer_rsrc_t rs, uint32_t off, const uint32_t (&w)[NW]) {
   if constexpr (NW == 1) {
-    __builtin_amdgcn_raw_buffer_store_b32(w[0], rs, off, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b32(w[0], rs, off, 0, kNt);
   } else if constexpr (NW == 2) {
-    __builtin_amdgcn_raw_buffer_store_b64(gd_u32x2{w[0], w[1]}, rs, off, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b64(gd_u32x2{w[0], w[1]}, rs, off, 0, kNt);
   } else {
 #pragma unroll
     for (int c = 0; c < NW / 4; ++c)
       __builtin_amdgcn_raw_buffer_store_b128(u32x4{w[4 * c], w[4 * c + 1], w[4 * c + 2], w[4 * c + 3]},
-                                             rs, off + 16 * c, 0, 0);
+                                             rs, off + 16 * c, 0, kNt);
   }
 }
 

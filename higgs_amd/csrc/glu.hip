@@ -23,6 +23,8 @@
 // which promote a bf16 input): 0.5*g*(1+tanh(k0*(g + k1*g^3))) is evaluated as
 // the identical g / (1 + exp(-2*k0*(g + k1*g^3))), using the hardware exp2 and
 // reciprocal (relative error ~1e-6), and the product with up is rounded once.
+#include <algorithm>
+
 #include "../../include/higgs_hip.h"
 #include "hgk_common.h"
 #include "hgk_host.h"
@@ -103,10 +105,12 @@ __device__ inline float glu1(float g, float u) {
       return X::round(s * u);
     }
   } else {
-    const float k0 = 0.7978845608028654f, k1 = 0.044715f;
-    const float g3 = g * g * g;
-    const float inner = k0 * (g + k1 * g3);
-    const float e = __builtin_amdgcn_exp2f(inner * -2.8853900817779268f);  // exp(-2*inner)
+    // exp(-2*k0*(g + k1*g^3)) = exp2(g * (c1 + c2*g^2)) with k0 = sqrt(2/pi),
+    // k1 = 0.044715, c1 = -2*k0*log2(e), c2 = c1*k1: three VALU operations
+    // before the exp2 instead of six
+    const float c1 = -2.302208198144325f, c2 = -0.1029432395800235f;
+    const float z = g * __builtin_fmaf(g * g, c2, c1);
+    const float e = __builtin_amdgcn_exp2f(z);
     const float gl = g * __builtin_amdgcn_rcpf(1.0f + e);
     return gl * u;
   }
@@ -141,8 +145,8 @@ __global__ __launch_bounds__(256) void glu_kernel(GluArgs a) {
     const uint32_t qq = q < a.total ? q : a.total - 1;
     int64_t go, uo;
     glu_offsets<V, CONTIG>(a, qq, go, uo, oo[k]);
-    gr[k] = ld16<X>(a.g, go);
-    ur[k] = ld16<X>(a.u, uo);
+    gr[k] = ld16_nt<X>(a.g, go);
+    ur[k] = ld16_nt<X>(a.u, uo);
   }
   if constexpr (ACT == HGK_ACT_SILU && X::kBytes == 2) {
     float gv[U * V], uv[U * V], o[U * V];
@@ -168,20 +172,84 @@ __global__ __launch_bounds__(256) void glu_kernel(GluArgs a) {
   }
 }
 
-// Any alignment / width: one element per thread.
+// 16-bit inputs with an f32 output (GeGLU's promoted result): a unit is 4
+// elements, read as 8 bytes of gate and of up and written as 16 bytes, so
+// every load instruction of a wave covers 512 contiguous bytes and every store
+// 1 KB. (With 16-byte input chunks each lane would write 32 bytes in two
+// instructions, each covering every other 16 bytes of a 2 KB span.)
+template <class X, class Y, int ACT, int U, bool CONTIG>
+__global__ __launch_bounds__(256) void glu_wide_kernel(GluArgs a) {
+  static_assert(X::kBytes == 2 && Y::kBytes == 4, "16-bit in, f32 out");
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+  constexpr int V = 4;
+  const uint32_t base = blockIdx.x * (256u * U) + threadIdx.x;
+  u32x2 gr[U], ur[U];
+  int64_t oo[U];
+#pragma unroll
+  for (int k = 0; k < U; ++k) {
+    const uint32_t q = base + 256u * k;
+    const uint32_t qq = q < a.total ? q : a.total - 1;
+    int64_t go, uo;
+    glu_offsets<V, CONTIG>(a, qq, go, uo, oo[k]);
+    gr[k] = ld_raw_nt<8>(a.g, go * 2);
+    ur[k] = ld_raw_nt<8>(a.u, uo * 2);
+  }
+  float gv[U * V], uv[U * V], o[U * V];
+#pragma unroll
+  for (int k = 0; k < U; ++k)
+#pragma unroll
+    for (int e = 0; e < V; e += 2) {
+      gv[k * V + e] = X::lo(gr[k][e / 2]);
+      gv[k * V + e + 1] = X::hi(gr[k][e / 2]);
+      uv[k * V + e] = X::lo(ur[k][e / 2]);
+      uv[k * V + e + 1] = X::hi(ur[k][e / 2]);
+    }
+  if constexpr (ACT == HGK_ACT_SILU) {
+    swiglu16<X, U * V>(gv, uv, o);
+  } else {
+#pragma unroll
+    for (int e = 0; e < U * V; ++e) o[e] = glu1<X, ACT>(gv[e], uv[e]);
+  }
+#pragma unroll
+  for (int k = 0; k < U; ++k)
+    if (base + 256u * k < a.total) store_elems<Y, V>(a.o, oo[k], o + k * V);
+}
+
+// Any alignment / width: one element per thread per pass of a grid-stride
+// loop (the grid is capped, so any element count launches).
 template <class X, class Y, int ACT>
 __global__ __launch_bounds__(256) void glu_generic_kernel(GluArgs a, int64_t n, int64_t rows) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= n * rows) return;
-  const int64_t row = i / n, c = i - row * n;
-  const float g = load1<X>(a.g, row * a.gs + c), u = load1<X>(a.u, row * a.us + c);
-  store1<Y>(a.o, row * a.os + c, glu1<X, ACT>(g, u));
+  const int64_t total = n * rows;
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += stride) {
+    const int64_t row = i / n, c = i - row * n;
+    const float g = load1<X>(a.g, row * a.gs + c), u = load1<X>(a.u, row * a.us + c);
+    store1<Y>(a.o, row * a.os + c, glu1<X, ACT>(g, u));
+  }
 }
 
 namespace {
 
 template <class X, class Y, int ACT>
-void launch(const GluArgs& a, bool vec_ok, int64_t rows, int64_t n, hipStream_t s) {
+void launch(const GluArgs& a0, bool vec_ok, int64_t rows, int64_t n, hipStream_t s) {
+  if constexpr (X::kBytes == 2 && Y::kBytes == 4) {
+    if (vec_ok && n % 4 == 0 && rows * (n / 4) < ((int64_t)1 << 31)) {
+      GluArgs a = a0;  // units of 4 elements
+      a.cpr = (uint32_t)(n / 4);
+      a.total = (uint32_t)(rows * (n / 4));
+      if (a.total >= 256u * 4u * 1024u) {
+        const unsigned blocks = (a.total + 1024u - 1u) / 1024u;
+        if (a.contig) hipLaunchKernelGGL((glu_wide_kernel<X, Y, ACT, 4, true>), dim3(blocks), dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((glu_wide_kernel<X, Y, ACT, 4, false>), dim3(blocks), dim3(256), 0, s, a);
+      } else {
+        const unsigned blocks = (a.total + 511u) / 512u;
+        if (a.contig) hipLaunchKernelGGL((glu_wide_kernel<X, Y, ACT, 2, true>), dim3(blocks), dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((glu_wide_kernel<X, Y, ACT, 2, false>), dim3(blocks), dim3(256), 0, s, a);
+      }
+      return;
+    }
+  }
+  const GluArgs& a = a0;
   if (vec_ok) {
     if (a.total >= 256u * 4u * 1024u) {
       const unsigned blocks = (a.total + 1024u - 1u) / 1024u;
@@ -194,7 +262,7 @@ void launch(const GluArgs& a, bool vec_ok, int64_t rows, int64_t n, hipStream_t 
     }
     return;
   }
-  const int64_t blocks = (n * rows + 255) / 256;
+  const int64_t blocks = std::min<int64_t>((n * rows + 255) / 256, (int64_t)1 << 20);
   hipLaunchKernelGGL((glu_generic_kernel<X, Y, ACT>), dim3((unsigned)blocks), dim3(256), 0, s,
                      a, n, rows);
 }

@@ -3,8 +3,10 @@
 //
 // Layout: rows of n contiguous elements, arbitrary row stride. A group of LPR
 // lanes owns one row (LPR = 64 for hidden-size rows, fewer for head_dim rows,
-// so a wave64 covers 64/LPR rows); each lane holds CPL 16-byte chunks of its
-// row in registers, strided by LPR so the wave's loads are fully coalesced.
+// so a wave64 covers 64/LPR rows); each lane holds CPL units of its row in
+// registers, strided by LPR so the wave's loads are fully coalesced. A unit is
+// 16 bytes of x, or 8 bytes when the output is wider than x (f32 out of a
+// 16-bit x), so that each unit's output is exactly one 16-byte store.
 // The f32 sum of squares is reduced across the group with xor shuffles, then
 // the same registers are scaled and written: x crosses HBM once, y once.
 //
@@ -49,48 +51,59 @@ __device__ inline int64_t z_row_offset(const NormArgs& a, int64_t r) {
   return g * a.zgs + (r - g * a.zg) * a.zs;
 }
 
-// X activation, Y output, W weight storage type (X's type or f32). Every load
-// of the row (x, weights, z) is issued before the reduction; all stay packed
-// in registers until the element is consumed.
-template <class X, class Y, class W, int LPR, int CPL, int MODE>
+// X activation, Y output, W weight storage type (X's type or f32). A lane's
+// unit is UB bytes of x (16, or 8 when Y is wider than X, so that a unit's
+// output is one 16-byte store and every store instruction of the wave covers
+// a contiguous span). Every load of the row (x, weights, z) is issued before
+// the reduction; all stay packed in registers until the element is consumed.
+template <class X, class Y, class W, int LPR, int CPL, int MODE, int UB>
 __global__ __launch_bounds__(256) void rms_norm_kernel(NormArgs a) {
   constexpr bool GATED = MODE == kGated, RESID = MODE == kResid, TWO = GATED || RESID;
-  constexpr int V = Vec<X>::N;
+  constexpr int UE = UB / X::kBytes;     // elements per unit
+  constexpr int UW = UB / 4;             // 32-bit words of x per unit
+  constexpr int WW = UE * W::kBytes / 4;  // 32-bit words of weights per unit
+  typedef typename RawVec<UB>::type XR;
   constexpr int RPW = 64 / LPR;
-  constexpr int WW = V * W::kBytes / 4;  // 32-bit words of weights per chunk
   const int lane = threadIdx.x & 63;
   const int64_t wave = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   const int64_t row = wave * RPW + lane / LPR;
   const int j = lane % LPR;
   const bool live = row < a.rows;
   const int64_t r = live ? row : a.rows - 1;
-  const int nchunks = a.n / V;
+  const int nchunks = a.n / UE;
   const bool has_w = a.w != nullptr;
 
-  // Loads are unconditional: chunk indices past the row are clamped to its
-  // last chunk (then ignored), so no select waits on a loaded value before
+  // Loads are unconditional: unit indices past the row are clamped to its
+  // last unit (then ignored), so no select waits on a loaded value before
   // the next load can issue.
-  u32x4 xr[CPL];
+  XR xr[CPL];
   uint32_t wr[CPL][WW];
-  u32x4 zr[TWO ? CPL : 1];
+  XR zr[TWO ? CPL : 1];
   const int64_t zoff = TWO ? z_row_offset(a, r) : 0;
 #pragma unroll
   for (int c = 0; c < CPL; ++c) {
     const int ch = j + c * LPR;
     const int chc = ch < nchunks ? ch : nchunks - 1;
-    xr[c] = ld16<X>(a.x, r * a.xs + (int64_t)chc * V);
-    if constexpr (TWO) zr[c] = ld16<X>(a.z, zoff + (int64_t)chc * V);
+    xr[c] = ld_raw<UB>(a.x, (r * a.xs + (int64_t)chc * UE) * X::kBytes);
+    if constexpr (TWO) zr[c] = ld_raw<UB>(a.z, (zoff + (int64_t)chc * UE) * X::kBytes);
   }
   if (has_w) {
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
       const int ch = j + c * LPR;
       const int chc = ch < nchunks ? ch : nchunks - 1;
+      const int64_t wb = (int64_t)chc * UE * W::kBytes;
+      if constexpr (WW == 2) {
+        const u32x2 t = ld_raw<8>(a.w, wb);
+        wr[c][0] = t[0];
+        wr[c][1] = t[1];
+      } else {
 #pragma unroll
-      for (int q = 0; q < WW / 4; ++q) {
-        const u32x4 t = ld16<W>(a.w, (int64_t)chc * V + q * Vec<W>::N);
+        for (int q = 0; q < WW / 4; ++q) {
+          const u32x4 t = ld_raw<16>(a.w, wb + 16 * q);
 #pragma unroll
-        for (int k = 0; k < 4; ++k) wr[c][4 * q + k] = t[k];
+          for (int k = 0; k < 4; ++k) wr[c][4 * q + k] = t[k];
+        }
       }
     }
   }
@@ -99,7 +112,7 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(NormArgs a) {
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
+      for (int k = 0; k < UW; ++k) {
         if constexpr (X::kBytes == 2) {
           xr[c][k] = X::pack(X::lo(xr[c][k]) + X::lo(zr[c][k]), X::hi(xr[c][k]) + X::hi(zr[c][k]));
         } else {
@@ -108,9 +121,7 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(NormArgs a) {
       }
       const int ch = j + c * LPR;
       if (a.h && live && ch < nchunks)
-        __builtin_nontemporal_store(
-            xr[c], reinterpret_cast<u32x4*>(reinterpret_cast<char*>(a.h) +
-                                            (r * a.hs + (int64_t)ch * V) * X::kBytes));
+        st_raw_nt<UB>(a.h, (r * a.hs + (int64_t)ch * UE) * X::kBytes, xr[c]);
     }
   }
   double ss = 0.0;
@@ -118,7 +129,7 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(NormArgs a) {
   for (int c = 0; c < CPL; ++c) {
     if (j + c * LPR >= nchunks) continue;
 #pragma unroll
-    for (int e = 0; e < V; ++e) {
+    for (int e = 0; e < UE; ++e) {
       const double d = (double)elem<X>(xr[c], e);
       ss = __builtin_fma(d, d, ss);
     }
@@ -133,9 +144,9 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(NormArgs a) {
   for (int c = 0; c < CPL; ++c) {
     const int ch = j + c * LPR;
     if (ch >= nchunks) continue;
-    float o[V];
+    float o[UE];
 #pragma unroll
-    for (int e = 0; e < V; e += 2) {
+    for (int e = 0; e < UE; e += 2) {
       float n0 = elem<X>(xr[c], e) * rr, n1 = elem<X>(xr[c], e + 1) * rr;
       if (rx) round2<X>(n0, n1);
       float w0 = has_w ? elem<W>(wr[c], e) : 1.0f, w1 = has_w ? elem<W>(wr[c], e + 1) : 1.0f;
@@ -161,7 +172,7 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(NormArgs a) {
       o[e] = n0;
       o[e + 1] = n1;
     }
-    if (live) store_elems<Y, V>(a.y, r * a.ys + (int64_t)ch * V, o);
+    if (live) store_elems<Y, UE>(a.y, r * a.ys + (int64_t)ch * UE, o);
   }
 }
 
@@ -209,14 +220,19 @@ __global__ __launch_bounds__(256) void rms_norm_generic_kernel(NormArgs a) {
 
 namespace {
 
+// Unit bytes of x per lane: 8 when Y is wider than X (so a unit's output is
+// one 16-byte store), else 16.
+template <class X, class Y>
+constexpr int unit_bytes() { return Y::kBytes > X::kBytes ? 8 : 16; }
+
 template <class X, class Y, class W, int LPR, int CPL, int MODE>
 void launch_fast(const NormArgs& a, hipStream_t s) {
   constexpr int RPW = 64 / LPR;
   const int64_t waves = (a.rows + RPW - 1) / RPW;
   const int wpb = waves >= 4096 ? 4 : 1;  // small problems: spread over CUs
   const int64_t blocks = (waves + wpb - 1) / wpb;
-  hipLaunchKernelGGL((rms_norm_kernel<X, Y, W, LPR, CPL, MODE>), dim3((unsigned)blocks),
-                     dim3(64 * wpb), 0, s, a);
+  hipLaunchKernelGGL((rms_norm_kernel<X, Y, W, LPR, CPL, MODE, unit_bytes<X, Y>()>),
+                     dim3((unsigned)blocks), dim3(64 * wpb), 0, s, a);
 }
 
 template <class X, class Y, int MODE>
@@ -227,8 +243,8 @@ void launch_generic(const NormArgs& a, hipStream_t s) {
                      dim3(64 * wpb), 0, s, a);
 }
 
-// Pick (LPR, CPL) for a row of `nchunks` 16-byte chunks; false -> generic.
-// The gated form (head_dim rows) stops at 128 chunks.
+// Pick (LPR, CPL) for a row of `nchunks` units; false -> generic.
+// The gated form (head_dim rows) stops at 128 units.
 template <class X, class Y, class W, int MODE>
 bool launch_by_shape(const NormArgs& a, int nchunks, hipStream_t s) {
   if (nchunks <= 4) { launch_fast<X, Y, W, 4, 1, MODE>(a, s); return true; }
@@ -248,8 +264,8 @@ bool launch_by_shape(const NormArgs& a, int nchunks, hipStream_t s) {
       case 8: launch_fast<X, Y, W, 64, 8, MODE>(a, s); return true;
       case 9: case 10: launch_fast<X, Y, W, 64, 10, MODE>(a, s); return true;
       case 11: case 12: launch_fast<X, Y, W, 64, 12, MODE>(a, s); return true;
-      case 13: case 14: case 15: case 16:
-        launch_fast<X, Y, W, 64, 16, MODE>(a, s); return true;
+      case 13: case 14: launch_fast<X, Y, W, 64, 14, MODE>(a, s); return true;
+      case 15: case 16: launch_fast<X, Y, W, 64, 16, MODE>(a, s); return true;
       default: break;
     }
   }
@@ -260,7 +276,7 @@ bool launch_by_shape(const NormArgs& a, int nchunks, hipStream_t s) {
 // any other weight dtype goes to the generic kernel.
 template <class X, class Y, int MODE>
 void launch_xy(const NormArgs& a, bool vec_ok, hipStream_t s) {
-  const int nchunks = a.n / Vec<X>::N;
+  const int nchunks = a.n / (unit_bytes<X, Y>() / X::kBytes);
   if (vec_ok) {
     if (!a.w || a.wdt == X::kCode) {
       if (launch_by_shape<X, Y, X, MODE>(a, nchunks, s)) return;

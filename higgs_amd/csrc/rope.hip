@@ -48,6 +48,7 @@ struct RopeArgs {
   uint32_t L;
   uint32_t tokens;
   int D, dims, half, R, tpb, hsum;
+  uint32_t hsum_magic;  // ceil(2^32 / hsum) for hsum >= 2: r / hsum = mulhi(r, magic)
   float scale, eps, inv_d;
   float inv_freq[kMaxHalf];
 };
@@ -69,7 +70,16 @@ __device__ inline void fill_table(const RopeArgs& a, float* cs, float* sn, uint3
   }
 }
 
-constexpr int kRopeBatch = 4;  // head rows a lane group keeps in flight
+// Head rows a lane group keeps in flight, and a fixed tokens-per-block count
+// (0: derived from the shape). Compile-time so that sweeps can rebuild with
+// other values.
+#ifndef HGK_ROPE_RB
+#define HGK_ROPE_RB 4
+#endif
+#ifndef HGK_ROPE_TPB
+#define HGK_ROPE_TPB 0
+#endif
+constexpr int kRopeBatch = HGK_ROPE_RB;
 
 // Row r of the block's rows (token-major: tk = r / hsum, head = r % hsum).
 struct RopeRow {
@@ -117,7 +127,57 @@ __device__ inline RopeRow rope_row(const RopeArgs& a, const RopePair& p, uint32_
   return o;
 }
 
-template <class X, int LPR, bool NORM>
+// The block's rows relative to its first token (b0, l0), for launches where
+// the host has checked that every row's element offset from that token fits
+// in 32 bits and that a block spans at most two sequences (L >= tokens per
+// block): no division and no 64-bit multiply per row.
+struct RopeBlock {
+  const char* x[2];
+  char* y[2];
+  int32_t xs1[2], xs2[2], xw[2], ys1[2], ys2[2], yw[2];  // xw = xs0 - L*xs1 (a wrap)
+  uint32_t l0;
+};
+
+template <class X>
+__device__ inline RopeBlock rope_block(const RopeArgs& a, uint32_t t0) {
+  RopeBlock o;
+  const uint32_t b0 = t0 / a.L;
+  o.l0 = t0 - b0 * a.L;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const RopeTensor& T = a.t[i];
+    o.x[i] = reinterpret_cast<const char*>(T.x) + ((int64_t)b0 * T.xs0 + (int64_t)o.l0 * T.xs1) * X::kBytes;
+    o.y[i] = reinterpret_cast<char*>(T.y) + ((int64_t)b0 * T.ys0 + (int64_t)o.l0 * T.ys1) * X::kBytes;
+    o.xs1[i] = (int32_t)T.xs1; o.xs2[i] = (int32_t)T.xs2;
+    o.xw[i] = (int32_t)(T.xs0 - (int64_t)a.L * T.xs1);
+    o.ys1[i] = (int32_t)T.ys1; o.ys2[i] = (int32_t)T.ys2;
+    o.yw[i] = (int32_t)(T.ys0 - (int64_t)a.L * T.ys1);
+  }
+  return o;
+}
+
+// Row r of the block: (token tk, head) with the element offsets of its q or
+// k row from the block's first token.
+struct RopeRow32 {
+  int32_t xo, yo;
+  int tk;
+  bool isk;
+};
+
+__device__ inline RopeRow32 rope_row32(const RopeArgs& a, const RopeBlock& bb, int qheads, int r) {
+  RopeRow32 o;
+  o.tk = a.hsum == 1 ? r : (int)__umulhi((uint32_t)r, a.hsum_magic);
+  const int h = r - o.tk * a.hsum;
+  o.isk = h >= qheads;
+  const int hh = o.isk ? h - qheads : h;
+  const int i = o.isk ? 1 : 0;
+  const bool wrap = bb.l0 + (uint32_t)o.tk >= a.L;
+  o.xo = o.tk * bb.xs1[i] + hh * bb.xs2[i] + (wrap ? bb.xw[i] : 0);
+  o.yo = o.tk * bb.ys1[i] + hh * bb.ys2[i] + (wrap ? bb.yw[i] : 0);
+  return o;
+}
+
+template <class X, int LPR, bool NORM, bool FAST>
 __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
   constexpr int V = Vec<X>::N;
   constexpr int RB = kRopeBatch;
@@ -142,17 +202,41 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
   }
 
   const RopePair pr = rope_pair(a);
+  RopeBlock bb;
+  if constexpr (FAST) bb = rope_block<X>(a, t0);
   u32x4 d0[RB], d1[RB];
-  RopeRow rw[RB];
+  struct {
+    char* y;  // the row's first output element
+    int tk;
+    bool isk;
+  } rw[RB];
   auto load_batch = [&](int base) {
 #pragma unroll
     for (int k = 0; k < RB; ++k) {
       // rows past the block's last are clamped to it (loaded, never stored)
       const int r = base + k * slots;
-      rw[k] = rope_row(a, pr, t0, r < rows ? r : rows - 1);
-      const void* xp = rw[k].isk ? pr.x[1] : pr.x[0];
-      d0[k] = ld16<X>(xp, rw[k].xb + c0 * V);
-      d1[k] = ld16<X>(xp, rw[k].xb + c1 * V);
+      const int rc = r < rows ? r : rows - 1;
+      const char* xp;
+      if constexpr (FAST) {
+        const RopeRow32 o = rope_row32(a, bb, pr.qheads, rc);
+        xp = (o.isk ? bb.x[1] : bb.x[0]) + (int64_t)o.xo * X::kBytes;
+        rw[k].y = (o.isk ? bb.y[1] : bb.y[0]) + (int64_t)o.yo * X::kBytes;
+        rw[k].tk = o.tk;
+        rw[k].isk = o.isk;
+      } else {
+        const RopeRow o = rope_row(a, pr, t0, rc);
+        xp = reinterpret_cast<const char*>(o.isk ? pr.x[1] : pr.x[0]) + o.xb * X::kBytes;
+        rw[k].y = reinterpret_cast<char*>(o.isk ? pr.y[1] : pr.y[0]) + o.yb * X::kBytes;
+        rw[k].tk = o.tk;
+        rw[k].isk = o.isk;
+      }
+      if constexpr (LPR >= 8) {  // each load instruction reads whole 128-byte lines
+        d0[k] = ld16_nt<X>(xp, c0 * V);
+        d1[k] = ld16_nt<X>(xp, c1 * V);
+      } else {  // half lines: the default policy keeps the line for its other half
+        d0[k] = ld16<X>(xp, c0 * V);
+        d1[k] = ld16<X>(xp, c1 * V);
+      }
     }
   };
 
@@ -220,9 +304,8 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
           v1[e + 1] = d1 + f1;
         }
       }
-      void* yp = isk ? pr.y[1] : pr.y[0];
-      store_elems<X, V>(yp, rw[k].yb + c0 * V, v0);
-      store_elems<X, V>(yp, rw[k].yb + c1 * V, v1);
+      store_elems<X, V>(rw[k].y, c0 * V, v0);
+      store_elems<X, V>(rw[k].y, c1 * V, v1);
     }
     base += slots * RB;
     if (base >= rows) break;
@@ -292,6 +375,23 @@ __global__ __launch_bounds__(256) void rope_generic_kernel(RopeArgs a) {
 namespace {
 
 
+// Whether the 32-bit row offsets of rope_row32 are exact for this launch.
+bool fast_index_ok(const RopeArgs& a) {
+  if ((uint32_t)a.tpb > a.L || a.hsum >= 16384) return false;
+  const int64_t lim = ((int64_t)1 << 31) - 1;
+  for (int i = 0; i < 2; ++i) {
+    const RopeTensor& T = a.t[i];
+    if (T.heads == 0) continue;
+    const int64_t st[2][3] = {{T.xs0, T.xs1, T.xs2}, {T.ys0, T.ys1, T.ys2}};
+    for (const auto& v : st) {
+      const int64_t wrap = v[0] - (int64_t)a.L * v[1];
+      const int64_t span = (int64_t)a.tpb * v[1] + (int64_t)T.heads * v[2] + (wrap < 0 ? -wrap : wrap);
+      if (v[1] > lim || v[2] > lim || span > lim) return false;
+    }
+  }
+  return true;
+}
+
 template <class X, int LPR, bool NORM>
 void launch_fast(RopeArgs& a, hipStream_t s) {
   // as many tokens per block as keep every lane group's rows in one batch of
@@ -301,10 +401,15 @@ void launch_fast(RopeArgs& a, hipStream_t s) {
   // chain's 4096 tokens x 40 heads measured 8% slower than 4)
   int tpb = std::max(1, std::min((slots * kRopeBatch) / a.hsum, kMaxTpb));
   while (tpb > 1 && (a.tokens + tpb - 1) / tpb < 1024u) --tpb;
+  if (HGK_ROPE_TPB > 0) tpb = std::min(HGK_ROPE_TPB, kMaxTpb);
   a.tpb = tpb;
+  a.hsum_magic = a.hsum >= 2 ? (uint32_t)((((uint64_t)1 << 32) + a.hsum - 1) / a.hsum) : 0u;
   const unsigned blocks = (a.tokens + tpb - 1) / tpb;
   const size_t shmem = 2u * tpb * a.half * sizeof(float);
-  hipLaunchKernelGGL((rope_kernel<X, LPR, NORM>), dim3(blocks), dim3(256), shmem, s, a);
+  if (fast_index_ok(a))
+    hipLaunchKernelGGL((rope_kernel<X, LPR, NORM, true>), dim3(blocks), dim3(256), shmem, s, a);
+  else
+    hipLaunchKernelGGL((rope_kernel<X, LPR, NORM, false>), dim3(blocks), dim3(256), shmem, s, a);
 }
 
 template <class X, bool NORM>

@@ -58,7 +58,7 @@ def test_launch_records_keep_every_buffer_alive():
                                                     torch.zeros(4, 8))], wg, 4, 8, 1e-6, 8, 0, 0))
         tab = track(torch.zeros(16, 2, dtype=torch.int32), torch.zeros(16, 1), torch.zeros(16, 1))
         ks.append(bench.k_embed(cx, "emb", [track(torch.zeros(3, dtype=torch.int32),
-                                                  torch.zeros(3, 16))], tab, 16, 16, 3, group=16))
+                                                  torch.zeros(3, 16))], [tab], 16, 16, 3, group=16))
         return ks
 
     kernels = build()
@@ -72,7 +72,13 @@ def test_algorithmic_bytes_match_the_published_table():
     z = torch.zeros(1)
     assert bench.k_rmsnorm(cx, "n", [(z, z)], z, 4096, 2048, 1e-5).bytes == 33_558_528
     assert bench.k_glu(cx, "g", [(z, z, z)], 4096, 8192, bench.SILU).bytes == 201_326_592
-    assert bench.k_embed(cx, "e", [(z, z)], (z, z, z), 128256, 2048, 4096).bytes == 21_512_192
+    assert bench.k_embed(cx, "e", [(z, z)], [(z, z, z)], 128256, 2048, 4096).bytes == 21_512_192
+    # the Gemma-2-9B chain's f32-output kernels: (1+w) norm and GeGLU
+    assert bench.k_rmsnorm(cx, "n", [(z, z)], z, 16384, 3584, 1e-6, plus_one=1,
+                           ydt=bench.F32).bytes == 16384 * 3584 * 6 + 3584 * 2
+    assert bench.k_glu(cx, "g", [(z, z, z)], 16384, 14336, bench.GELU,
+                       ydt=bench.F32).bytes == 1_879_048_192
+
     r = bench.k_qkrope(cx, "r", [(z, z, z, z)], 4, 1024, 32, 8, 64, 64, 5e5)
     assert r.bytes == 41_943_040
     r = bench.k_qkrope(cx, "r", [(z, z, z, z)], 8, 2048, 32, 8, 128, 128, 1e6, wq=z, wk=z)
@@ -83,3 +89,12 @@ def test_multi_gpu_request_is_refused():
     r = subprocess.run([sys.executable, "bench.py", "--gpus", "2"], capture_output=True,
                        text=True, cwd=bench.__file__.rsplit("/", 1)[0])
     assert r.returncode == 2 and "one GPU" in r.stderr
+
+
+def test_every_kernel_rotation_exceeds_the_infinity_cache():
+    """Per-kernel timing cycles each kernel over the buffer sets: the bytes it
+    touches per cycle must be well past the 256 MB cache."""
+    for kb in ([21_512_192, 33_558_528, 41_943_040, 201_326_592],
+               [150_536_192, 352_328_704, 402_653_184, 1_879_048_192]):
+        ns = bench.nsets_per_kernel(kb)
+        assert min(kb) * ns >= 1 << 30
