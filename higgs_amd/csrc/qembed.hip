@@ -21,6 +21,8 @@
 // embedding h (the residual stream) and y = rms_norm(h) in one pass: the
 // `embed_tokens.forward(ids)` then `input_layernorm.forward(&h)` pair of
 // transformer.rs:494 and 407.
+#include <algorithm>
+
 #include "../../include/higgs_hip.h"
 #include "hgk_common.h"
 #include "hgk_host.h"
@@ -117,21 +119,24 @@ __global__ __launch_bounds__(256) void qembed_kernel(QembArgs a) {
   }
 }
 
-// Any layout: one output element per thread.
+// Any layout: one output element per thread per pass of a grid-stride loop
+// (the grid is capped, so any element count launches).
 template <class S>
 __global__ __launch_bounds__(256) void qembed_generic_kernel(QembArgs a) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= a.n * a.hidden) return;
-  const int64_t t = i / a.hidden, k = i - t * a.hidden;
-  const int64_t id = load_id(a, t);
-  float x = 0.0f;
-  if (id >= 0 && id < a.vocab) {
-    const uint32_t q = (a.wq[id * a.wpr + k / 8] >> (4 * (k % 8))) & 0xfu;
-    const int64_t g = id * a.gpr + k / a.group;
-    x = deq<S>(q, load1<S>(a.sc, g), load1<S>(a.bi, g));
-    if (a.has_scale) x = S::round(x * S::round(a.scale));
+  const int64_t total = a.n * a.hidden;
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += stride) {
+    const int64_t t = i / a.hidden, k = i - t * a.hidden;
+    const int64_t id = load_id(a, t);
+    float x = 0.0f;
+    if (id >= 0 && id < a.vocab) {
+      const uint32_t q = (a.wq[id * a.wpr + k / 8] >> (4 * (k % 8))) & 0xfu;
+      const int64_t g = id * a.gpr + k / a.group;
+      x = deq<S>(q, load1<S>(a.sc, g), load1<S>(a.bi, g));
+      if (a.has_scale) x = S::round(x * S::round(a.scale));
+    }
+    store1<S>(a.out, t * a.os + k, x);
   }
-  store1<S>(a.out, t * a.os + k, x);
 }
 
 // Gather + dequantize + RMSNorm: one wave per token, as qembed_kernel. The
@@ -282,7 +287,7 @@ void launch(const QembArgs& a, bool vec_ok, hipStream_t s) {
     else hipLaunchKernelGGL((qembed_kernel<S, 16>), g, b, 0, s, a);
     return;
   }
-  const int64_t blocks = (a.n * a.hidden + 255) / 256;
+  const int64_t blocks = std::min<int64_t>((a.n * a.hidden + 255) / 256, (int64_t)1 << 20);
   hipLaunchKernelGGL((qembed_generic_kernel<S>), dim3((unsigned)blocks), dim3(256), 0, s, a);
 }
 

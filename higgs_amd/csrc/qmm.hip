@@ -26,6 +26,8 @@
 // MI355X -- the pairs of one expert run at the same time on different CUs,
 // and serialising them costs more than the re-read. At prefill (16 or more
 // pairs per expert) the grouped matrix-core kernel in qgemm.hip runs instead.
+#include <algorithm>
+
 #include "../../include/higgs_hip.h"
 #include "hgk_common.h"
 #include "hgk_host.h"
@@ -191,24 +193,28 @@ __global__ __launch_bounds__(256) void qmv_bf16_kernel(QmmArgs a) {
 // exact dequantized values, element-strided.
 template <class X, class S>
 __global__ __launch_bounds__(256) void qmv_generic_kernel(QmmArgs a) {
+  // one wave per output element, in a grid-stride loop over the waves (the
+  // loop bound is uniform per wave, so the reduction has every lane)
   const int lane = threadIdx.x & 63;
-  const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (item >= a.pairs * a.N) return;  // whole wave leaves together
-  const int64_t p = item / a.N, n = item - p * a.N;
-  const int64_t e = pair_expert(a, p);
-  const int64_t xr = pair_row(a, p);
-  float acc = 0.0f;
-  if (e >= 0 && e < a.E && xr >= 0) {
-    const int64_t gpr = a.K / a.group;
-    for (int64_t k = lane; k < a.K; k += 64) {
-      const uint32_t q = (a.w[(e * a.N + n) * (a.K / 8) + k / 8] >> (4 * (k % 8))) & 0xfu;
-      const int64_t g = (e * a.N + n) * gpr + k / a.group;
-      const float wv = load1<S>(a.sc, g) * (float)q + load1<S>(a.bi, g);
-      acc = __builtin_fmaf(load1<X>(a.x, xr * a.xs + k), wv, acc);
+  const int64_t items = a.pairs * a.N;
+  const int64_t stride = (int64_t)gridDim.x * 4;
+  for (int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); item < items; item += stride) {
+    const int64_t p = item / a.N, n = item - p * a.N;
+    const int64_t e = pair_expert(a, p);
+    const int64_t xr = pair_row(a, p);
+    float acc = 0.0f;
+    if (e >= 0 && e < a.E && xr >= 0) {
+      const int64_t gpr = a.K / a.group;
+      for (int64_t k = lane; k < a.K; k += 64) {
+        const uint32_t q = (a.w[(e * a.N + n) * (a.K / 8) + k / 8] >> (4 * (k % 8))) & 0xfu;
+        const int64_t g = (e * a.N + n) * gpr + k / a.group;
+        const float wv = load1<S>(a.sc, g) * (float)q + load1<S>(a.bi, g);
+        acc = __builtin_fmaf(load1<X>(a.x, xr * a.xs + k), wv, acc);
+      }
     }
+    acc = group_sum<64>(acc);
+    if (lane == 0) store1<X>(a.y, p * a.ys + n, acc);
   }
-  acc = group_sum<64>(acc);
-  if (lane == 0) store1<X>(a.y, p * a.ys + n, acc);
 }
 
 namespace {
@@ -238,7 +244,9 @@ bool launch_bf16(const QmmArgs& a, hipStream_t s) {
 template <class X, class S>
 void launch_generic(const QmmArgs& a, hipStream_t s) {
   const int64_t items = a.pairs * a.N;
-  hipLaunchKernelGGL((qmv_generic_kernel<X, S>), dim3((unsigned)((items + 3) / 4)), dim3(256), 0, s, a);
+  // a grid of at most 2^20 blocks (2^28 work-items), well inside HIP's limit
+  const int64_t blocks = std::min<int64_t>((items + 3) / 4, (int64_t)1 << 20);
+  hipLaunchKernelGGL((qmv_generic_kernel<X, S>), dim3((unsigned)blocks), dim3(256), 0, s, a);
 }
 
 }  // namespace

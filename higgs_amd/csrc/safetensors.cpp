@@ -512,21 +512,28 @@ extern "C" int hgk_st_upload(const hgk_st_file* f, int64_t index, void* dst, int
   // the copy that last read it
   const unsigned char* src = f->data + t->begin;
   bool used[2] = {false, false};
+  // On an error part-way, copies already queued may still read the staging
+  // buffers, which the next call refills: wait for the whole stream before
+  // returning, so no exit leaves a copy in flight.
+  auto drain_fail = [&](const char* what) {
+    (void)hipStreamSynchronize(s);
+    return fail(HGK_ERR_HIP, "%s: %s for '%s'", fn, what, t->name.c_str());
+  };
   for (int64_t off = 0, k = 0; off < n; off += (int64_t)kStage, ++k) {
     const int bi = (int)(k & 1);
     const size_t len = (size_t)std::min<int64_t>((int64_t)kStage, n - off);
     if (used[bi] && hipEventSynchronize(g_stage_ev[bi]) != hipSuccess)
-      return fail(HGK_ERR_HIP, "%s: hipEventSynchronize failed", fn);
+      return drain_fail("hipEventSynchronize failed");
     std::memcpy(g_stage[bi], src + off, len);
     if (hipMemcpyAsync(static_cast<char*>(dst) + off, g_stage[bi], len, hipMemcpyDefault, s) != hipSuccess)
-      return fail(HGK_ERR_HIP, "%s: hipMemcpyAsync failed for '%s'", fn, t->name.c_str());
-    if (hipEventRecord(g_stage_ev[bi], s) != hipSuccess) return fail(HGK_ERR_HIP, "%s: hipEventRecord failed", fn);
+      return drain_fail("hipMemcpyAsync failed");
+    if (hipEventRecord(g_stage_ev[bi], s) != hipSuccess) return drain_fail("hipEventRecord failed");
     used[bi] = true;
   }
   // the staging buffers are reused by the next call: wait for the last copies
   for (int i = 0; i < 2; ++i)
     if (used[i] && hipEventSynchronize(g_stage_ev[i]) != hipSuccess)
-      return fail(HGK_ERR_HIP, "%s: hipEventSynchronize failed", fn);
+      return drain_fail("hipEventSynchronize failed");
   return HGK_OK;
 }
 

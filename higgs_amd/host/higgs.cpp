@@ -6,6 +6,7 @@
 #include <cmath>
 #include <cstring>
 #include <initializer_list>
+#include <mutex>
 #include <sstream>
 
 namespace higgs {
@@ -196,15 +197,40 @@ StreamScope::~StreamScope() { t_current = prev_; }
 
 // ------------------------------------------------------------------ Buffer
 namespace detail {
+// A stream-ordered device allocation. It holds the Stream it was allocated on
+// (with that stream's owner, so the stream outlives the allocation) and every
+// other stream that has used it; the free is ordered after the work already
+// queued on each of those streams, so memory read by an op on another stream
+// is not handed out again while that op may still run.
 struct Buffer {
   void* ptr = nullptr;
   std::size_t bytes = 0;
-  hipStream_t stream = nullptr;
-  Buffer(std::size_t n, hipStream_t s) : bytes(n), stream(s) {
-    if (n) hip_check(hipMallocAsync(&ptr, n, s), "hipMallocAsync");
+  Stream stream;
+  std::mutex mu;
+  std::vector<Stream> users;  // streams other than `stream` that used the buffer
+  Buffer(std::size_t n, const Stream& s) : bytes(n), stream(s) {
+    if (n) hip_check(hipMallocAsync(&ptr, n, s.get()), "hipMallocAsync");
+  }
+  void note_use(const Stream& s) {
+    if (s.get() == stream.get()) return;
+    std::lock_guard<std::mutex> g(mu);
+    for (const Stream& u : users)
+      if (u.get() == s.get()) return;
+    users.push_back(s);
   }
   ~Buffer() {
-    if (ptr) (void)hipFreeAsync(ptr, stream);
+    if (!ptr) return;
+    for (const Stream& u : users) {
+      hipEvent_t ev = nullptr;
+      bool ordered = false;
+      if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) == hipSuccess) {
+        ordered = hipEventRecord(ev, u.get()) == hipSuccess &&
+                  hipStreamWaitEvent(stream.get(), ev, 0) == hipSuccess;
+        (void)hipEventDestroy(ev);
+      }
+      if (!ordered) (void)hipStreamSynchronize(u.get());
+    }
+    (void)hipFreeAsync(ptr, stream.get());
   }
   Buffer(const Buffer&) = delete;
   Buffer& operator=(const Buffer&) = delete;
@@ -237,7 +263,7 @@ Array Array::empty(const Shape& shape, Dtype dt) {
   a.strides_ = row_major(shape);
   a.dtype_ = dt;
   a.buf_ = std::make_shared<detail::Buffer>(static_cast<std::size_t>(numel(shape)) * size_of(dt),
-                                            Stream::task_local_or_default().get());
+                                            Stream::task_local_or_default());
   return a;
 }
 
@@ -298,6 +324,8 @@ bool Array::is_contiguous() const { return strides_ == row_major(shape_) || size
 
 void* Array::data() const {
   if (!buf_ || !buf_->ptr) return nullptr;
+  // every device access goes through here, on the calling thread's stream
+  buf_->note_use(Stream::task_local_or_default());
   return static_cast<char*>(buf_->ptr) + offset_ * static_cast<int64_t>(itemsize());
 }
 

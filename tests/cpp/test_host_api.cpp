@@ -876,6 +876,39 @@ TEST(test_ops_run_on_the_scoped_stream) {
   ASSERT_BITS_EQ(other, base);
 }
 
+// An Array outlives the scope and the Stream object it was allocated under:
+// the buffer keeps that stream alive, and its free waits for the other stream
+// that read it.
+TEST(test_array_outlives_its_stream_and_orders_cross_stream_frees) {
+  const int64_t R = 512, N = 4096;
+  auto xb = bits_of(normal(9010, R * N), OR_BF16);
+  auto wb = bits_of(normal(9011, N, 1.0f, 0.02f), OR_BF16);
+  const auto base =
+      higgs::fast::rms_norm(dev16(xb, {R, N}, Dtype::Bfloat16), dev16(wb, {N}, Dtype::Bfloat16), 1e-5f)
+          .to_bits();
+  Array x, w;
+  {
+    higgs::Stream a = higgs::Stream::create();
+    higgs::StreamScope scope(a);
+    x = dev16(xb, {R, N}, Dtype::Bfloat16);
+    w = dev16(wb, {N}, Dtype::Bfloat16);
+  }  // the Stream object `a` is gone; x and w still hold its stream
+  higgs::Stream b = higgs::Stream::create();
+  std::vector<uint16_t> got;
+  {
+    higgs::StreamScope scope(b);
+    Array y = higgs::fast::rms_norm(x, w, 1e-5f);
+    x = Array();  // freed on stream a, ordered after b's read of it
+    w = Array();
+    for (int i = 0; i < 8; ++i) {  // reuse the pool while b's kernel may still run
+      Array t = dev16(xb, {R, N}, Dtype::Bfloat16);
+      (void)t;
+    }
+    got = y.to_bits();
+  }
+  ASSERT_BITS_EQ(got, base);
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {

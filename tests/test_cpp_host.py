@@ -26,6 +26,7 @@ EXPECTED = {
     "test_quantized_embedding_forward_rms_norm",
     "test_load_quantized_checkpoint_drives_embedding_and_norm", "test_switch_mlp_forward_gather",
     "test_gated_delta_reference_cases_and_decode", "test_qlinear_forward_matches_oracle",
+    "test_array_outlives_its_stream_and_orders_cross_stream_frees",
 }
 
 

@@ -248,3 +248,45 @@ def test_unaligned_inputs_take_the_per_row_kernel(dev):
     ry, rs = _oracle(inp, O.BF16, norm=True)
     _check(to_host(y), ry, O.BF16, "unaligned y")
     _check(to_host(s), rs, O.BF16, "unaligned state")
+
+
+@pytest.mark.parametrize("dt,T,p_native,misalign", [
+    (O.BF16, 1, True, False),   # token kernel with a_log/dt_bias in the activation dtype
+    (O.F16, 1, False, False),   # f16 token kernel
+    (O.F16, 2, True, False),    # f16 two-step decode kernel, f16 params
+    (O.F16, 40, False, False),  # f16 chunked prefill
+    (O.F16, 5, False, True),    # f16 row kernel (q, k and the state 2 bytes off 16-byte alignment)
+    (O.BF16, 3, True, True),    # bf16 row kernel, bf16 params
+], ids=["bf16-token-bf16params", "f16-token", "f16-decode2-f16params", "f16-chunk", "f16-row",
+        "bf16-row-bf16params"])
+def test_param_dtypes_and_f16_kernels(dev, dt, T, p_native, misalign):
+    """Every kernel instantiation the header advertises beyond the paths above:
+    a_log/dt_bias stored in the activation dtype (the reference passes them in
+    the model dtype, qwen3_next.rs:1185-1201) and f16 activations, on the
+    token, decode, chunk and row kernels, with the fused q/k norm."""
+    B, Hk, Dk, Hv, Dv = 2, 2, 64, 4, 64
+    inp = _inputs(2900 + T + 7 * dt + int(misalign), B, T, Hk, Dk, Hv, Dv, dt)
+    p_dt = dt if p_native else O.F32
+    if p_native:
+        inp["a_log"] = O.from_f32(inp["a_log"], dt)
+        inp["dt_bias"] = O.from_f32(inp["dt_bias"], dt)
+    d = {n: to_dev(inp[n], dt, dev) for n in ("q", "k", "v", "a", "b", "state")}
+    if misalign:  # the same values one element into a larger buffer
+        for n in ("q", "k", "state"):
+            t = d[n]
+            buf = torch.empty(t.numel() + 1, dtype=t.dtype, device=dev)
+            buf[1:] = t.reshape(-1)
+            d[n] = buf[1:].view(t.shape)
+            assert d[n].data_ptr() % 16 != 0
+    a_log = to_dev(inp["a_log"], p_dt, dev)
+    dt_bias = to_dev(inp["dt_bias"], p_dt, dev)
+    tdt = {O.BF16: torch.bfloat16, O.F16: torch.float16}[dt]
+    wq, wk = H.gdn_qk_norm_weights(Dk, tdt, dev)
+    y, s = H.gated_delta(d["q"], d["k"], d["v"], a_log, d["a"], dt_bias, d["b"], d["state"],
+                         q_norm_w=wq, k_norm_w=wk)
+    owq, owk = O.gdn_qk_norm_weights(Dk, dt)
+    ry, rs = O.gated_delta(inp["q"], inp["k"], inp["v"], inp["a_log"], inp["a"], inp["dt_bias"],
+                           inp["b"], dt, p_dt=p_dt, state=inp["state"], qw=owq, kw=owk)
+    what = f"dt={dt} T={T} p_dt={p_dt} misalign={misalign}"
+    _check(to_host(y), ry, dt, what + " y")
+    _check(to_host(s), rs, dt, what + " state")

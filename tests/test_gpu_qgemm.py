@@ -113,3 +113,16 @@ def test_strided_rows_and_leading_dims(dev):
                             to_dev(s, O.BF16, dev), to_dev(b, O.BF16, dev))
     assert tuple(y3.shape) == (B, L, N)
     _check(to_host(y3).reshape(B * L, N), ref, O.BF16, "3-d x")
+
+
+def test_f16_gemv_grid_beyond_two_to_the_32_work_items(dev):
+    """f16 runs one wave per output element: M = 512 rows of a 151936-column
+    projection (the Qwen3 vocabulary) is 4.98e9 work-items, more than one HIP
+    launch holds; the kernel walks the outputs in a capped grid instead. The
+    oracle checks the first and last rows."""
+    M, N, K = 512, 151936, 64
+    x, w, s, b = _case(3601, M, N, K, dt=O.F16)
+    got = _run(dev, x, w, s, b, O.F16)
+    for rows in (np.r_[0:4], np.r_[M - 4:M]):
+        ref = O.quantized_matmul(x[rows], O.F16, w, s, b, O.F16)
+        _check(got[rows], ref, O.F16, f"f16 M={M} N={N} rows {rows[0]}..{rows[-1]}")
