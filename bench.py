@@ -602,6 +602,116 @@ def wl_qwen3_next_decode(cx):
                     cpu_sample=cpu_sample_ops)
 
 
+def k_qmm_swiglu(cx, name, sets, tab_g, tab_u, E, N, K, T, top_k, group=64):
+    """The gate and up gather_qmm and the SwiGLU in one launch; bytes = both
+    projections' distinct experts' weights + x + the activation + ids."""
+    P = T * top_k
+    per_expert = N * K // 2 + 2 * N * (K // group) * 2
+    uniq = sum(len(set(st[1].tolist())) for st in sets) / len(sets)
+    nbytes = int(2 * uniq * per_expert) + T * K * 2 + P * N * 2 + P * 4
+    (wg, sg, bg), (wu, su, bu) = tab_g, tab_u
+    args = [(BF16, _vp(x), T, K, top_k, None, _vp(wg), _vp(sg), _vp(bg), _vp(wu), _vp(su),
+             _vp(bu), BF16, E, N, K, group, 4, _vp(exd), I32, P, _vp(y), N, cx.stream)
+            for x, ex, exd, y in sets]
+    return Kernel(name, nbytes, cx.lib.hgk_gather_qmm_swiglu, args, T,
+                  keep=(sets, tab_g, tab_u))
+
+
+def k_gdn_gated(cx, name, sets, wq, wk, alog, dtb, wn, B, Hk, Dk, Hv, Dv, zrow, zgroup, zgs):
+    """One decode token of the recurrence and its gated output norm in one
+    launch; bytes = state read and written + q, k, v, a, b, z + the output."""
+    nbytes = (2 * B * Hv * Dv * Dk * 2 + B * (2 * Hk * Dk + Hv * Dv + 2 * Hv) * 2 +
+              2 * B * Hv * Dv * 2 + 2 * Dk * 2 + Dv * 2 + 2 * Hv * 4)
+    args = [(BF16, _vp(q), _vp(k), _vp(v), _vp(alog), _vp(a), _vp(dtb), _vp(b), F32, _vp(st),
+             _vp(wq), _vp(wk), _f(1e-6), B, Hk, Dk, Hv, Dv, _vp(st), None, _vp(z), zrow, zgroup,
+             zgs, _vp(wn), BF16, _f(1e-6), _vp(o), cx.stream) for q, k, v, a, b, st, z, o in sets]
+    return Kernel(name, nbytes, cx.lib.hgk_gated_delta_gated_norm, args, B,
+                  keep=(sets, wq, wk, alog, dtb, wn))
+
+
+def wl_qwen3_next_decode_layers(cx, fused=False):
+    """One decode step of 64 sequences through the 48 Qwen3-Next-80B-A3B
+    layers' per-layer kernels around the dense projections: per layer a
+    hidden RMSNorm [64, 2048]; for the 36 linear-attention layers the
+    gated-delta recurrence (Hk 16, Dk 128, Hv 32, Dv 128, fused q/k norm, the
+    state updated in place) and its gated output norm (z read in place from
+    in_proj_qkvz), for the 12 full-attention layers the q/k-norm + partial
+    RoPE; a second hidden RMSNorm; the routed experts' gate and up
+    gather_qmm (top-10 of 512, 512 x 2048, 4-bit) and SwiGLU. Unfused: the
+    reference's separate calls (7 launches per linear-attention layer).
+    Fused: recurrence + gated norm in one launch and gate + up + SwiGLU in
+    one launch (4 per layer). Replayed as one captured graph per step."""
+    torch = cx.torch
+    S, Hd, Hk, Dk, Hv, Dv, Hq, Hkv, D, E, top_k, I = 64, 2048, 16, 128, 32, 128, 16, 2, 256, 512, 10, 512
+    P = S * top_k
+    from higgs_amd.ops import gdn_qk_norm_weights
+    gwq, gwk = gdn_qk_norm_weights(Dk, torch.bfloat16, cx.dev)
+    alog = (torch.rand(Hv, device=cx.dev, generator=cx.gen) - 1.0).contiguous()
+    dtb = (torch.rand(Hv, device=cx.dev, generator=cx.gen) - 0.5).contiguous()
+    wn = cx.randn((Hd,), torch.bfloat16, 1.0, 0.02)
+    wg = cx.randn((Dv,), torch.bfloat16, 1.0, 0.02)
+    wq = cx.randn((D,), torch.bfloat16, 1.0, 0.02)
+    wk = cx.randn((D,), torch.bfloat16, 1.0, 0.02)
+    offs = torch.randint(1, 32769, (S,), dtype=torch.int32, device=cx.dev, generator=cx.gen)
+    ntab = 4  # expert table sets, rotated over the layers (~0.6 GB each)
+    tabs = [{nm: cx.qtable_experts(E, I, Hd) for nm in ("gate", "up")} for _ in range(ntab)]
+    g = torch.Generator().manual_seed(7)
+    ns = 1  # one set: every layer has its own buffers and the step walks ~6 GB
+    r = lambda shape, lo, hi: (torch.rand(shape, device=cx.dev, generator=cx.gen) * (hi - lo) + lo
+                               ).to(torch.bfloat16)
+    kernels = []
+    for layer in range(48):
+        n1 = [(cx.randn((S, Hd), torch.bfloat16), cx.empty((S, Hd), torch.bfloat16))]
+        n2 = [(cx.randn((S, Hd), torch.bfloat16), cx.empty((S, Hd), torch.bfloat16))]
+        kernels.append(k_rmsnorm(cx, "rms_norm", n1, wn, S, Hd, 1e-6))
+        if layer % 4 == 3:
+            rp = [(cx.randn((S, 1, Hq, 512), torch.bfloat16), cx.randn((S, 1, Hkv, D), torch.bfloat16),
+                   cx.empty((S, Hq, 1, D), torch.bfloat16), cx.empty((S, Hkv, 1, D), torch.bfloat16))]
+            kernels.append(k_qkrope(cx, "qk_norm_partial_rope", rp, S, 1, Hq, Hkv, D, 64, 1e7,
+                                    wq=wq, wk=wk, eps=1e-6, offsets=offs, q_block=512))
+        else:
+            q, k = r((S, 1, Hk, Dk), -1, 1), r((S, 1, Hk, Dk), -1, 1)
+            v, a, b = r((S, 1, Hv, Dv), -1, 1), r((S, 1, Hv), -1, 1), r((S, 1, Hv), -1, 1)
+            st = r((S, Hv, Dv, Dk), -0.1, 0.1)
+            qkvz = cx.randn((S, Hk, 768), torch.bfloat16)
+            z = qkvz[:, :, 512:]
+            if fused:
+                o = cx.empty((S, Hv, Dv), torch.bfloat16)
+                kernels.append(k_gdn_gated(cx, "gdn_gated_norm", [(q, k, v, a, b, st, z, o)], gwq,
+                                           gwk, alog, dtb, wg, S, Hk, Dk, Hv, Dv, Dv, 2, 768))
+            else:
+                y = cx.empty((S, 1, Hv, Dv), torch.bfloat16)
+                kernels.append(k_gdn(cx, "gdn_decode", [(q, k, v, a, b, st, y, st)], gwq, gwk, alog,
+                                     dtb, S, 1, Hk, Dk, Hv, Dv))
+                o = cx.empty((S * Hv, Dv), torch.bfloat16)
+                kernels.append(k_gated(cx, "gated_rms_norm", [(y, z, o)], wg, S * Hv, Dv, 1e-6,
+                                       Dv, 2, 768))
+        kernels.append(k_rmsnorm(cx, "rms_norm", n2, wn, S, Hd, 1e-6))
+        ex = torch.stack([torch.randperm(E, generator=g)[:top_k] for _ in range(S)]).reshape(-1).to(
+            torch.int32)
+        exd = ex.to(cx.dev)
+        x = cx.randn((S, Hd), torch.bfloat16)
+        tb = tabs[layer % ntab]
+        if fused:
+            act = cx.empty((P, I), torch.bfloat16)
+            kernels.append(k_qmm_swiglu(cx, "qmm_gate_up_swiglu", [(x, ex, exd, act)], tb["gate"],
+                                        tb["up"], E, I, Hd, S, top_k))
+        else:
+            go, uo = cx.empty((P, I), torch.bfloat16), cx.empty((P, I), torch.bfloat16)
+            kernels.append(k_qmm(cx, "qmm_gate", [(x, ex, exd, go)], tb["gate"], E, I, Hd, S, top_k,
+                                 top_k))
+            kernels.append(k_qmm(cx, "qmm_up", [(x, ex, exd, uo)], tb["up"], E, I, Hd, S, top_k,
+                                 top_k))
+            kernels.append(k_glu(cx, "swiglu_experts", [(go, uo, cx.empty((P, I), torch.bfloat16))],
+                                 P, I, SILU))
+    cfg = {"workload": "qwen3-next-80b-a3b decode step, 48 layers' per-layer kernels" +
+                       (" (fused)" if fused else " (separate calls)"),
+           "sequences": S, "layers": 48, "launches": len(kernels), "hidden": Hd,
+           "gdn": "Hk 16 x 128, Hv 32 x 128", "experts": f"top-{top_k} of {E}, {I} x {Hd}, 4-bit"}
+    return Workload("qwen3_next_decode_layers" + ("_fused" if fused else ""), cfg, kernels, ns, S,
+                    graph=True)
+
+
 WORKLOADS = {
     "llama32_1b_chain": wl_llama_chain,
     "rmsnorm_512x2048": wl_rmsnorm_512,
@@ -614,6 +724,8 @@ WORKLOADS = {
     "qwen3_next_gdn": wl_qwen3_next_gdn,
     "qwen3_next_qlinear": wl_qwen3_next_qlinear,
     "qwen3_next_moe_prefill": wl_qwen3_next_moe_prefill,
+    "qwen3_next_decode_layers": wl_qwen3_next_decode_layers,
+    "qwen3_next_decode_layers_fused": lambda cx: wl_qwen3_next_decode_layers(cx, fused=True),
 }
 
 
@@ -691,19 +803,27 @@ def kernel_times(cx, wl, graph, per_group=20, groups=5):
     he = HipEvents()
     rec = he.h.hipEventRecord
     st = cx.stream
-    seen, per = set(), []
+    # every instance of a kernel (e.g. one per layer, each on its own buffers)
+    # takes its turn, so a kernel's launches walk all of its buffers
+    inst, order = {}, []
     for k in wl.kernels:
-        if k.name in seen:
-            continue
-        seen.add(k.name)
+        if k.name not in inst:
+            inst[k.name] = []
+            order.append(k.name)
+        inst[k.name].append(k)
+    per = []
+    for name in order:
+        ks = inst[name]
+        k = ks[0]
+        plan = [(ks[i % len(ks)], (i // len(ks)) % wl.nsets) for i in range(per_group)]
         if graph:
-            g = _capture(cx, [_launcher(k, i % wl.nsets) for i in range(per_group)])
+            g = _capture(cx, [_launcher(kk, si) for kk, si in plan])
             go = g.replay
         else:
-            plan = [k.argsets[i % wl.nsets] for i in range(per_group)]
+            calls = [(kk.fn, kk.argsets[si]) for kk, si in plan]
 
-            def go(plan=plan, fn=k.fn, name=k.name):
-                for a in plan:
+            def go(calls=calls, name=k.name):
+                for fn, a in calls:
                     if fn(*a):
                         raise RuntimeError(f"{name}: {cx.lib.hgk_last_error().decode()}")
         go()  # warm

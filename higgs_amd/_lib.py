@@ -46,10 +46,17 @@ PROTOTYPES = {
                                                 _int, _f32, _vp, _int, _i64, _vp]),
     "hgk_gather_qmm": (_int, [_int, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _int, _i64, _i64,
                               _i64, _int, _int, _vp, _int, _i64, _vp, _i64, _vp]),
+    "hgk_gather_qmm_swiglu": (_int, [_int, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp,
+                                     _vp, _int, _i64, _i64, _i64, _int, _int, _vp, _int, _i64,
+                                     _vp, _i64, _vp]),
     "hgk_quantized_matmul": (_int, [_int, _vp, _i64, _i64, _vp, _vp, _vp, _int, _i64, _i64, _int,
                                     _int, _vp, _i64, _vp]),
     "hgk_gated_delta": (_int, [_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _int, _vp, _vp, _vp, _f32,
                                _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp]),
+    "hgk_gated_delta_gated_norm": (_int, [_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _int, _vp,
+                                          _vp, _vp, _f32, _i64, _i64, _i64, _i64, _i64, _vp,
+                                          _vp, _vp, _i64, _i64, _i64, _vp, _int, _f32, _vp,
+                                          _vp]),
     "hgk_st_open": (_int, [C.c_char_p, C.POINTER(_vp)]),
     "hgk_st_close": (None, [_vp]),
     "hgk_st_count": (_i64, [_vp]),

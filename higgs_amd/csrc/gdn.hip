@@ -61,6 +61,14 @@ struct GdnArgs {
   int64_t B, T, Hk, Dk, Hv, Dv;
   void* y;
   void* state_out;
+  // gated RMSNorm epilogue (token kernel): out = round(round(z*round(sigmoid z))
+  // * rms_norm(y, gw, geps)) over each (b, v-head) row of Dv, z row r at
+  // (r / gzg) * gzgs + (r % gzg) * gzs
+  const void* gz;
+  int64_t gzs, gzg, gzgs;
+  const void* gw;
+  float geps, inv_dv;
+  void* gout;
 };
 
 // Sum over the 32 lanes of a half wave (every lane receives the sum).
@@ -641,7 +649,7 @@ __device__ inline void buf_store_words(__amdgpu_buffer_rsrc_t rs, uint32_t off, 
   }
 }
 
-template <class X, class P, int NPT, bool NORM, int RPL>
+template <class X, class P, int NPT, bool NORM, int RPL, bool GN = false>
 __global__ __launch_bounds__(256) void gated_delta_token_kernel(GdnArgs a) {
   constexpr int DK = 16 * NPT;
   constexpr int NW = NPT * X::kBytes / 4;
@@ -668,6 +676,16 @@ __global__ __launch_bounds__(256) void gated_delta_token_kernel(GdnArgs a) {
   }
 #pragma unroll
   for (int r = 0; r < RPL; ++r) vraw[r] = ldraw<X>(a.v, row * a.Dv + (r0 + r < a.Dv ? r0 + r : a.Dv - 1));
+  // gated-norm epilogue: this group's RPL rows of z and of the norm weight
+  // (contiguous in dv; the launcher checks their 16-byte alignment)
+  constexpr int GW = GN ? RPL * X::kBytes / 4 : 1;
+  uint32_t zraw[GW], gwraw[GW];
+  if constexpr (GN) {
+    const int64_t rc = r0 < a.Dv ? r0 : 0;
+    const int64_t zrow = (row / a.gzg) * a.gzgs + (row % a.gzg) * a.gzs;
+    load_row_raw<X, RPL>(a.gz, zrow + rc, zraw);
+    load_row_raw<X, RPL>(a.gw, rc, gwraw);
+  }
   // the state rows through buffer descriptors (the launcher keeps the state
   // under 2^31 bytes): no state reads zeros, rows past Dv read zeros and
   // their stores are dropped, so no load or store sits under a branch and
@@ -741,10 +759,48 @@ __global__ __launch_bounds__(256) void gated_delta_token_kernel(GdnArgs a) {
     if (r + HGK_GDN_WIN < RPL) buf_load_words<NW>(sin, soff[r + HGK_GDN_WIN], raw[r + HGK_GDN_WIN]);
     __builtin_amdgcn_sched_barrier(0);
   }
-  if (j == 0) {
+  if (j == 0 && (!GN || a.y != nullptr)) {
 #pragma unroll
     for (int r = 0; r < RPL; ++r)
       if (r0 + r < a.Dv) store1<X>(a.y, row * a.Dv + r0 + r, out[r]);
+  }
+  if constexpr (GN) {
+    // the block holds the whole (b, v-head) row of Dv outputs (one row tile):
+    // each lane group sums its rows' squares (y rounded to X, as the norm
+    // reads it) in f64, and every thread adds the groups' sums in one order
+    constexpr int G = 256 / 16;
+    __shared__ double part[G];
+    const int grp = tid >> 4;
+    float yr[RPL];
+    double ss = 0.0;
+#pragma unroll
+    for (int r = 0; r < RPL; ++r) {
+      yr[r] = r0 + r < a.Dv ? X::round(out[r]) : 0.0f;
+      ss = __builtin_fma((double)yr[r], (double)yr[r], ss);
+    }
+    if (j == 0) part[grp] = ss;
+    __syncthreads();
+    double tot = 0.0;
+#pragma unroll
+    for (int q = 0; q < G; ++q) tot += part[q];
+    const float rs = rms_scale(tot, a.inv_dv, a.geps);
+    // lane j < RPL of the group finishes row r0 + j (every lane holds the
+    // group's y, z and weights)
+    if (j < RPL && r0 + j < a.Dv) {
+      float yj = yr[0], zj = elem<X>(zraw, 0), wj = elem<X>(gwraw, 0);
+#pragma unroll
+      for (int r = 1; r < RPL; ++r) {
+        if (j == r) {
+          yj = yr[r];
+          zj = elem<X>(zraw, r);
+          wj = elem<X>(gwraw, r);
+        }
+      }
+      const float nv = X::round(X::round(yj * rs) * wj);
+      const float sg = X::round(mlx_sigmoid(zj));
+      const float act = X::round(zj * sg);
+      store1<X>(a.gout, row * a.Dv + r0 + j, act * nv);
+    }
   }
 }
 
@@ -1212,6 +1268,31 @@ bool launch_token_p(const GdnArgs& a, hipStream_t s) {
   }
 }
 
+// The token kernel with the gated-norm epilogue: one block per (b, v-head)
+// row of Dv (Dv <= the block's rows, a multiple of the rows per lane group).
+template <class X, bool NORM>
+bool launch_token_gn(const GdnArgs& a, hipStream_t s) {
+  constexpr int RPL = HGK_GDN_RPL, WPB = HGK_GDN_WPB;
+  static_assert(WPB == 4, "the epilogue reduces over a 256-thread block");
+  const dim3 grid(1u, (unsigned)a.Hv, (unsigned)a.B);
+  const dim3 block(64 * WPB);
+  const bool p32 = a.pdt == DT_F32;
+#define HGK_GDN_GN(NPT)                                                                          \
+  if (p32) hipLaunchKernelGGL((gated_delta_token_kernel<X, F32, NPT, NORM, RPL, true>), grid,    \
+                              block, 0, s, a);                                                   \
+  else hipLaunchKernelGGL((gated_delta_token_kernel<X, X, NPT, NORM, RPL, true>), grid, block,  \
+                          0, s, a);                                                              \
+  return true;
+  switch (a.Dk) {
+    case 32: HGK_GDN_GN(2)
+    case 64: HGK_GDN_GN(4)
+    case 128: HGK_GDN_GN(8)
+    case 256: HGK_GDN_GN(16)
+    default: return false;
+  }
+#undef HGK_GDN_GN
+}
+
 // a_log / dt_bias in f32 or in the activation dtype (other pairings take the
 // decode kernel, which reads them in any float dtype)
 template <class X, bool NORM>
@@ -1320,6 +1401,71 @@ extern "C" int hgk_gated_delta(int dtype, const void* q, const void* k, const vo
   if (dtype == DT_BF16) ok = norm ? launch_x<BF16, true>(g, s, aligned) : launch_x<BF16, false>(g, s, aligned);
   else if (dtype == DT_F16) ok = norm ? launch_x<F16, true>(g, s, aligned) : launch_x<F16, false>(g, s, aligned);
   else ok = norm ? launch_x<F32, true>(g, s, aligned) : launch_x<F32, false>(g, s, aligned);
+  if (!ok) return fail(HGK_ERR_UNSUPPORTED, "%s: head_k_dim not supported", fn);
+  return launch_status(fn);
+}
+
+extern "C" int hgk_gated_delta_gated_norm(
+    int dtype, const void* q, const void* k, const void* v, const void* a_log, const void* a,
+    const void* dt_bias, const void* b, int param_dtype, const void* state_in,
+    const void* q_norm_w, const void* k_norm_w, float eps, int64_t batch, int64_t k_heads,
+    int64_t head_k_dim, int64_t v_heads, int64_t head_v_dim, void* state_out, void* y,
+    const void* z, int64_t z_row_stride, int64_t z_group_rows, int64_t z_group_stride,
+    const void* norm_w, int norm_w_dtype, float norm_eps, void* out, void* stream) {
+  clear_error();
+  const char* fn = "hgk_gated_delta_gated_norm";
+  if (dtype != DT_BF16 && dtype != DT_F16 && dtype != DT_F32)
+    return fail(HGK_ERR_ARG, "%s: dtype must be f32, bf16 or f16", fn);
+  if (param_dtype != DT_F32 && param_dtype != dtype)
+    return fail(HGK_ERR_UNSUPPORTED, "%s: a_log/dt_bias must be f32 or the activation dtype", fn);
+  if (norm_w_dtype != dtype)
+    return fail(HGK_ERR_UNSUPPORTED, "%s: the norm weight must have the activation dtype", fn);
+  if (batch < 0 || k_heads <= 0 || v_heads <= 0 || head_v_dim <= 0 || v_heads % k_heads)
+    return fail(HGK_ERR_ARG, "%s: bad shape", fn);
+  if (head_k_dim != 32 && head_k_dim != 64 && head_k_dim != 128 && head_k_dim != 256)
+    return fail(HGK_ERR_UNSUPPORTED, "%s: head_k_dim=%lld (32, 64, 128 or 256)", fn, (long long)head_k_dim);
+  constexpr int RPL = HGK_GDN_RPL, ROWS = 4 * RPL * HGK_GDN_WPB;
+  if (head_v_dim > ROWS || head_v_dim % RPL)
+    return fail(HGK_ERR_UNSUPPORTED, "%s: head_v_dim=%lld (a multiple of %d up to %d)", fn,
+                (long long)head_v_dim, RPL, ROWS);
+  if ((q_norm_w == nullptr) != (k_norm_w == nullptr))
+    return fail(HGK_ERR_ARG, "%s: pass both q and k norm weights or neither", fn);
+  if (!(eps >= 0.0f) || !(norm_eps >= 0.0f)) return fail(HGK_ERR_ARG, "%s: eps must be >= 0", fn);
+  if (!q || !k || !v || !a_log || !a || !dt_bias || !b || !state_out || !z || !norm_w || !out)
+    return fail(HGK_ERR_ARG, "%s: null pointer", fn);
+  const int64_t rows = batch * v_heads;
+  if (z_group_rows <= 0 || z_group_rows > rows) {
+    z_group_rows = rows > 0 ? rows : 1;
+    z_group_stride = 0;
+  }
+  if ((z_group_rows > 1 && z_row_stride < head_v_dim) || z_row_stride < 0 ||
+      (rows > z_group_rows && z_group_stride < (z_group_rows - 1) * z_row_stride + head_v_dim))
+    return fail(HGK_ERR_ARG, "%s: z rows overlap", fn);
+  if (batch > 65535 || v_heads > 65535) return fail(HGK_ERR_UNSUPPORTED, "%s: batch or v_heads > 65535", fn);
+  const int64_t dk_bytes = dtype_bytes(dtype);
+  if (batch * v_heads * head_v_dim * head_k_dim * dk_bytes >= ((int64_t)1 << 31))
+    return fail(HGK_ERR_UNSUPPORTED, "%s: state of 2 GiB or more", fn);
+  auto al = [](const void* p) { return p == nullptr || ((uintptr_t)p & 15u) == 0; };
+  const int vpc = 16 / (int)dk_bytes;  // elements per 16 bytes
+  if (!al(q) || !al(k) || !al(state_in) || !al(state_out) || !al(z) || !al(norm_w) ||
+      z_row_stride % vpc || z_group_stride % vpc)
+    return fail(HGK_ERR_UNSUPPORTED, "%s: q, k, the state, z and the norm weight must be 16-byte aligned", fn);
+  if (batch == 0) return HGK_OK;
+  GdnArgs g{};
+  g.q = q; g.k = k; g.v = v; g.a_log = a_log; g.a = a; g.dt_bias = dt_bias; g.b = b;
+  g.state_in = state_in; g.qw = q_norm_w; g.kw = k_norm_w; g.pdt = param_dtype; g.eps = eps;
+  g.inv_dk = (float)(1.0 / (double)head_k_dim);
+  g.B = batch; g.T = 1; g.Hk = k_heads; g.Dk = head_k_dim; g.Hv = v_heads; g.Dv = head_v_dim;
+  g.hgrp = (int)(v_heads / k_heads);
+  g.y = y; g.state_out = state_out;
+  g.gz = z; g.gzs = z_row_stride; g.gzg = z_group_rows; g.gzgs = z_group_stride; g.gw = norm_w;
+  g.geps = norm_eps; g.inv_dv = (float)(1.0 / (double)head_v_dim); g.gout = out;
+  const hipStream_t s = as_stream(stream);
+  const bool norm = q_norm_w != nullptr;
+  bool ok;
+  if (dtype == DT_BF16) ok = norm ? launch_token_gn<BF16, true>(g, s) : launch_token_gn<BF16, false>(g, s);
+  else if (dtype == DT_F16) ok = norm ? launch_token_gn<F16, true>(g, s) : launch_token_gn<F16, false>(g, s);
+  else ok = norm ? launch_token_gn<F32, true>(g, s) : launch_token_gn<F32, false>(g, s);
   if (!ok) return fail(HGK_ERR_UNSUPPORTED, "%s: head_k_dim not supported", fn);
   return launch_status(fn);
 }

@@ -26,6 +26,7 @@
 #include <algorithm>
 
 #include "../../include/higgs_hip.h"
+#include "hgk_act.h"
 #include "hgk_common.h"
 #include "hgk_host.h"
 
@@ -42,55 +43,6 @@ struct GluArgs {
   uint32_t total;  // chunks overall
   int contig;      // all three tensors densely packed
 };
-
-constexpr int kTieWindow = 16;  // f32 ulps; the fast sigmoid errs by <= 3
-
-// True when the f32 value `b` (bits) lies within kTieWindow ulps of a value
-// halfway between two neighbours of T, or where T's rounding is not decided
-// by the low bits alone (f16 subnormal range).
-template <class X>
-__device__ inline bool near_tie(uint32_t b) {
-  if constexpr (X::kCode == DT_BF16) {
-    const int d = (int)(b & 0xffffu) - 0x8000;
-    return d <= kTieWindow && d >= -kTieWindow;
-  } else {
-    const int d = (int)(b & 0x1fffu) - 0x1000;
-    return (d <= kTieWindow && d >= -kTieWindow) || (b & 0x7fffffffu) < 0x38800000u;
-  }
-}
-
-// Fast sigmoid with MLX's branch structure; *slow is set when the result may
-// round differently from the exact one.
-template <class X>
-__device__ inline float sigmoid16_fast(float g, bool* slow) {
-  const float e = __builtin_amdgcn_exp2f(fabsf(g) * 1.4426950408889634f);
-  const float y = __builtin_amdgcn_rcpf(1.0f + e);
-  const float sg = g < 0.0f ? y : 1.0f - y;
-  *slow = !(fabsf(g) <= 64.0f) || near_tie<X>(f2u(sg));  // !(<=) also catches NaN
-  return sg;
-}
-
-// N SwiGLU outputs round_T(round_T(g*round_T(sigmoid(g))) * u) for 16-bit T,
-// bit-identical to the exact MLX composition: all fast sigmoids first, then
-// one (rarely taken) branch that redoes the flagged ones exactly.
-template <class X, int N>
-__device__ inline void swiglu16(const float* g, const float* u, float* o) {
-  float sg[N];
-  bool fl[N];
-  bool any = false;
-#pragma unroll
-  for (int e = 0; e < N; ++e) {
-    sg[e] = sigmoid16_fast<X>(g[e], &fl[e]);
-    any |= fl[e];
-  }
-  if (any) {
-#pragma unroll
-    for (int e = 0; e < N; ++e)
-      if (fl[e]) sg[e] = mlx_sigmoid(g[e]);
-  }
-#pragma unroll
-  for (int e = 0; e < N; ++e) o[e] = X::round(X::round(g[e] * X::round(sg[e])) * u[e]);
-}
 
 template <class X, int ACT>
 __device__ inline float glu1(float g, float u) {

@@ -867,11 +867,38 @@ Array nn::SwitchMlpWeights::forward_gather(const Array& x, const Array& indices)
                             operands_text({{"x", &x}, {"indices", &indices}}));
   const int64_t T = x.dim(0), top_k = indices.dim(1);
   const Array idx = indices.reshape({T * top_k});
-  const Array g = gather_qmm(x, gate_proj.weight, gate_proj.scales, gate_proj.biases, idx, true,
-                             gate_proj.group_size, gate_proj.bits, top_k);
-  const Array u = gather_qmm(x, up_proj.weight, up_proj.scales, up_proj.biases, idx, true,
-                             up_proj.group_size, up_proj.bits, top_k);
-  const Array act = swiglu(g, u);
+  // gate, up and the SwiGLU in one launch where the fused decode kernel
+  // applies (same weights' shapes, bf16, few pairs per expert); otherwise the
+  // reference's three calls
+  Array act;
+  bool fused = false;
+  const Array& gw = gate_proj.weight;
+  const bool same = gw.shape() == up_proj.weight.shape() &&
+                    gate_proj.scales.shape() == up_proj.scales.shape() &&
+                    gate_proj.group_size == up_proj.group_size && gate_proj.bits == up_proj.bits;
+  if (same && gw.ndim() == 3 && x.dtype() == Dtype::Bfloat16 && x.strides()[1] == 1 &&
+      gw.is_contiguous() && up_proj.weight.is_contiguous() && gate_proj.scales.is_contiguous() &&
+      gate_proj.biases.is_contiguous() && up_proj.scales.is_contiguous() &&
+      up_proj.biases.is_contiguous() && idx.is_contiguous()) {
+    const int64_t E = gw.dim(0), N = gw.dim(1), K = x.dim(1), P = T * top_k;
+    act = Array::empty({P, N}, x.dtype());
+    const int st = hgk_gather_qmm_swiglu(
+        static_cast<int>(x.dtype()), x.data(), T, x.strides()[0], top_k, nullptr,
+        static_cast<const uint32_t*>(gw.data()), gate_proj.scales.data(), gate_proj.biases.data(),
+        static_cast<const uint32_t*>(up_proj.weight.data()), up_proj.scales.data(),
+        up_proj.biases.data(), static_cast<int>(gate_proj.scales.dtype()), E, N, K,
+        gate_proj.group_size, gate_proj.bits, idx.data(), static_cast<int>(idx.dtype()), P,
+        act.data(), N, stream_arg());
+    if (st != HGK_ERR_UNSUPPORTED) check(st, "forward_gather", {{"x", &x}, {"indices", &indices}});
+    fused = st == HGK_OK;
+  }
+  if (!fused) {
+    const Array g = gather_qmm(x, gate_proj.weight, gate_proj.scales, gate_proj.biases, idx, true,
+                               gate_proj.group_size, gate_proj.bits, top_k);
+    const Array u = gather_qmm(x, up_proj.weight, up_proj.scales, up_proj.biases, idx, true,
+                               up_proj.group_size, up_proj.bits, top_k);
+    act = swiglu(g, u);
+  }
   const Array d = gather_qmm(act, down_proj.weight, down_proj.scales, down_proj.biases, idx, true,
                              down_proj.group_size, down_proj.bits, 1);
   return d.reshape({T, top_k, d.dim(1)});

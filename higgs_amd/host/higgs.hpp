@@ -258,7 +258,8 @@ struct QLinear {
 struct SwitchMlpWeights {
   QLinear gate_proj, up_proj, down_proj;
   // x [T, D], indices [T, top_k] (Int32/Uint32) -> [T, top_k, D]: gate and up
-  // gather_qmm, swiglu, down gather_qmm, as forward_gather does.
+  // gather_qmm, swiglu, down gather_qmm, as forward_gather does (gate, up and
+  // swiglu in one launch where the fused decode kernel applies).
   Array forward_gather(const Array& x, const Array& indices) const;
 };
 }  // namespace nn

@@ -341,6 +341,41 @@ def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: t
     return out
 
 
+def gather_qmm_swiglu(x: torch.Tensor, w_gate: torch.Tensor, scales_gate: torch.Tensor,
+                      biases_gate: torch.Tensor, w_up: torch.Tensor, scales_up: torch.Tensor,
+                      biases_up: torch.Tensor, rhs_indices: torch.Tensor, group_size: int = 64,
+                      bits: int = 4, *, x_row_div: int = 1,
+                      lhs_indices: Optional[torch.Tensor] = None,
+                      out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """swiglu(gather_qmm(x, gate...), gather_qmm(x, up...)) -- the gate/up half of
+    SwitchMlpWeights::forward_gather (qwen3_next.rs:862-886) -- in one launch
+    where the fused decode kernel applies, else as the three calls. Returns
+    [P, N] in x's dtype."""
+    E, N = w_gate.shape[0], w_gate.shape[1]
+    K = x.shape[1]
+    idx = rhs_indices.reshape(-1).contiguous()
+    P = idx.numel()
+    lhs = None if lhs_indices is None else lhs_indices.reshape(-1).contiguous()
+    if out is None:
+        out = torch.empty((P, N), dtype=x.dtype, device=x.device)
+    if w_up.shape != w_gate.shape or scales_up.shape != scales_gate.shape:
+        raise HgkError(1, "gate and up weights must have the same shapes")
+    st = lib().hgk_gather_qmm_swiglu(
+        dtype_code(x.dtype), _ptr(x), x.shape[0], x.stride(0), x_row_div, _ptr(lhs),
+        _ptr(w_gate.contiguous()), _ptr(scales_gate.contiguous()), _ptr(biases_gate.contiguous()),
+        _ptr(w_up.contiguous()), _ptr(scales_up.contiguous()), _ptr(biases_up.contiguous()),
+        dtype_code(scales_gate.dtype), E, N, K, group_size, bits, _ptr(idx),
+        dtype_code(idx.dtype), P, _ptr(out), out.stride(0), _stream(x.device))
+    if st == 2:  # not the fused kernel's regime: the reference's three calls
+        g = gather_qmm(x, w_gate, scales_gate, biases_gate, idx, True, group_size, bits,
+                       x_row_div=x_row_div, lhs_indices=lhs)
+        u = gather_qmm(x, w_up, scales_up, biases_up, idx, True, group_size, bits,
+                       x_row_div=x_row_div, lhs_indices=lhs)
+        return swiglu(g, u, out=out)
+    check(st)
+    return out
+
+
 def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
                      biases: torch.Tensor, transpose: bool = True, group_size: int = 64,
                      bits: int = 4, *, out: Optional[torch.Tensor] = None) -> torch.Tensor:
@@ -407,6 +442,48 @@ def gated_delta(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, a_log: torch.
                                 _ptr(q_norm_w), _ptr(k_norm_w), eps, B, T, Hk, Dk, Hv, Dv,
                                 _ptr(y), _ptr(state_out), _stream(q.device)))
     return y, state_out
+
+
+def gated_delta_gated_norm(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                           a_log: torch.Tensor, a: torch.Tensor, dt_bias: torch.Tensor,
+                           b: torch.Tensor, state: Optional[torch.Tensor], z: torch.Tensor,
+                           norm_weight: torch.Tensor, norm_eps: float, *,
+                           q_norm_w: Optional[torch.Tensor] = None,
+                           k_norm_w: Optional[torch.Tensor] = None, eps: float = 1e-6,
+                           state_out: Optional[torch.Tensor] = None,
+                           out: Optional[torch.Tensor] = None):
+    """One decode token of GatedDeltaNet from the recurrence through its gated
+    output norm (qwen3_next.rs:1185-1205): swiglu(z, norm(gated_delta(...).y))
+    in one launch where it applies, else as the two calls. q, k [B, 1, Hk, Dk],
+    v [B, 1, Hv, Dv], a, b [B, 1, Hv]; z [B, 1, Hv, Dv] (may be a strided view
+    of in_proj_qkvz). Returns (out [B, 1, Hv, Dv], new_state)."""
+    B, T, Hk, Dk = q.shape
+    Hv, Dv = v.shape[2], v.shape[3]
+    if T != 1:
+        raise HgkError(1, "gated_delta_gated_norm is the one-token (decode) form")
+    for t in (q, k, v, a, b):
+        if not t.is_contiguous() or t.dtype != q.dtype:
+            raise HgkError(1, "q, k, v, a, b must be contiguous and share a dtype")
+    if a_log.dtype != dt_bias.dtype:
+        raise HgkError(1, "a_log and dt_bias must share a dtype")
+    if state_out is None:
+        state_out = torch.empty((B, Hv, Dv, Dk), dtype=q.dtype, device=q.device)
+    if out is None:
+        out = torch.empty((B, T, Hv, Dv), dtype=q.dtype, device=q.device)
+    zs, zg, zgs = _z_layout(z, B * Hv, Dv)
+    st = lib().hgk_gated_delta_gated_norm(
+        dtype_code(q.dtype), _ptr(q), _ptr(k), _ptr(v), _ptr(a_log.contiguous()), _ptr(a),
+        _ptr(dt_bias.contiguous()), _ptr(b), dtype_code(a_log.dtype),
+        None if state is None else _ptr(state.contiguous()), _ptr(q_norm_w), _ptr(k_norm_w), eps,
+        B, Hk, Dk, Hv, Dv, _ptr(state_out), None, _ptr(z), zs, zg, zgs, _ptr(norm_weight),
+        dtype_code(norm_weight.dtype), norm_eps, _ptr(out), _stream(q.device))
+    if st == 2:  # outside the fused form: the reference's two calls
+        y, state_out = gated_delta(q, k, v, a_log, a, dt_bias, b, state, q_norm_w=q_norm_w,
+                                   k_norm_w=k_norm_w, eps=eps, state_out=state_out)
+        gated_rms_norm(y, z, norm_weight, norm_eps, out=out)
+        return out, state_out
+    check(st)
+    return out, state_out
 
 
 # ---------------------------------------------------------------- embedding

@@ -257,6 +257,30 @@ int hgk_gather_qmm(int dtype, const void* x, int64_t x_rows, int64_t x_row_strid
                    int rhs_dtype, int64_t pairs, void* y, int64_t y_row_stride, void* stream);
 
 /*
+ * The gate and up expert projections of SwitchMlpWeights::forward_gather and
+ * the SwiGLU between them (crates/higgs-models/src/qwen3_next.rs:862-886:
+ * gate_out = gather_qmm(x, gate...), up_out = gather_qmm(x, up...),
+ * activated = swiglu(&gate_out, &up_out)) in one launch: for each pair p and
+ * column n,
+ *   g = bf16(gather_qmm(x, w_gate)[p, n]), u = bf16(gather_qmm(x, w_up)[p, n])
+ *   y[p, n] = round(round(g * round(sigmoid(g))) * u)
+ * bit-identical to the three calls (each projection rounded to bf16 as
+ * gather_qmm writes it, then hgk_glu's SwiGLU). Operands as hgk_gather_qmm,
+ * with two weight sets of the same shape [n_experts, n, k/8] and one expert
+ * index per pair. The decode (one GEMV per pair) form only: bf16 x and
+ * scales, k in {512, 1024, 2048, 4096}, 16-byte aligned x and weights, and
+ * fewer than 16 pairs per expert on average; other calls return
+ * HGK_ERR_UNSUPPORTED and run as hgk_gather_qmm twice plus hgk_glu.
+ */
+int hgk_gather_qmm_swiglu(int dtype, const void* x, int64_t x_rows, int64_t x_row_stride,
+                          int64_t x_row_div, const int32_t* lhs_indices, const uint32_t* w_gate,
+                          const void* scales_gate, const void* biases_gate, const uint32_t* w_up,
+                          const void* scales_up, const void* biases_up, int scales_dtype,
+                          int64_t n_experts, int64_t n, int64_t k, int group_size, int bits,
+                          const void* rhs_indices, int rhs_dtype, int64_t pairs, void* y,
+                          int64_t y_row_stride, void* stream);
+
+/*
  * quantized_matmul(x, w, scales, biases, transpose = true, group_size, bits):
  * QLinear::forward (crates/higgs-models/src/qwen3_next.rs:174-221, via
  * quantized_forward 174-183). x [M, K] (row stride x_row_stride, unit column
@@ -293,6 +317,33 @@ int hgk_gated_delta(int dtype, const void* q, const void* k, const void* v, cons
                     const void* state_in, const void* q_norm_w, const void* k_norm_w, float eps,
                     int64_t batch, int64_t seq_len, int64_t k_heads, int64_t head_k_dim,
                     int64_t v_heads, int64_t head_v_dim, void* y, void* state_out, void* stream);
+
+/*
+ * One decode token of the GatedDeltaNet layer from the recurrence through its
+ * gated output norm (crates/higgs-models/src/qwen3_next.rs:1185-1205:
+ * gated_delta_kernel_ffi, then normed = self.norm.forward(&y) and
+ * gated_out = swiglu(&z, &normed)) in one launch:
+ *   y   = hgk_gated_delta(...) for T = 1 (rounded to `dtype`)
+ *   out = round(round(z * round(sigmoid(z))) * rms_norm(y, norm_w, norm_eps))
+ * over each (b, v-head) row of Dv -- bit-identical to hgk_gated_delta then
+ * hgk_gated_rms_norm. Operands as hgk_gated_delta with seq_len 1; y may be
+ * NULL (not written). z's rows are addressed as in hgk_gated_rms_norm (row r
+ * = b * v_heads + hv at (r / z_group_rows) * z_group_stride + (r %
+ * z_group_rows) * z_row_stride, so z is read in place from in_proj_qkvz);
+ * norm_w [Dv] in `dtype`; out [B, Hv, Dv] contiguous. head_v_dim a multiple
+ * of 8 up to 128 (one block per value head), q, k, the state, z and norm_w
+ * 16-byte aligned, z's strides whole 16-byte units, the state under 2 GiB;
+ * otherwise HGK_ERR_UNSUPPORTED (run the two calls).
+ */
+int hgk_gated_delta_gated_norm(int dtype, const void* q, const void* k, const void* v,
+                               const void* a_log, const void* a, const void* dt_bias,
+                               const void* b, int param_dtype, const void* state_in,
+                               const void* q_norm_w, const void* k_norm_w, float eps,
+                               int64_t batch, int64_t k_heads, int64_t head_k_dim,
+                               int64_t v_heads, int64_t head_v_dim, void* state_out, void* y,
+                               const void* z, int64_t z_row_stride, int64_t z_group_rows,
+                               int64_t z_group_stride, const void* norm_w, int norm_w_dtype,
+                               float norm_eps, void* out, void* stream);
 
 /* ------------------------------------------------------------------------
  * Checkpoint files: the safetensors files MLX 4-bit checkpoints ship in

@@ -290,3 +290,67 @@ def test_param_dtypes_and_f16_kernels(dev, dt, T, p_native, misalign):
     what = f"dt={dt} T={T} p_dt={p_dt} misalign={misalign}"
     _check(to_host(y), ry, dt, what + " y")
     _check(to_host(s), rs, dt, what + " state")
+
+
+# ------------------------------------------------------------------ with the gated output norm
+@pytest.mark.parametrize("dt,B,Hk,Dk,Hv,Dv,p_native", [
+    (O.BF16, 64, 16, 128, 32, 128, False),  # Qwen3-Next-80B-A3B decode, 64 sequences
+    (O.BF16, 3, 2, 64, 4, 64, True),        # half a block of rows, bf16 params
+    (O.F16, 2, 2, 128, 4, 128, False),
+    (O.F32, 2, 1, 32, 2, 32, False),
+    (O.BF16, 2, 2, 128, 4, 256, False),     # Dv past one block: the two calls
+], ids=["qwen3-next-decode", "dv64-bf16params", "f16", "f32", "dv256-two-calls"])
+def test_decode_token_with_gated_norm(dev, dt, B, Hk, Dk, Hv, Dv, p_native):
+    """gated_delta then norm(y) and swiglu(z, normed) (qwen3_next.rs:1185-1205)
+    in one launch: bit-identical to hgk_gated_delta + hgk_gated_rms_norm on the
+    device, and within the recurrence's bar of the oracle's composition
+    (1 ulp in y can move the gated output by up to 2 ulp). z is read in place
+    from an in_proj_qkvz-shaped buffer ([B, 1, Hk, 2*Dk + 2*(Hv/Hk)*Dv], z the
+    last (Hv/Hk)*Dv of each key head's block)."""
+    inp = _inputs(3000 + B + Dv + dt, B, 1, Hk, Dk, Hv, Dv, dt)
+    p_dt = dt if p_native else O.F32
+    if p_native:
+        inp["a_log"] = O.from_f32(inp["a_log"], dt)
+        inp["dt_bias"] = O.from_f32(inp["dt_bias"], dt)
+    vpk = Hv // Hk
+    blk = 2 * Dk + 2 * vpk * Dv
+    qkvz = O.from_f32(O.normal(3100 + Dv, (B, 1, Hk, blk)), dt)
+    nw = O.from_f32(O.normal(3101 + Dv, (Dv,), 1.0, 0.02), dt)
+    tdt = {O.BF16: torch.bfloat16, O.F16: torch.float16, O.F32: torch.float32}[dt]
+    d = {n: to_dev(inp[n], dt, dev) for n in ("q", "k", "v", "a", "b", "state")}
+    a_log, dt_bias = to_dev(inp["a_log"], p_dt, dev), to_dev(inp["dt_bias"], p_dt, dev)
+    tq = to_dev(qkvz, dt, dev)
+    z = tq[..., blk - vpk * Dv:].unflatten(-1, (vpk, Dv))  # [B, 1, Hk, vpk, Dv] view
+    twn = to_dev(nw, dt, dev)
+    wq, wk = H.gdn_qk_norm_weights(Dk, tdt, dev)
+    out, st = H.gated_delta_gated_norm(d["q"], d["k"], d["v"], a_log, d["a"], dt_bias, d["b"],
+                                       d["state"], z, twn, 1e-6, q_norm_w=wq, k_norm_w=wk)
+    y2, st2 = H.gated_delta(d["q"], d["k"], d["v"], a_log, d["a"], dt_bias, d["b"], d["state"],
+                            q_norm_w=wq, k_norm_w=wk)
+    out2 = H.gated_rms_norm(y2, z, twn, 1e-6)
+    assert np.array_equal(to_host(st), to_host(st2)), "state differs from gated_delta's"
+    assert np.array_equal(to_host(out), to_host(out2)), "out differs from the two calls"
+    # the oracle's gated norm on the device's y, bit for bit
+    yh = to_host(y2).reshape(B * Hv, Dv)
+    zh = np.ascontiguousarray(qkvz[..., blk - vpk * Dv:]).reshape(B * Hv, Dv)
+    on_dev_y = O.gated_rms_norm(yh, zh, dt, nw, dt, 1e-6).reshape(B, 1, Hv, Dv)
+    if dt == O.F32:
+        assert_close(to_host(out), on_dev_y, O.F32, rtol=1e-5, atol=1e-6, what="gated norm f32")
+    else:
+        assert np.array_equal(to_host(out), on_dev_y), "gated norm differs from the oracle's"
+    owq, owk = O.gdn_qk_norm_weights(Dk, dt)
+    ry, rs = O.gated_delta(inp["q"], inp["k"], inp["v"], inp["a_log"], inp["a"], inp["dt_bias"],
+                           inp["b"], dt, p_dt=p_dt, state=inp["state"], qw=owq, kw=owk)
+    zr = np.ascontiguousarray(qkvz[..., blk - vpk * Dv:]).reshape(B * Hv, Dv)
+    ref = O.gated_rms_norm(ry.reshape(B * Hv, Dv), zr, dt, nw, dt, 1e-6).reshape(B, 1, Hv, Dv)
+    got = to_host(out)
+    what = f"gdn+gated norm dt={dt} B={B} Dv={Dv}"
+    if dt == O.F32:
+        err = float(np.abs(got - ref).max())
+        print(f"[gdn] {what}: max|err|={err:.2e}", flush=True)
+        assert err <= 1e-4, what
+    else:
+        ef = exact_frac(got, ref, dt)
+        print(f"[gdn] {what}: exact vs oracle composition={ef:.5f}", flush=True)
+        assert_close(got, ref, dt, max_ulp=2, what=what)
+        assert ef >= 0.98, what
