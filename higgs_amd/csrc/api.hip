@@ -1,5 +1,6 @@
 // api.hip -- library-wide C-ABI pieces: thread-local last error, ABI
 // version, and the host-side RoPE frequency helpers.
+#include <atomic>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -29,6 +30,24 @@ int launch_status(const char* what) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(HGK_ERR_HIP, "%s: launch failed: %s", what, hipGetErrorString(e));
   return HGK_OK;
+}
+
+int resident_waves() {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<int> cached[kMaxDevices];  // 0: not yet queried
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) dev = -1;
+  if (dev >= 0) {
+    const int v = cached[dev].load(std::memory_order_relaxed);
+    if (v > 0) return v;
+  }
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev < 0 ? 0 : dev) !=
+          hipSuccess || cus <= 0)
+    cus = 256;
+  const int v = cus * 4 * 8;
+  if (dev >= 0) cached[dev].store(v, std::memory_order_relaxed);
+  return v;
 }
 
 }  // namespace hgk

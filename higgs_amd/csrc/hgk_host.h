@@ -15,6 +15,11 @@ void clear_error();
 // After a launch: HGK_OK, or HGK_ERR_HIP with the HIP error text.
 int launch_status(const char* what);
 
+// Waves the current device keeps resident at once when each uses at most 64
+// VGPRs: compute units x 4 SIMDs x 8 waves (256 x 32 = 8192 on MI355X).
+// Queried once per device; used to size persistent (grid-stride) launches.
+int resident_waves();
+
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 inline int dtype_bytes(int dt) { return (dt == 1 || dt == 2) ? 2 : 4; }

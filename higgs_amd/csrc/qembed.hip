@@ -69,53 +69,108 @@ __device__ inline float deq(uint32_t q, float s, float b) {
   return S::round(S::round((float)q * s) + b);
 }
 
-// One wave per token. At step s lane i owns packed word w = s*64 + i (8 codes,
-// one group): each load instruction of the wave reads 256 contiguous bytes of
-// the row and each store writes 1 KB contiguous, so no cache line is touched
-// by more than one instruction.
-template <class S, int STEPS>
+// The loads of one token's row, issued together and kept as raw words until
+// used (converting a value where it is loaded would make the compiler wait for
+// it step by step). At step s lane i owns packed word w = s*64 + i (8 codes,
+// one group): each code load instruction of the wave reads 256 contiguous
+// bytes of the row. Addresses are clamped into the row instead of predicating
+// the loads, so no select has to wait on a loaded value before the next load
+// issues.
+//  PERM: the row's scales and biases (gpr even, gpr <= 64) come in with one
+//        32-bit load per lane -- lane l < gpr/2 holds scale pair l, lane
+//        gpr/2 + l bias pair l -- and each step takes its group's pair from
+//        the owning lane by a cross-lane permute: 1 load instruction per row
+//        instead of 2 per step (each of which read 16 useful bytes).
+//  else: one 16-bit scale and bias load per step.
+template <class S, int STEPS, bool PERM>
+struct QembRow {
+  uint32_t codes[STEPS];
+  uint32_t sraw[PERM ? 1 : STEPS], braw[PERM ? 1 : STEPS];
+  bool valid;
+
+  __device__ inline void load(const QembArgs& a, int64_t t, int lane) {
+    const int64_t id = load_id(a, t);
+    valid = id >= 0 && id < a.vocab;
+    const int64_t row = valid ? id : 0;
+    const uint32_t* wrow = a.wq + row * a.wpr;
+    const uint16_t* sc = reinterpret_cast<const uint16_t*>(a.sc) + row * a.gpr;
+    const uint16_t* bi = reinterpret_cast<const uint16_t*>(a.bi) + row * a.gpr;
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s) {
+      const int w = s * 64 + lane;
+      codes[s] = wrow[w < a.wpr ? w : a.wpr - 1];
+    }
+    if constexpr (PERM) {
+      const int half = a.gpr >> 1;
+      const int l = lane < a.gpr ? lane : a.gpr - 1;
+      const uint16_t* p = l < half ? sc + 2 * l : bi + 2 * (l - half);
+      sraw[0] = *reinterpret_cast<const uint32_t*>(p);
+    } else {
+#pragma unroll
+      for (int s = 0; s < STEPS; ++s) {
+        const int w = s * 64 + lane;
+        const int g = ((w < a.wpr ? w : a.wpr - 1) * 8) / a.group;
+        sraw[s] = (uint32_t)sc[g];
+        braw[s] = (uint32_t)bi[g];
+      }
+    }
+  }
+
+  // The scale and bias of step s's group, as f32.
+  __device__ inline void group_affine(const QembArgs& a, int s, int lane, float& sv, float& bv) const {
+    if constexpr (PERM) {
+      const int w = s * 64 + lane;
+      int g = (w * 8) / a.group;
+      g = g < a.gpr ? g : a.gpr - 1;
+      const uint32_t sw = (uint32_t)__shfl((int)sraw[0], g >> 1);
+      const uint32_t bw = (uint32_t)__shfl((int)sraw[0], (a.gpr >> 1) + (g >> 1));
+      sv = (g & 1) ? S::hi(sw) : S::lo(sw);
+      bv = (g & 1) ? S::hi(bw) : S::lo(bw);
+    } else {
+      sv = S::lo(sraw[s]);
+      bv = S::lo(braw[s]);
+    }
+  }
+};
+
+// Persistent waves over the tokens (wave w takes tokens w, w + W, w + 2W, ...
+// for W waves in the grid, sized to what the chip holds resident), software
+// pipelined: the next token's loads are issued before the current token's
+// row is dequantized and stored, so every wave keeps one row of reads in
+// flight under its stores. Each store writes 1 KB contiguous.
+template <class S, int STEPS, bool PERM>
 __global__ __launch_bounds__(256) void qembed_kernel(QembArgs a) {
   const int lane = threadIdx.x & 63;
-  const int64_t t = (int64_t)blockIdx.x * (blockDim.x >> 6) +
-                    __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wpb = blockDim.x >> 6;
+  const int64_t nw = (int64_t)gridDim.x * wpb;
+  int64_t t = (int64_t)blockIdx.x * wpb + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (t >= a.n) return;  // whole wave leaves together
-  const int64_t id = load_id(a, t);
-  const bool valid = id >= 0 && id < a.vocab;
-  const int64_t row = valid ? id : 0;
   const float osc = S::round(a.scale);
-  const uint32_t* wrow = a.wq + row * a.wpr;
-  const int64_t grow = row * a.gpr;
-
-  // every load of the token goes out first, as raw words (converting a value
-  // where it is loaded would make the compiler wait for it step by step)
-  uint32_t codes[STEPS], sraw[STEPS], braw[STEPS];
-  const uint16_t* sc = reinterpret_cast<const uint16_t*>(a.sc);
-  const uint16_t* bi = reinterpret_cast<const uint16_t*>(a.bi);
-  // (addresses are clamped into the row instead of predicating the loads, so
-  // no select has to wait on a loaded value before the next load issues)
+  QembRow<S, STEPS, PERM> cur, nxt;
+  cur.load(a, t, lane);
+  for (;;) {
+    const int64_t tn = t + nw;
+    const bool more = tn < a.n;
+    if (more) nxt.load(a, tn, lane);
 #pragma unroll
-  for (int s = 0; s < STEPS; ++s) {
-    const int w = s * 64 + lane;
-    const int wc = w < a.wpr ? w : a.wpr - 1;
-    const int g = (wc * 8) / a.group;
-    codes[s] = wrow[wc];
-    sraw[s] = (uint32_t)sc[grow + g];
-    braw[s] = (uint32_t)bi[grow + g];
-  }
+    for (int s = 0; s < STEPS; ++s) {
+      float sv, bv;
+      cur.group_affine(a, s, lane, sv, bv);  // (a permute: every lane takes part)
+      const int w = s * 64 + lane;
+      if (w >= a.wpr) continue;
+      float v[8];
 #pragma unroll
-  for (int s = 0; s < STEPS; ++s) {
-    const int w = s * 64 + lane;
-    if (w >= a.wpr) continue;
-    const float sv = S::lo(sraw[s]), bv = S::lo(braw[s]);
-    float v[8];
-#pragma unroll
-    for (int nib = 0; nib < 8; ++nib) {
-      const uint32_t q = (codes[s] >> (4 * nib)) & 0xfu;
-      float x = deq<S>(q, sv, bv);
-      x = a.has_scale ? S::round(x * osc) : x;
-      v[nib] = valid ? x : 0.0f;
+      for (int nib = 0; nib < 8; ++nib) {
+        const uint32_t q = (cur.codes[s] >> (4 * nib)) & 0xfu;
+        float x = deq<S>(q, sv, bv);
+        x = a.has_scale ? S::round(x * osc) : x;
+        v[nib] = cur.valid ? x : 0.0f;
+      }
+      store_elems<S, 8>(a.out, t * a.os + (int64_t)w * 8, v);
     }
-    store_elems<S, 8>(a.out, t * a.os + (int64_t)w * 8, v);
+    if (!more) break;
+    t = tn;
+    cur = nxt;
   }
 }
 
@@ -272,19 +327,26 @@ __global__ __launch_bounds__(256) void qembed_norm_generic_kernel(QembArgs a) {
 
 namespace {
 
+template <class S, bool PERM>
+void launch_fast(const QembArgs& a, int steps, hipStream_t s) {
+  // waves: one per token up to what the chip keeps resident (8 per SIMD)
+  const int wpb = a.n >= 1024 ? 4 : 1;
+  const int64_t waves = std::min<int64_t>(a.n, (int64_t)resident_waves());
+  const dim3 g((unsigned)((waves + wpb - 1) / wpb)), b(64 * wpb);
+  if (steps <= 1) hipLaunchKernelGGL((qembed_kernel<S, 1, PERM>), g, b, 0, s, a);
+  else if (steps <= 2) hipLaunchKernelGGL((qembed_kernel<S, 2, PERM>), g, b, 0, s, a);
+  else if (steps <= 4) hipLaunchKernelGGL((qembed_kernel<S, 4, PERM>), g, b, 0, s, a);
+  else if (steps <= 7) hipLaunchKernelGGL((qembed_kernel<S, 7, PERM>), g, b, 0, s, a);
+  else if (steps <= 8) hipLaunchKernelGGL((qembed_kernel<S, 8, PERM>), g, b, 0, s, a);
+  else hipLaunchKernelGGL((qembed_kernel<S, 16, PERM>), g, b, 0, s, a);
+}
+
 template <class S>
-void launch(const QembArgs& a, bool vec_ok, hipStream_t s) {
+void launch(const QembArgs& a, bool vec_ok, bool perm_ok, hipStream_t s) {
   const int steps = (a.wpr + 63) / 64;
   if (vec_ok && steps <= 16) {
-    const int wpb = a.n >= 1024 ? 4 : 1;
-    const unsigned blocks = (unsigned)((a.n + wpb - 1) / wpb);
-    const dim3 g(blocks), b(64 * wpb);
-    if (steps <= 1) hipLaunchKernelGGL((qembed_kernel<S, 1>), g, b, 0, s, a);
-    else if (steps <= 2) hipLaunchKernelGGL((qembed_kernel<S, 2>), g, b, 0, s, a);
-    else if (steps <= 4) hipLaunchKernelGGL((qembed_kernel<S, 4>), g, b, 0, s, a);
-    else if (steps <= 7) hipLaunchKernelGGL((qembed_kernel<S, 7>), g, b, 0, s, a);
-    else if (steps <= 8) hipLaunchKernelGGL((qembed_kernel<S, 8>), g, b, 0, s, a);
-    else hipLaunchKernelGGL((qembed_kernel<S, 16>), g, b, 0, s, a);
+    if (perm_ok) launch_fast<S, true>(a, steps, s);
+    else launch_fast<S, false>(a, steps, s);
     return;
   }
   const int64_t blocks = std::min<int64_t>((a.n * a.hidden + 255) / 256, (int64_t)1 << 20);
@@ -329,8 +391,12 @@ extern "C" int hgk_quantized_embedding(const void* ids, int ids_dtype, int64_t n
   a.out = out; a.os = out_row_stride; a.hidden = hidden;
   const bool vec_ok = (reinterpret_cast<uintptr_t>(w_q) & 3u) == 0 && aligned16(out) &&
                       hidden % 8 == 0 && out_row_stride % 8 == 0;
-  if (scales_dtype == DT_BF16) launch<BF16>(a, vec_ok, as_stream(stream));
-  else launch<F16>(a, vec_ok, as_stream(stream));
+  // one 32-bit load per lane brings a row's scales and biases when they fit
+  // one register across the wave and every row's pairs are 4-byte aligned
+  const bool perm_ok = a.gpr % 2 == 0 && a.gpr <= 64 &&
+                       ((reinterpret_cast<uintptr_t>(scales) | reinterpret_cast<uintptr_t>(biases)) & 3u) == 0;
+  if (scales_dtype == DT_BF16) launch<BF16>(a, vec_ok, perm_ok, as_stream(stream));
+  else launch<F16>(a, vec_ok, perm_ok, as_stream(stream));
   return launch_status(fn);
 }
 

@@ -388,6 +388,37 @@ def test_qembed_codes_bitexact_and_variants(dev):
     assert not got[3].any() and not got[4].any()
 
 
+@pytest.mark.parametrize("V,Hd,n,group,sdt,offset", [
+    (300, 4608, 9000, 32, O.BF16, 0),   # 144 groups a row: one scale/bias load per step
+    (300, 448, 9000, 64, O.BF16, 0),    # 7 groups (odd): one scale/bias load per step
+    (300, 3584, 9000, 64, O.F16, 0),    # 56 groups: one load per row, permuted
+    (300, 2048, 8193, 64, O.BF16, 1),   # scales/biases 2-byte aligned only
+    (300, 8192, 8500, 128, O.BF16, 0),  # 16 steps a row, permuted
+])
+def test_qembed_row_load_forms(dev, V, Hd, n, group, sdt, offset):
+    """Both ways of loading a row's scales and biases (one 32-bit load per
+    lane plus a cross-lane permute when the row's groups fit one register and
+    are 4-byte aligned, else a 16-bit load per step), each with more ids than
+    the chip keeps waves resident, so every wave runs the pipelined loop over
+    several tokens. Bit-exact against the oracle."""
+    key = 1870 + group + Hd
+    wq = O.u32(key, (V, Hd // 8))
+    s = O.from_f32(O.uniform(key + 1, (V, Hd // group), 0.005, 0.02), sdt)
+    b = O.from_f32(O.uniform(key + 2, (V, Hd // group), -0.1, 0.1), sdt)
+    ids = O.ids(key + 3, n, V)
+    ref = O.qembed(ids, wq, s, b, sdt, group=group)
+
+    def placed(a):  # the table at an element offset inside a larger buffer
+        flat = to_dev(a.reshape(-1), sdt, dev)
+        buf = torch.zeros(flat.numel() + offset, dtype=flat.dtype, device=dev)
+        buf[offset:] = flat
+        return buf[offset:].view(a.shape)
+
+    emb = H.QuantizedEmbedding(words_dev(wq, dev), placed(s), placed(b), group_size=group)
+    got = to_host(emb.forward(to_dev(ids, O.U32, dev)))
+    assert np.array_equal(got, ref)
+
+
 # ------------------------------------------------------------------ hgk_sync
 def test_sync_waits_for_the_stream_it_names(dev):
     """hgk_sync is the only blocking entry: after it returns for a side stream,
