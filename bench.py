@@ -847,7 +847,48 @@ def kernel_times(cx, wl, graph, per_group=20, groups=5):
         if k.flops:
             per[-1]["tflops"] = k.flops / (avg * 1e-3) / 1e12
             per[-1]["frac_of_mfma_peak"] = per[-1]["tflops"] / PEAK_BF16_TFLOPS
+        elif not graph:
+            # the same bytes through a plain copy: a ratio near or above 1 means
+            # the kernel is as fast as moving its bytes can be at this size
+            cu = copy_floor(cx, k.bytes, per_group, groups)
+            per[-1]["copy_us"] = cu
+            per[-1]["copy_over_kernel"] = cu / (avg * 1e3)
     return per
+
+
+def copy_floor(cx, nbytes, per_group=20, groups=5):
+    """Average duration of a plain device-to-device copy (the runtime's blit
+    kernel, hipMemcpyAsync) of nbytes / 2, i.e. nbytes of HBM traffic: what a
+    kernel moving the same bytes costs with no arithmetic at all, launch and
+    tail included. Source/destination pairs rotate over >= 1 GB like the
+    kernels' buffer sets."""
+    torch = cx.torch
+    half = max(16, (int(nbytes) // 2 + 255) // 256 * 256)
+    npairs = max(2, math.ceil((1 << 30) / (2 * half)))
+    bufs = [(cx.empty((half,), torch.uint8), cx.empty((half,), torch.uint8))
+            for _ in range(npairs)]
+    he = HipEvents()
+    h = he.h
+    h.hipMemcpyAsync.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int, C.c_void_p]
+    st = cx.stream
+
+    def go():
+        for i in range(per_group):
+            src, dst = bufs[i % npairs]
+            if h.hipMemcpyAsync(dst.data_ptr(), src.data_ptr(), half, 3, st):  # DeviceToDevice
+                raise RuntimeError("hipMemcpyAsync failed")
+    go()
+    torch.cuda.synchronize()
+    evs = he.create(groups + 1)
+    h.hipEventRecord(evs[0], st)
+    for i in range(groups):
+        go()
+        h.hipEventRecord(evs[i + 1], st)
+    torch.cuda.synchronize()
+    d = sorted(he.elapsed_ms(evs[i], evs[i + 1]) / per_group for i in range(groups))
+    he.destroy(evs)
+    del bufs
+    return sum(d) / len(d) * 1e3
 
 
 def settle(cx, fn, seconds):
@@ -1269,8 +1310,10 @@ def main(argv=None):
             for k in r["kernels"] or []:
                 cpu = k.get("cpu")
                 cpu_txt = (f"   cpu {cpu['gbs']:.2f} GB/s ({cpu['cores']} threads)" if cpu else "")
+                cp_txt = (f"   copy of the same bytes {k['copy_us']:.2f} us"
+                          if "copy_us" in k else "")
                 print(f"[table]    {k['kernel']:<24} {k['avg_us']:9.2f} us  {k['gbs']:7.0f} GB/s "
-                      f"({k['frac_of_peak']:.1%}){cpu_txt}", file=sys.stderr, flush=True)
+                      f"({k['frac_of_peak']:.1%}){cp_txt}{cpu_txt}", file=sys.stderr, flush=True)
         os.makedirs("gpurun_out", exist_ok=True)
         with open(os.path.join("gpurun_out", "bench_table.json"), "w") as f:
             json.dump(rows, f, indent=1)

@@ -22,12 +22,19 @@
 // `embed_tokens.forward(ids)` then `input_layernorm.forward(&h)` pair of
 // transformer.rs:494 and 407.
 #include <algorithm>
+#include <cmath>
 
 #include "../../include/higgs_hip.h"
 #include "hgk_common.h"
 #include "hgk_host.h"
 
 namespace hgk {
+
+// Dequantize with dot2 products where the row's scales and biases allow it
+// (0 keeps the element-by-element form everywhere, for comparisons).
+#ifndef HGK_QEMB_DOT2
+#define HGK_QEMB_DOT2 1
+#endif
 
 struct QembArgs {
   const void* ids;
@@ -42,6 +49,7 @@ struct QembArgs {
   int group;
   float scale;
   int has_scale;
+  int fast_scale_ok;  // no output scale, or bf16/f16(scale) in [2^-20, 2^20]
   void* out;  // h (may be null in the fused form)
   int64_t os;
   int64_t hidden;
@@ -67,6 +75,81 @@ __device__ inline int64_t load_id(const QembArgs& a, int64_t t) {
 template <class S>
 __device__ inline float deq(uint32_t q, float s, float b) {
   return S::round(S::round((float)q * s) + b);
+}
+
+// The same dequantization of one packed word (8 codes, one group) from the
+// packed forms, with dot2 products: a code enters as the 16-bit number
+// K + q (K = 128 for bf16, 1024 for f16: two bit operations per pair of
+// codes), and
+//   q s         = dot2((K + q_i, K + q_i+4), (s, 0)) - K s     (exact in f32)
+//   round(q s) + b = dot2(P, (1, 0)) + b                        (P = the rounded pair)
+//   round(v) * o   = dot2(V, (o, 0)) - 0                        (o = the output scale)
+// Each product has at most 22 significant bits and each sum is exact, so
+// every value is the IEEE one before its rounding to S; the roundings are
+// the packing conversions. About half the VALU work of unpacking and
+// multiplying element by element. A dot2 also multiplies the pair's other
+// element by zero, so every intermediate must stay finite and normal: the
+// scale and bias ranges of deq_fast_ok guarantee that (bf16: 2^-100 <= |s| <
+// 2^100, b = +-0 or 2^-100 <= |b| < 2^126; f16: normal |s| < 2^12, |b| <
+// 2^11), the host admits output scales in [2^-20, 2^20] only, and a negative
+// scale beside a bias of -0 is excluded (q = 0 would give +0 where the
+// reference has -0). Rows with any other group take deq() instead.
+template <class S> struct DeqK;
+template <> struct DeqK<BF16> {
+  static constexpr uint32_t kMagic = 0x43004300u;  // bf16 128 in each half
+  static constexpr float kOff = 128.0f;
+  static constexpr uint32_t kOne = 0x3f80u;
+};
+template <> struct DeqK<F16> {
+  static constexpr uint32_t kMagic = 0x64006400u;  // f16 1024 in each half
+  static constexpr float kOff = 1024.0f;
+  static constexpr uint32_t kOne = 0x3c00u;
+};
+
+template <class S>
+__device__ inline bool deq_fast_ok(uint32_t s16, uint32_t b16) {
+  const bool neg_zero = (s16 & 0x8000u) && b16 == 0x8000u;
+  if constexpr (DeqK<S>::kOff == 128.0f) {  // bf16: exponent field e, |x| ~ 2^(e - 127)
+    const uint32_t se = (s16 >> 7) & 0xffu, be = (b16 >> 7) & 0xffu;
+    const bool s_ok = se >= 27u && se <= 226u;
+    const bool b_ok = (b16 & 0x7fffu) == 0u || (be >= 27u && be <= 252u);
+    return s_ok && b_ok && !neg_zero;
+  } else {  // f16: exponent field e, |x| ~ 2^(e - 15)
+    const uint32_t se = (s16 >> 10) & 0x1fu, be = (b16 >> 10) & 0x1fu;
+    return se >= 1u && se <= 26u && be <= 25u && !neg_zero;
+  }
+}
+
+// One word's 8 outputs, packed in S (out[k] = elements 2k, 2k + 1).
+template <class S>
+__device__ inline u32x4 deq_word_fast(uint32_t c, uint32_t s16, float sv, float bv, bool has_scale,
+                                      uint32_t o16) {
+  const uint32_t slo = s16, shi = s16 << 16, olo = o16, ohi = o16 << 16;
+  // (1, 0) and (0, 1) live in registers: given 0x00003f80 as an immediate,
+  // this compiler encodes it as the inline constant 1.0, which the hardware
+  // reads in v_dot2c_f32_bf16 as a different pair (measured: the product
+  // then took the high element)
+  uint32_t one_lo = DeqK<S>::kOne, one_hi = DeqK<S>::kOne << 16;
+  asm volatile("" : "+v"(one_lo), "+v"(one_hi));
+  const float nks = -DeqK<S>::kOff * sv;
+  float v[8];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const uint32_t q = ((c >> (4 * k)) & 0x000f000fu) | DeqK<S>::kMagic;  // codes k, k + 4
+    const uint32_t p = S::pack(dot2_16<S>(q, slo, nks), dot2_16<S>(q, shi, nks));
+    float v0 = dot2_16<S>(p, one_lo, bv), v1 = dot2_16<S>(p, one_hi, bv);
+    if (has_scale) {
+      const uint32_t w = S::pack(v0, v1);
+      v0 = dot2_16<S>(w, olo, -0.0f);
+      v1 = dot2_16<S>(w, ohi, -0.0f);
+    }
+    v[k] = v0;
+    v[k + 4] = v1;
+  }
+  u32x4 o;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) o[k] = S::pack(v[2 * k], v[2 * k + 1]);
+  return o;
 }
 
 // The loads of one token's row, issued together and kept as raw words until
@@ -116,19 +199,38 @@ struct QembRow {
     }
   }
 
-  // The scale and bias of step s's group, as f32.
-  __device__ inline void group_affine(const QembArgs& a, int s, int lane, float& sv, float& bv) const {
+  // The scale and bias of step s's group, as f32 and as their 16-bit codes.
+  __device__ inline void group_affine(const QembArgs& a, int s, int lane, float& sv, float& bv,
+                                      uint32_t& s16, uint32_t& b16) const {
     if constexpr (PERM) {
       const int w = s * 64 + lane;
       int g = (w * 8) / a.group;
       g = g < a.gpr ? g : a.gpr - 1;
       const uint32_t sw = (uint32_t)__shfl((int)sraw[0], g >> 1);
       const uint32_t bw = (uint32_t)__shfl((int)sraw[0], (a.gpr >> 1) + (g >> 1));
-      sv = (g & 1) ? S::hi(sw) : S::lo(sw);
-      bv = (g & 1) ? S::hi(bw) : S::lo(bw);
+      s16 = (g & 1) ? sw >> 16 : sw & 0xffffu;
+      b16 = (g & 1) ? bw >> 16 : bw & 0xffffu;
     } else {
-      sv = S::lo(sraw[s]);
-      bv = S::lo(braw[s]);
+      s16 = sraw[s] & 0xffffu;
+      b16 = braw[s] & 0xffffu;
+    }
+    sv = S::lo(s16);
+    bv = S::lo(b16);
+  }
+
+  // Whether every group of the row takes deq_word_fast (uniform over the
+  // wave; PERM rows only, whose lanes hold all of the row's scales and biases).
+  __device__ inline bool fast_row(const QembArgs& a, int lane) const {
+    if constexpr (PERM) {
+      const int half = a.gpr >> 1;
+      // lane l < half holds scale pair l; its biases are in lane half + l
+      const uint32_t bw = (uint32_t)__shfl((int)sraw[0], (lane < half ? lane : 0) + half);
+      bool ok = true;
+      if (lane < half)
+        ok = deq_fast_ok<S>(sraw[0] & 0xffffu, bw & 0xffffu) && deq_fast_ok<S>(sraw[0] >> 16, bw >> 16);
+      return __builtin_amdgcn_ballot_w64(!ok) == 0;
+    } else {
+      return false;
     }
   }
 };
@@ -146,18 +248,28 @@ __global__ __launch_bounds__(256) void qembed_kernel(QembArgs a) {
   int64_t t = (int64_t)blockIdx.x * wpb + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (t >= a.n) return;  // whole wave leaves together
   const float osc = S::round(a.scale);
+  const uint32_t o16 = S::pack(osc, 0.0f) & 0xffffu;
   QembRow<S, STEPS, PERM> cur, nxt;
   cur.load(a, t, lane);
   for (;;) {
     const int64_t tn = t + nw;
     const bool more = tn < a.n;
     if (more) nxt.load(a, tn, lane);
+    const bool fast = HGK_QEMB_DOT2 && a.fast_scale_ok && cur.fast_row(a, lane);
 #pragma unroll
     for (int s = 0; s < STEPS; ++s) {
       float sv, bv;
-      cur.group_affine(a, s, lane, sv, bv);  // (a permute: every lane takes part)
+      uint32_t s16, b16;
+      cur.group_affine(a, s, lane, sv, bv, s16, b16);  // (a permute: every lane takes part)
       const int w = s * 64 + lane;
       if (w >= a.wpr) continue;
+      char* op = reinterpret_cast<char*>(a.out) + (t * a.os + (int64_t)w * 8) * S::kBytes;
+      if (fast) {
+        u32x4 o = deq_word_fast<S>(cur.codes[s], s16, sv, bv, a.has_scale, o16);
+        if (!cur.valid) o = u32x4{0u, 0u, 0u, 0u};
+        __builtin_nontemporal_store(o, reinterpret_cast<u32x4*>(op));
+        continue;
+      }
       float v[8];
 #pragma unroll
       for (int nib = 0; nib < 8; ++nib) {
@@ -388,6 +500,12 @@ extern "C" int hgk_quantized_embedding(const void* ids, int ids_dtype, int64_t n
   a.ids = ids; a.ids_i32 = ids_dtype == DT_I32; a.n = n_ids; a.wq = w_q; a.sc = scales;
   a.bi = biases; a.vocab = vocab; a.wpr = (int)(hidden / 8); a.gpr = (int)(hidden / group_size);
   a.group = group_size; a.scale = out_scale; a.has_scale = out_scale != 0.0f;
+  {
+    // the output scale as the scales dtype rounds it (|x| in [2^-20, 2^20]
+    // keeps every product of the dot2 form normal)
+    const float m = std::fabs(out_scale);
+    a.fast_scale_ok = !a.has_scale || (m >= 0x1p-19f && m <= 0x1p19f);
+  }
   a.out = out; a.os = out_row_stride; a.hidden = hidden;
   const bool vec_ok = (reinterpret_cast<uintptr_t>(w_q) & 3u) == 0 && aligned16(out) &&
                       hidden % 8 == 0 && out_row_stride % 8 == 0;

@@ -7,12 +7,19 @@
 //  phase A: the block fills an LDS table of cos/sin for its tokens x dims/2
 //           frequencies (computed once per (token, frequency) and shared by all
 //           heads), rounded to the activation dtype as MLX's fallback does.
-//  phase B: a group of LPR = head_dim/(2*V) lanes owns one head row; lane j
-//           holds two 16-byte chunks: the rotation pair (j, j+R) when
-//           j < R = dims/(2*V), else the pass-through chunks (2j, 2j+1). The
-//           row is read once, optionally normalised (group shuffle reduction),
-//           rotated and written once to an arbitrary (b, l, h) layout, which
-//           folds the [B,L,H,D] -> [B,H,L,D] transpose into the store.
+//  phase B: a lane group owns one head row, in one of two layouts:
+//           - two chunks per lane (rows of >= 256 bytes, full rotation):
+//             LPR = head_dim/(2*V) lanes, lane j holds the rotation pair
+//             (j, j+R) when j < R = dims/(2*V), else the pass-through chunks
+//             (2j, 2j+1); each store instruction still covers whole lines;
+//           - one chunk per lane (rows under 256 bytes): LPR =
+//             head_dim/V lanes, lane j holds chunk j and fetches its rotation
+//             partner j ^ R from the partner lane (DPP within a 16-lane row),
+//             so every load and store instruction moves whole rows.
+//           The row is read once, optionally normalised (group shuffle
+//           reduction), rotated and written once to an arbitrary (b, l, h)
+//           layout, which folds the [B,L,H,D] -> [B,H,L,D] transpose into the
+//           store.
 //
 // Arithmetic (MLX CPU fallback of fast::rope, T = activation dtype):
 //   pos = (f32(l) + offset_b) * scale;  th = pos * inv_freq[i]
@@ -313,6 +320,167 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
   }
 }
 
+// The same chunk (16 bytes) of lane j ^ R, for aligned groups of 2R lanes.
+// R <= 8 stays inside a 16-lane row and uses DPP; R = 4 composes the
+// half-row mirror (j -> 7 - j) with a quad reversal (j -> 3 - j), which
+// together map j to j ^ 4. Wider partners go through the LDS crossbar.
+template <int R>
+__device__ inline u32x4 xor_partner(u32x4 v) {
+  u32x4 o;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int s = (int)v[k];
+    int t;
+    if constexpr (R == 1) t = __builtin_amdgcn_update_dpp(0, s, 0xB1, 0xF, 0xF, true);
+    else if constexpr (R == 2) t = __builtin_amdgcn_update_dpp(0, s, 0x4E, 0xF, 0xF, true);
+    else if constexpr (R == 4)
+      t = __builtin_amdgcn_update_dpp(
+          0, __builtin_amdgcn_update_dpp(0, s, 0x141, 0xF, 0xF, true), 0x1B, 0xF, 0xF, true);
+    else if constexpr (R == 8) t = __builtin_amdgcn_update_dpp(0, s, 0x128, 0xF, 0xF, true);
+    else t = __shfl_xor(s, R, 64);
+    o[k] = (uint32_t)t;
+  }
+  return o;
+}
+
+#ifndef HGK_ROPE_LRB
+#define HGK_ROPE_LRB 8
+#endif
+constexpr int kRopeLaneBatch = HGK_ROPE_LRB;
+
+// One chunk per lane: a group of LPR = head_dim / V lanes owns a head row and
+// lane j holds chunk j, so each load and each store instruction moves whole
+// rows (whole 128-byte lines for rows of >= 128 bytes). The rotation partner
+// of chunk j < 2R is chunk j ^ R (R = dims / (2V), a power of two), fetched
+// from the partner lane after the optional norm. Both halves of a pair use
+// the same two rounded products: a = round(x * c), b = round(p * s), with
+// y = a - b in the first half (x = x1, p = x2) and y = a + b in the second
+// (x = x2, p = x1), which is y2 = round(x1 * s) + round(x2 * c) reordered.
+// A row's partner lanes and norm-reduction lanes all sit in its own aligned
+// group, so a group that leaves the batch early (its next row is past the
+// block's last) never feeds a cross-lane move of a group still running.
+template <class X, int LPR, int R, bool NORM, bool FAST>
+__global__ __launch_bounds__(256) void rope_lane_kernel(RopeArgs a) {
+  constexpr int V = Vec<X>::N;
+  constexpr int RB = kRopeLaneBatch;
+  constexpr int slots = 256 / LPR;
+  static_assert(2 * R <= LPR, "rotated chunks within the row");
+  extern __shared__ float smem[];
+  float* cs = smem;
+  float* sn = smem + a.tpb * a.half;
+  const uint32_t t0 = blockIdx.x * (uint32_t)a.tpb;
+  const int ntok = (int)min((uint32_t)a.tpb, a.tokens - t0);
+  const int rows = ntok * a.hsum;
+  const int slot = threadIdx.x / LPR;
+  const int j = threadIdx.x % LPR;
+  const bool rot = j < 2 * R;
+  const bool first = j < R;
+  const int f0 = (j & (R - 1)) * V;  // this lane's first frequency index
+
+  u32x4 wq{1u, 1u, 1u, 1u}, wk = wq;
+  if constexpr (NORM) {
+    if (a.t[0].nw) wq = ld16<X>(a.t[0].nw, j * V);
+    if (a.t[1].nw) wk = ld16<X>(a.t[1].nw, j * V);
+  }
+
+  const RopePair pr = rope_pair(a);
+  RopeBlock bb;
+  if constexpr (FAST) bb = rope_block<X>(a, t0);
+  u32x4 d[RB];
+  struct {
+    char* y;
+    int tk;
+    bool isk;
+  } rw[RB];
+  auto load_batch = [&](int base) {
+#pragma unroll
+    for (int k = 0; k < RB; ++k) {
+      const int r = base + k * slots;
+      const int rc = r < rows ? r : rows - 1;
+      const char* xp;
+      if constexpr (FAST) {
+        const RopeRow32 o = rope_row32(a, bb, pr.qheads, rc);
+        xp = (o.isk ? bb.x[1] : bb.x[0]) + (int64_t)o.xo * X::kBytes;
+        rw[k].y = (o.isk ? bb.y[1] : bb.y[0]) + (int64_t)o.yo * X::kBytes;
+        rw[k].tk = o.tk;
+        rw[k].isk = o.isk;
+      } else {
+        const RopeRow o = rope_row(a, pr, t0, rc);
+        xp = reinterpret_cast<const char*>(o.isk ? pr.x[1] : pr.x[0]) + o.xb * X::kBytes;
+        rw[k].y = reinterpret_cast<char*>(o.isk ? pr.y[1] : pr.y[0]) + o.yb * X::kBytes;
+        rw[k].tk = o.tk;
+        rw[k].isk = o.isk;
+      }
+      if constexpr (LPR * 16 >= 128) d[k] = ld16_nt<X>(xp, j * V);
+      else d[k] = ld16<X>(xp, j * V);
+    }
+  };
+
+  load_batch(slot);
+  fill_table<X>(a, cs, sn, t0, ntok);
+  __syncthreads();
+
+  for (int base = slot;;) {
+#pragma unroll
+    for (int k = 0; k < RB; ++k) {
+      const int r = base + k * slots;
+      if (r >= rows) break;
+      const bool isk = rw[k].isk;
+      float v[V];
+#pragma unroll
+      for (int e = 0; e < V; ++e) v[e] = elem<X>(d[k], e);
+      u32x4 own = d[k];
+      if constexpr (NORM) {
+        const bool has = isk ? (a.t[1].nw != nullptr) : (a.t[0].nw != nullptr);
+        if (has) {  // uniform across the row's lane group
+          double ss = 0.0;
+#pragma unroll
+          for (int e = 0; e < V; ++e) ss = __builtin_fma((double)v[e], (double)v[e], ss);
+          ss = group_sum<LPR>(ss);
+          const float rs = rms_scale(ss, a.inv_d, a.eps);
+          const u32x4 w = isk ? wk : wq;
+#pragma unroll
+          for (int e = 0; e < V; e += 2) {
+            float p0 = v[e] * rs, p1 = v[e + 1] * rs;
+            round2<X>(p0, p1);
+            p0 = p0 * elem<X>(w, e);
+            p1 = p1 * elem<X>(w, e + 1);
+            round2<X>(p0, p1);
+            v[e] = p0;
+            v[e + 1] = p1;
+          }
+          // the normalised values are representable in X: pack them exactly
+          if constexpr (X::kBytes == 2) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) own[q] = X::pack(v[2 * q], v[2 * q + 1]);
+          } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) own[q] = f2u(v[q]);
+          }
+        }
+      }
+      const u32x4 pt = xor_partner<R>(own);
+      if (rot) {
+        const float* cp = cs + rw[k].tk * a.half + f0;
+        const float* sp = sn + rw[k].tk * a.half + f0;
+#pragma unroll
+        for (int e = 0; e < V; e += 2) {
+          float a0 = v[e] * cp[e], a1 = v[e + 1] * cp[e + 1];
+          float b0 = elem<X>(pt, e) * sp[e], b1 = elem<X>(pt, e + 1) * sp[e + 1];
+          round2<X>(a0, a1);
+          round2<X>(b0, b1);
+          v[e] = first ? a0 - b0 : a0 + b0;
+          v[e + 1] = first ? a1 - b1 : a1 + b1;
+        }
+      }
+      store_elems<X, V>(rw[k].y, j * V, v);
+    }
+    base += slots * RB;
+    if (base >= rows) break;
+    load_batch(base);
+  }
+}
+
 // Fallback for any head_dim / dims / alignment: one wave per (token, head).
 template <class X, bool NORM>
 __global__ __launch_bounds__(256) void rope_generic_kernel(RopeArgs a) {
@@ -412,6 +580,65 @@ void launch_fast(RopeArgs& a, hipStream_t s) {
     hipLaunchKernelGGL((rope_kernel<X, LPR, NORM, false>), dim3(blocks), dim3(256), shmem, s, a);
 }
 
+template <class X, int LPR, int R, bool NORM>
+void launch_lane(RopeArgs& a, hipStream_t s) {
+  const int slots = 256 / LPR;
+  int tpb = std::max(1, std::min((slots * kRopeLaneBatch) / a.hsum, kMaxTpb));
+  while (tpb > 1 && (a.tokens + tpb - 1) / tpb < 1024u) --tpb;
+  if (HGK_ROPE_TPB > 0) tpb = std::min(HGK_ROPE_TPB, kMaxTpb);
+  a.tpb = tpb;
+  a.hsum_magic = a.hsum >= 2 ? (uint32_t)((((uint64_t)1 << 32) + a.hsum - 1) / a.hsum) : 0u;
+  const unsigned blocks = (a.tokens + tpb - 1) / tpb;
+  const size_t shmem = 2u * tpb * a.half * sizeof(float);
+  if (fast_index_ok(a))
+    hipLaunchKernelGGL((rope_lane_kernel<X, LPR, R, NORM, true>), dim3(blocks), dim3(256), shmem, s, a);
+  else
+    hipLaunchKernelGGL((rope_lane_kernel<X, LPR, R, NORM, false>), dim3(blocks), dim3(256), shmem, s, a);
+}
+
+template <class X, int LPR, bool NORM>
+bool launch_lane_r(RopeArgs& a, int R, hipStream_t s) {
+  switch (R) {
+    case 1: if constexpr (LPR >= 2) { launch_lane<X, LPR, 1, NORM>(a, s); return true; } break;
+    case 2: if constexpr (LPR >= 4) { launch_lane<X, LPR, 2, NORM>(a, s); return true; } break;
+    case 4: if constexpr (LPR >= 8) { launch_lane<X, LPR, 4, NORM>(a, s); return true; } break;
+    case 8: if constexpr (LPR >= 16) { launch_lane<X, LPR, 8, NORM>(a, s); return true; } break;
+    case 16: if constexpr (LPR >= 32) { launch_lane<X, LPR, 16, NORM>(a, s); return true; } break;
+    case 32: if constexpr (LPR >= 64) { launch_lane<X, LPR, 32, NORM>(a, s); return true; } break;
+    default: break;
+  }
+  return false;
+}
+
+// Which layout runs a vectorisable shape: one chunk per lane (whole-row
+// loads and stores, a cross-lane move for the rotation partner) when the
+// two-chunk layout's store instructions would cover less than a 128-byte line
+// per row (rows under 256 bytes: at head_dim 64 in bf16 the two-chunk layout
+// wrote 1.21x the output bytes to HBM, the one-chunk layout exactly 1.00x);
+// else two chunks per lane, which needs no cross-lane move (at head_dim 128
+// and 256 it measured 15 % and 9 % faster, and at the 64-sequence partial
+// rotation of head_dim 256 also faster). HGK_ROPE_LANE = 0 / 2 forces the
+// two-chunk / one-chunk layout wherever it applies (the one-chunk layout
+// only for rows of up to 8 lanes).
+#ifndef HGK_ROPE_LANE
+#define HGK_ROPE_LANE 1
+#endif
+
+template <class X, bool NORM>
+bool try_lane(RopeArgs& a, hipStream_t s) {
+  constexpr int V = Vec<X>::N;
+  const int lpr = a.D / V;
+  const int R = a.dims / (2 * V);
+  const bool narrow = a.D * X::kBytes < 256;
+  if (HGK_ROPE_LANE == 0 || (HGK_ROPE_LANE == 1 && !narrow)) return false;
+  switch (lpr) {  // rows under 256 bytes: at most 8 lanes
+    case 2: return launch_lane_r<X, 2, NORM>(a, R, s);
+    case 4: return launch_lane_r<X, 4, NORM>(a, R, s);
+    case 8: return launch_lane_r<X, 8, NORM>(a, R, s);
+    default: return false;
+  }
+}
+
 template <class X, bool NORM>
 void launch_x(RopeArgs& a, bool vec_ok, hipStream_t s) {
   constexpr int V = Vec<X>::N;
@@ -419,6 +646,7 @@ void launch_x(RopeArgs& a, bool vec_ok, hipStream_t s) {
   const int lpr = a.D / (2 * V);
   if (vec_ok && shape_ok) {
     a.R = a.dims / (2 * V);
+    if (try_lane<X, NORM>(a, s)) return;
     switch (lpr) {
       case 2: launch_fast<X, 2, NORM>(a, s); return;
       case 4: launch_fast<X, 4, NORM>(a, s); return;

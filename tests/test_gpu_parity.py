@@ -218,6 +218,40 @@ def test_qk_norm_rope_f32(dev):
     _check_rope(gk, rk, O.F32, "qk-norm-rope f32 k")
 
 
+# Shapes that take the one-chunk-per-lane layout (rows under 256 bytes), over
+# every partner distance R = dims / (2 * chunk) it meets (1, 2, 4), each
+# dtype, full and partial rotation, with and without the fused norm; ragged
+# sequences (L 37) and per-sequence offsets.
+LANE_CASES = [
+    # D, dims, dtype, norm
+    (16, 16, O.BF16, False),   # R 1, 2 lanes per row
+    (32, 32, O.BF16, True),    # R 2, 4 lanes
+    (64, 64, O.F16, True),     # R 4, 8 lanes
+    (64, 32, O.BF16, True),    # partial: R 2 of 8 lanes
+    (64, 16, O.F16, False),    # partial: R 1 of 8 lanes
+    (32, 32, O.F32, False),    # f32 rows of 128 bytes: R 4
+    (32, 16, O.F32, True),     # partial f32: R 2 of 8 lanes
+    (8, 8, O.F32, True),       # f32: R 1, 2 lanes
+]
+
+
+@pytest.mark.parametrize("case", LANE_CASES, ids=lambda c: f"D{c[0]}-dims{c[1]}-dt{c[2]}-n{int(c[3])}")
+def test_rope_one_chunk_per_lane_layouts(dev, case):
+    D, dims, dt, norm = case
+    offs = O.offsets(1450 + D + dims, 3, 0, 5000)
+    if norm:
+        (gq, rq), (gk, rk) = _qk_case(dev, B=3, L=37, Hq=5, Hk=3, D=D, dims=dims, base=1e4,
+                                      eps=1e-6, dt=dt, offsets=offs, key=1460 + D + dims)
+        _check_rope(gq, rq, dt, f"lane layout {case} q")
+        _check_rope(gk, rk, dt, f"lane layout {case} k")
+    else:
+        got, ref, _ = _rope_case(dev, B=3, L=37, Hq=5, D=D, dims=dims, base=1e4, dt=dt,
+                                 offsets=offs, layout="BLHD", key=1470 + D + dims)
+        _check_rope(got, ref, dt, f"lane layout {case}")
+        if dims < D:  # the pass-through dims are copied bit-exactly
+            assert np.array_equal(got[..., dims:], ref[..., dims:])
+
+
 # ------------------------------------------------------------------ GLU
 @pytest.mark.parametrize("dt", [O.BF16, O.F16, O.F32])
 def test_swiglu_bitexact(dev, dt):
@@ -417,6 +451,60 @@ def test_qembed_row_load_forms(dev, V, Hd, n, group, sdt, offset):
     emb = H.QuantizedEmbedding(words_dev(wq, dev), placed(s), placed(b), group_size=group)
     got = to_host(emb.forward(to_dev(ids, O.U32, dev)))
     assert np.array_equal(got, ref)
+
+
+def _bits16(key, shape, sdt, exp_lo, exp_hi, zero_frac=0.0):
+    """Random 16-bit float codes of `sdt` with a random sign and mantissa and an
+    exponent field uniform in [exp_lo, exp_hi]; a fraction of them +-0."""
+    mbits = 7 if sdt == O.BF16 else 10
+    r = O.u32(key, shape)
+    sign = (r >> np.uint32(31)) & np.uint32(1)
+    mant = r & np.uint32((1 << mbits) - 1)
+    ex = np.uint32(exp_lo) + (O.u32(key + 1, shape) % np.uint32(exp_hi - exp_lo + 1))
+    out = ((sign << np.uint32(15)) | (ex << np.uint32(mbits)) | mant).astype(np.uint16)
+    if zero_frac:
+        z = (O.u32(key + 2, shape) % np.uint32(1000)) < np.uint32(zero_frac * 1000)
+        out[z] &= np.uint16(0x8000)
+    return out
+
+
+@pytest.mark.parametrize("sdt", [O.BF16, O.F16])
+@pytest.mark.parametrize("out_scale", [0.0, math.sqrt(3584.0)])
+def test_qembed_any_scale_and_bias_values(dev, sdt, out_scale):
+    """Rows whose scales and biases span every exponent the dot2 form takes
+    (bf16: scales of either sign from 2^-100 to 2^100, biases +-0 or from
+    2^-100 to 2^126, so that round(q s) + b is often inexact in f32; f16:
+    normal scales below 2^12, biases below 2^11), rows of arbitrary 16-bit
+    codes (zeros, subnormals, huge values, inf, NaN: those rows take the
+    element-by-element form and overflow) and ordinary rows, with and without
+    the output scale. Bit-exact against the oracle (NaN positions compared as
+    a mask)."""
+    V, Hd, n = 1536, 2048, 3000
+    G = Hd // 64
+    key = 1950 + 10 * sdt + int(out_scale > 0)
+    wq = O.u32(key, (V, Hd // 8))
+    s = O.from_f32(O.uniform(key + 1, (V, G), 0.005, 0.02), sdt)
+    b = O.from_f32(O.uniform(key + 2, (V, G), -0.1, 0.1), sdt)
+    bf = sdt == O.BF16
+    wide_s = _bits16(key + 3, (V, G), sdt, 27 if bf else 1, 226 if bf else 26)
+    wide_b = _bits16(key + 6, (V, G), sdt, 27 if bf else 0, 252 if bf else 25, zero_frac=0.05)
+    any_s = (O.u32(key + 9, (V, G)) & np.uint32(0xffff)).astype(np.uint16)
+    any_b = (O.u32(key + 10, (V, G)) & np.uint32(0xffff)).astype(np.uint16)
+    rows = np.arange(V)
+    s[rows % 3 == 1] = wide_s[rows % 3 == 1]
+    b[rows % 3 == 1] = wide_b[rows % 3 == 1]
+    s[rows % 3 == 2] = any_s[rows % 3 == 2]
+    b[rows % 3 == 2] = any_b[rows % 3 == 2]
+    # a negative scale beside a -0 bias (q = 0 must give -0), and a +0 bias
+    s[4, :] = s[4, :] | np.uint16(0x8000)
+    b[4, :] = np.uint16(0x8000)
+    b[7, :] = np.uint16(0x0000)
+    ids = O.ids(key + 11, n, V)
+    ids[:4] = np.array([4, 7, 1, 2], ids.dtype)
+    ref = O.qembed(ids, wq, s, b, sdt, out_scale=out_scale)
+    emb = H.QuantizedEmbedding(words_dev(wq, dev), to_dev(s, sdt, dev), to_dev(b, sdt, dev))
+    got = to_host(emb.forward(to_dev(ids, O.U32, dev), out_scale=out_scale))
+    _same_bits_nan_aware(got, ref, sdt)
 
 
 # ------------------------------------------------------------------ hgk_sync
