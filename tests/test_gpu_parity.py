@@ -453,6 +453,25 @@ def test_qembed_row_load_forms(dev, V, Hd, n, group, sdt, offset):
     assert np.array_equal(got, ref)
 
 
+def test_qembed_more_than_64_tokens_per_wave(dev):
+    """600,000 ids: more than 64 per resident wave (8192 waves on an MI355X),
+    so every persistent wave runs a long pipelined loop over its tokens; int32
+    ids with negative (from the end) and out-of-range values. Bit-exact."""
+    V, Hd, n = 1000, 256, 600000
+    key = 1940
+    wq = O.u32(key, (V, Hd // 8))
+    s = O.from_f32(O.uniform(key + 1, (V, Hd // 64), 0.005, 0.02), O.BF16)
+    b = O.from_f32(O.uniform(key + 2, (V, Hd // 64), -0.1, 0.1), O.BF16)
+    ids = O.ids(key + 3, n, V).astype(np.int32)
+    ids[::997] = -3
+    ids[5::1009] = V + 2
+    ref = O.qembed(ids, wq, s, b, O.BF16)
+    emb = H.QuantizedEmbedding(words_dev(wq, dev), to_dev(s, O.BF16, dev), to_dev(b, O.BF16, dev))
+    got = to_host(emb.forward(to_dev(ids, O.I32, dev)))
+    assert np.array_equal(got, ref)
+    assert not got[5].any() and got[0].any()
+
+
 def _bits16(key, shape, sdt, exp_lo, exp_hi, zero_frac=0.0):
     """Random 16-bit float codes of `sdt` with a random sign and mantissa and an
     exponent field uniform in [exp_lo, exp_hi]; a fraction of them +-0."""

@@ -86,6 +86,23 @@ def test_routing_lhs_and_out_of_range(dev):
     assert not got[2].any() and not got[4].any() and got[9].any()
 
 
+@pytest.mark.parametrize("K,x_div", [(512, 1), (1024, 3), (4096, 2)])
+def test_decode_pairs_skewed_over_experts(dev, K, x_div):
+    """Decode-sized pair counts (fewer than 16 per expert on average, so the
+    per-pair kernel) with one expert holding 1500 of the 4000 pairs and the
+    rest 0-8; a ragged N (200); an expert id out of range (zero row) and one
+    that wraps (-1); K 512, 1024 and 4096 with x rows shared by 1-3 pairs."""
+    P, E, N = 4000, 512, 200
+    x, w, s, b, ex = _case(2440 + K, P, (P + x_div - 1) // x_div, E, N, K)
+    ex = ex.copy()
+    ex[100:1600] = 3
+    ex[[5, 6]] = [E + 7, -1]
+    got = _run(dev, x, w, s, b, ex, O.BF16, x_div=x_div)
+    ref = O.gather_qmm(x, O.BF16, w, s, b, O.BF16, ex, x_div=x_div)
+    _check(got, ref, O.BF16, f"skewed decode K={K}")
+    assert not got[5].any() and got[6].any()
+
+
 def test_swiglu_expert_block_end_to_end(dev):
     """forward_gather's whole expert block: gate and up gather_qmm, SwiGLU,
     down gather_qmm (qwen3_next.rs:868-904), against the oracle chain."""
