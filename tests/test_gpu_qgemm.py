@@ -52,6 +52,19 @@ def test_mfma_path_matches_oracle(dev, M, N, K):
     _check(got, ref, O.BF16, f"M={M} N={N} K={K}")
 
 
+@pytest.mark.parametrize("M,N", [(64, 12288), (40, 12288), (64, 12400)],
+                         ids=["in_proj_qkvz", "rows40", "ragged-tiles"])
+def test_decode_wide_projection(dev, M, N):
+    """The decode step of a batch through in_proj_qkvz (2048 -> 12288), the
+    launch geometry bench.py times, plus a partly filled second row half and
+    a column count that leaves the last column tile ragged."""
+    K = 2048
+    x, w, s, b = _case(3701 + M + N, M, N, K)
+    got = _run(dev, x, w, s, b, O.BF16)
+    ref = O.quantized_matmul(x, O.BF16, w, s, b, O.BF16)
+    _check(got, ref, O.BF16, f"decode M={M} N={N} K={K}")
+
+
 def test_qwen3_next_prefill_projection(dev):
     """A 2048-token prefill through a 2048 -> 4096 projection (the attention
     q projection's shape class)."""
