@@ -59,6 +59,40 @@ __device__ inline bf16x8_t expand_codes(uint32_t c) {
   return __builtin_bit_cast(bf16x8_t, v);
 }
 
+// 8 codes of one word -> the bf16 numbers 128 + q in the order (q0, q4),
+// (q1, q5), (q2, q6), (q3, q7): for x stored in the same order, each pair is
+// one shift and one and-or (7 operations per word against 11 above).
+// The two masks are passed in registers (x4_masks): a three-operand and-or
+// takes no literal on this target, and with literals the compiler splits it
+// into a separate and and or.
+struct X4Masks {
+  uint32_t nib, one;  // 0x000f000f, 0x43004300
+};
+__device__ inline X4Masks x4_masks() {
+  X4Masks m{0x000f000fu, 0x43004300u};
+  asm volatile("" : "+v"(m.nib), "+v"(m.one));
+  return m;
+}
+__device__ inline bf16x8_t expand_codes_x4(uint32_t c, X4Masks m) {
+  u32x4 v;
+  v[0] = (c & m.nib) | m.one;
+  v[1] = ((c >> 4) & m.nib) | m.one;
+  v[2] = ((c >> 8) & m.nib) | m.one;
+  v[3] = ((c >> 12) & m.nib) | m.one;
+  return __builtin_bit_cast(bf16x8_t, v);
+}
+
+// A 16-byte piece of 8 bf16 values (x0 .. x7) reordered to (x0, x4),
+// (x1, x5), (x2, x6), (x3, x7), the order expand_codes_x4 gives the codes.
+__device__ inline u32x4 order_x4(u32x4 w) {
+  u32x4 v;
+  v[0] = __builtin_amdgcn_perm(w[2], w[0], 0x05040100u);
+  v[1] = __builtin_amdgcn_perm(w[2], w[0], 0x07060302u);
+  v[2] = __builtin_amdgcn_perm(w[3], w[1], 0x05040100u);
+  v[3] = __builtin_amdgcn_perm(w[3], w[1], 0x07060302u);
+  return v;
+}
+
 typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
 
 __device__ inline float dot2_ones(uint32_t w, float c) {
@@ -924,6 +958,314 @@ __global__ __launch_bounds__(WAVES * 64) void gather_hl_kernel(GatherArgs a) {
   }
 }
 
+// ---------------------------------------------------------------- grouped, exact
+// The prefill form of gather_qmm with no weight plane in LDS. A block is one
+// expert and 8 waves side by side over 512 columns (64 each, 4 column tiles);
+// its rows are the expert's listed pairs, up to 16 RT per pass. Per group a
+// wave loads its codes straight into B-operand registers, one 8-byte buffer
+// load per column tile (lane group j supplies code words 2j and 2j + 1, i.e.
+// k = 16 j .. 16 j + 15 of the group), and expands each word to the bf16
+// numbers 128 + q in the order (q0, q4), (q1, q5), (q2, q6), (q3, q7), which
+// x is stored in as well (7 operations per word). The MFMAs C = x . (128 + q)
+// are exact products summed in f32, with acc += s C per group from four
+// independent MFMA chains (one per column tile). The bias term
+// sum_g (b - 128 s)[n, g] Sx_g[m] is one f32 MFMA (16 x 16 x 4) per tile and
+// 4 groups. LDS holds x (double-buffered, one barrier per group), its
+// per-group row sums, the block's scales and biases (8 groups at a time,
+// double-buffered) and the pair list. Global loads are buffer loads at fixed
+// per-lane offsets; a row past the pass's last reads zeros through an
+// out-of-range offset, so the load sequence is the same on every path.
+// Measured at a 4096-token Qwen3-Next MoE prefill (40,960 pairs, top-10 of
+// 512): gate 234 us against 342 for the hi/lo kernel, down 280 against 414.
+// Non-temporal x loads, requesting all scan rounds' ids at once, and issuing
+// the next pass's first loads before a pass's stores all measured slower.
+constexpr int kXpWaves = 8, kXpT = 64 * kXpWaves;
+constexpr int kXpBN = 64 * kXpWaves;  // columns per block pass
+
+template <int RT>
+__global__ __launch_bounds__(kXpT) void gather_xp_kernel(GatherArgs a) {
+  constexpr int BM = 16 * RT, NT = 4;
+  constexpr int XP = (BM * 8 + kXpT - 1) / kXpT;  // 16-byte x pieces per thread per group
+  constexpr int RND = kGaRoundIds / kXpT;  // ids per thread per scan round
+  __shared__ __align__(16) uint16_t xs[2][BM][kQgPitch];
+  __shared__ float sxs[8][BM];              // row sums, ring of 8 groups
+  // scales and biases of 8 groups per column (double-buffered per 8 groups)
+  __shared__ __align__(16) u32x4 ssb[2][kXpBN], bsb[2][kXpBN];
+  __shared__ int32_t list[kGaCap];
+  __shared__ int32_t cnt;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int64_t e = blockIdx.y;
+  const int ntiles = (int)((a.N + kXpBN - 1) / kXpBN);
+  const int tpg = (ntiles + (int)gridDim.x - 1) / (int)gridDim.x;
+  const int nt0 = (int)blockIdx.x * tpg, nt1 = nt0 + tpg < ntiles ? nt0 + tpg : ntiles;
+  const int G = (int)(a.K / 64);
+
+  if (e == a.E) {
+    // pairs whose expert is out of range: zero rows (this block's columns)
+    const int64_t c0 = (int64_t)nt0 * kXpBN, c1 = (int64_t)nt1 * kXpBN < a.N ? (int64_t)nt1 * kXpBN : a.N;
+    for (int64_t p0 = 0; p0 < a.pairs; p0 += kXpT) {
+      const int64_t p = p0 + tid;
+      const int64_t ep = p < a.pairs ? ga_expert(a, p) : 0;
+      if (p < a.pairs && (ep < 0 || ep >= a.E))
+        for (int64_t c = c0; c < c1; ++c) a.y[p * a.ys + c] = 0;
+    }
+    return;
+  }
+
+  auto id_of = [&](uint32_t raw) -> int64_t {
+    if (a.experts_i32) {
+      const int64_t v = (int32_t)raw;
+      return v < 0 ? v + a.E : v;
+    }
+    return (int64_t)raw;
+  };
+  static_assert(RND % 4 == 0, "whole 16-byte id loads");
+  const __amdgpu_buffer_rsrc_t rid = buf_rsrc(a.experts, (uint32_t)(a.pairs * 4));
+  // one round's ids, kept raw; the next round's are requested before the
+  // current round is compared, so the scan pays the load latency once
+  uint32_t cur[RND], nxt[RND];
+  auto load_round = [&](uint32_t (&r)[RND], int64_t base) {
+    const bool live = base < a.pairs;
+#pragma unroll
+    for (int c = 0; c < RND / 4; ++c) {
+      const uint32_t off = live ? (uint32_t)((base + RND * tid + 4 * c) * 4) : 0x80000000u;
+      const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rid, off, 0, 0));
+#pragma unroll
+      for (int k = 0; k < 4; ++k) r[4 * c + k] = v[k];
+    }
+  };
+
+  const uint32_t xbytes = (uint32_t)(((a.xrows - 1) * a.xs + a.K) * 2);
+  const __amdgpu_buffer_rsrc_t rx = buf_rsrc(a.x, xbytes);
+  const __amdgpu_buffer_rsrc_t rw = buf_rsrc(a.w, (uint32_t)(a.E * a.N * a.K / 2));
+  const __amdgpu_buffer_rsrc_t rs = buf_rsrc(a.sc, (uint32_t)(a.E * a.N * G * 2));
+  const __amdgpu_buffer_rsrc_t rb = buf_rsrc(a.bi, (uint32_t)(a.E * a.N * G * 2));
+  const int C8 = G / 8;
+
+  // ---- per-pass addressing and loads (a pass: column chunk nt, rows t0 .. t0 + rp)
+  uint32_t wo[NT], so, xo[XP];
+  // this lane's columns of chunk nt: codes (words 2 lg, 2 lg + 1 of each
+  // group); this thread's column of the block's scale/bias staging
+  auto set_cols = [&](int nt) {
+    const int64_t n0 = (int64_t)nt * kXpBN + 64 * wave;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const int64_t n = n0 + 16 * t + l16;
+      const int64_t nc = n < a.N ? n : a.N - 1;
+      wo[t] = (uint32_t)((e * a.N + nc) * (a.K / 2)) + 8u * lg;
+    }
+    const int64_t sn = (int64_t)nt * kXpBN + tid;
+    so = (uint32_t)((e * a.N + (sn < a.N ? sn : a.N - 1)) * G * 2);
+  };
+  // this thread's x pieces: piece c = tid + 512 i is row c / 8, bytes 16 (c % 8)
+  // of the group's 128 (out of range past the pass's rows)
+  auto set_rows = [&](int t0, int rp) {
+#pragma unroll
+    for (int i = 0; i < XP; ++i) {
+      const int c = tid + kXpT * i, r = c / 8;
+      const int64_t xr = r < rp && c < BM * 8 ? ga_row(a, list[t0 + r]) : -1;
+      xo[i] = xr >= 0 ? (uint32_t)(xr * a.xs * 2) + 16u * (c & 7) : 0x80000000u;
+    }
+  };
+  u32x2_t cw[2][NT];   // codes of two groups in flight
+  u32x4 cx[2][XP];     // x pieces of two groups in flight
+  u32x4 sreg, breg;    // scales and biases of 8 groups of this thread's column
+  auto fetch_w = [&](u32x2_t (&q)[NT], int g) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+      q[t] = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(rw, wo[t], g * 32, 0));
+    asm volatile("" ::: "memory");
+  };
+  auto fetch_x = [&](u32x4 (&q)[XP], int g) {
+#pragma unroll
+    for (int i = 0; i < XP; ++i)
+      q[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, xo[i], g * 128, 0));
+    asm volatile("" ::: "memory");
+  };
+  auto fetch_sb = [&](int c8) {
+    sreg = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, so, c8 * 16, 0));
+    breg = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rb, so, c8 * 16, 0));
+    asm volatile("" ::: "memory");
+  };
+  auto publish_sb = [&](int buf) {
+    ssb[buf][tid] = sreg;
+    bsb[buf][tid] = breg;
+  };
+  auto publish_x = [&](const u32x4 (&q)[XP], int g) {
+    const int buf = g & 1;
+#pragma unroll
+    for (int i = 0; i < XP; ++i) {
+      const int c = tid + kXpT * i;
+      if (c < BM * 8) {  // whole waves (BM * 8 is a multiple of 64)
+        *reinterpret_cast<u32x4*>(&xs[buf][c / 8][(c & 7) * 8]) = order_x4(q[i]);
+        const float s8 = sum8_lanes(sum8_bf16(q[i]));
+        if ((c & 7) == 0) sxs[g & 7][c / 8] = s8;
+      }
+    }
+  };
+  // element j (0..7) of a column's staged scales or biases
+  auto stage_elem = [&](const u32x4 (&st)[kXpBN], int col, int j) {
+    const uint16_t* p = reinterpret_cast<const uint16_t*>(&st[col]);
+    return BF16::lo((uint32_t)p[j]);
+  };
+  const X4Masks xm = x4_masks();
+
+  int64_t scan = 0;
+  while (scan < a.pairs) {
+    // ---- list this expert's pairs from `scan` (kGaRoundIds ids per round)
+    load_round(cur, scan);
+    __syncthreads();
+    if (tid == 0) cnt = 0;
+    __syncthreads();
+    while (scan < a.pairs) {
+      if (cnt > kGaCap - kGaRoundIds) break;  // uniform: read after the round's barrier
+      load_round(nxt, scan + kGaRoundIds);
+#pragma unroll
+      for (int i = 0; i < RND; ++i) {
+        const int64_t p = scan + RND * tid + i;
+        const bool m = p < a.pairs && id_of(cur[i]) == e;
+        const uint64_t mask = __ballot(m);
+        if (mask) {  // uniform per wave
+          int base = 0;
+          if (lane == 0) base = atomicAdd(&cnt, __popcll(mask));
+          base = __shfl(base, 0, 64);
+          if (m) list[base + __popcll(mask & ((1ull << lane) - 1ull))] = (int32_t)p;
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < RND; ++i) cur[i] = nxt[i];
+      scan += kGaRoundIds;
+      __syncthreads();
+    }
+    const int rows = cnt;
+
+    for (int nt = nt0; nt < nt1; ++nt)
+    for (int t0 = 0; t0 < rows; t0 += BM) {
+      const int rp = rows - t0 < BM ? rows - t0 : BM;  // rows of this pass
+      const int rt = (rp + 15) >> 4;                   // live row tiles
+      const int64_t n0 = (int64_t)nt * kXpBN + 64 * wave;
+      set_cols(nt);
+      set_rows(t0, rp);
+      fetch_sb(0);
+      fetch_x(cx[0], 0);
+      fetch_w(cw[0], 0);
+      fetch_x(cx[1], 1);
+      fetch_w(cw[1], 1);
+
+      f32x4_t acc[RT][NT];
+#pragma unroll
+      for (int i = 0; i < RT; ++i)
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[i][t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+      // group g: its codes in cw[g & 1], its scales in stage (g / 8) & 1
+      auto compute = [&](const u32x2_t (&q)[NT], int g) {
+        const int sb = (g >> 3) & 1, j = g & 7;
+        bf16x8_t bw[NT][2];
+        float sc[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          uint32_t w0 = q[t][0], w1 = q[t][1];
+          asm volatile("" : "+v"(w0), "+v"(w1));
+          bw[t][0] = expand_codes_x4(w0, xm);
+          bw[t][1] = expand_codes_x4(w1, xm);
+          sc[t] = stage_elem(ssb[sb], 64 * wave + 16 * t + l16, j);
+        }
+        const int buf = g & 1;
+#pragma unroll
+        for (int i = 0; i < RT; ++i) {
+          if (i < rt) {  // uniform
+            const bf16x8_t a0 = *reinterpret_cast<const bf16x8_t*>(&xs[buf][i * 16 + l16][(2 * lg) * 8]);
+            const bf16x8_t a1 = *reinterpret_cast<const bf16x8_t*>(&xs[buf][i * 16 + l16][(2 * lg + 1) * 8]);
+            // four independent chains (one per column tile), then their epilogues
+            f32x4_t c[NT];
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+              c[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, bw[t][0], f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+              c[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, bw[t][1], c[t], 0, 0, 0);
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+              for (int r = 0; r < 4; ++r) acc[i][t][r] = __builtin_fmaf(sc[t], c[t][r], acc[i][t][r]);
+            // the row tile's update completes here (otherwise every MFMA
+            // result of the group is held at once)
+#pragma unroll
+            for (int t = 0; t < NT; ++t) asm volatile("" : "+v"(acc[i][t]));
+          }
+        }
+      };
+      // bias term of groups g4 .. g4 + 3 (g4 % 4 == 0): lane (l16, lg)
+      // supplies Sx of row l16 and (b - 128 s) of column l16 for group g4 + lg
+      auto bias = [&](int g4) {
+        const int sb = (g4 >> 3) & 1, j = (g4 & 7) + lg;
+        float bsel[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          const int col = 64 * wave + 16 * t + l16;
+          bsel[t] = stage_elem(bsb[sb], col, j) - 128.0f * stage_elem(ssb[sb], col, j);
+        }
+#pragma unroll
+        for (int i = 0; i < RT; ++i) {
+          if (i < rt) {
+            const float asel = sxs[(g4 + lg) & 7][i * 16 + l16];
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+              acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x4f32(asel, bsel[t], acc[i][t], 0, 0, 0);
+          }
+        }
+      };
+
+      __syncthreads();  // the previous pass's LDS readers are done
+      publish_sb(0);
+      fetch_sb(1 < C8 ? 1 : 0);
+      publish_x(cx[0], 0);
+      // two groups per unrolled body (G is a multiple of 8): the slots are
+      // fixed registers; every fetch is unconditional (past the last group
+      // it re-reads the last)
+      for (int g0 = 0; g0 < G; g0 += 2) {
+#pragma unroll
+        for (int d = 0; d < 2; ++d) {
+          const int g = g0 + d;
+          __syncthreads();  // group g's x and scales are in LDS; group g - 1's readers are done
+          compute(cw[d], g);
+          if ((g & 3) == 3) bias(g - 3);  // uniform
+          if ((g & 7) == 7) {
+            // the next 8 groups' scales go to the other stage (its readers,
+            // 8 groups back, are done); the 8 after that are requested
+            publish_sb(((g >> 3) + 1) & 1);
+            const int c2 = (g >> 3) + 2;
+            fetch_sb(c2 < C8 ? c2 : C8 - 1);
+          }
+          if (g + 1 < G) publish_x(cx[d ^ 1], g + 1);
+          fetch_x(cx[d], g + 2 < G ? g + 2 : G - 1);
+          fetch_w(cw[d], g + 2 < G ? g + 2 : G - 1);
+        }
+      }
+
+#pragma unroll
+      for (int i = 0; i < RT; ++i) {
+        if (i >= rt) continue;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int lr = i * 16 + 4 * lg + r;
+          if (lr >= rp) continue;
+          const int64_t p = list[t0 + lr];
+#pragma unroll
+          for (int t = 0; t < NT; ++t) {
+            const int64_t n = n0 + 16 * t + l16;
+            if (n < a.N) a.y[p * a.ys + n] = (uint16_t)(BF16::pack(acc[i][t][r], 0.0f) & 0xffffu);
+          }
+        }
+      }
+    }
+  }
+}
+
 bool gather_grouped_supported(int dtype, int sdt, int group_size, int bits, const void* x,
                               int64_t xs, const void* w, int64_t k, const void* experts,
                               int64_t pairs) {
@@ -934,7 +1276,36 @@ bool gather_grouped_supported(int dtype, int sdt, int group_size, int bits, cons
          pairs * 4 < ((int64_t)1 << 31);
 }
 
+#ifndef HGK_GATHER_XP
+#define HGK_GATHER_XP 1
+#endif
+#ifndef HGK_XP_RT
+#define HGK_XP_RT 6
+#endif
+
+// The exact-product grouped kernel takes K in units of 8 groups and addresses
+// x, the codes, scales and biases with 32-bit buffer offsets.
+bool gather_xp_fits(const GatherArgs& a) {
+  const int64_t lim = (int64_t)1 << 31;
+  return a.K % 512 == 0 && ((a.xrows - 1) * a.xs + a.K) * 2 < lim && a.E * a.N * a.K / 2 < lim &&
+         a.E * a.N * (a.K / 64) * 2 < lim;
+}
+
+void gather_xp_launch(const GatherArgs& a, hipStream_t s) {
+  const int64_t ntiles = (a.N + kXpBN - 1) / kXpBN;
+  int64_t gx = 1024 / (a.E + 1);
+  gx = gx < 1 ? 1 : (gx > ntiles ? ntiles : gx);
+  const int64_t tpg = (ntiles + gx - 1) / gx;
+  gx = (ntiles + tpg - 1) / tpg;
+  const dim3 grid((unsigned)gx, (unsigned)(a.E + 1));
+  hipLaunchKernelGGL((gather_xp_kernel<HGK_XP_RT>), grid, dim3(kXpT), 0, s, a);
+}
+
 void gather_grouped_launch(const GatherArgs& a, hipStream_t s) {
+  if (HGK_GATHER_XP && gather_xp_fits(a)) {
+    gather_xp_launch(a, s);
+    return;
+  }
   // column tiles are split over as many blocks as keep about 1024 blocks in
   // the grid; each block scans the expert ids once for all of its tiles
   // (2048, 4096 and 8192 measured slower: 12-40% more time at 512 experts,
@@ -949,6 +1320,7 @@ void gather_grouped_launch(const GatherArgs& a, hipStream_t s) {
   // 8 waves (2 per SIMD) measured 1.44x faster than 4 waves of 64 x 64 tiles
   hipLaunchKernelGGL((gather_hl_kernel<8>), grid, dim3(512), 0, s, a);
 }
+
 
 template <int MT>
 void decode_launch_mt(const QgemmArgs& a, int nt, hipStream_t s) {

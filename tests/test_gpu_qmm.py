@@ -175,6 +175,46 @@ def test_grouped_prefill_path_matches_oracle(dev):
     _check(got, ref, O.BF16, "grouped down")
 
 
+@pytest.mark.parametrize("proj", ["gate_up", "down"])
+def test_grouped_prefill_qwen3_next_shape(dev, proj):
+    """The 4096-token Qwen3-Next MoE prefill bench.py times: top-10 of 512
+    experts (40,960 pairs, ~80 per expert), gate/up 2048 -> 512 with x row =
+    pair // 10, down 512 -> 2048 with one x row per pair. The whole call runs
+    on the GPU; the oracle checks two blocks of 1024 pairs (every expert's
+    list holds pairs from all over the call)."""
+    T, top_k, E = 4096, 10, 512
+    N, K = (512, 2048) if proj == "gate_up" else (2048, 512)
+    P = T * top_k
+    key = 2431 if proj == "gate_up" else 2441
+    w = O.u32(key, (E, N, K // 8))
+    s = O.from_f32(O.uniform(key + 1, (E, N, K // 64), 0.005, 0.02), O.BF16)
+    b = O.from_f32(O.uniform(key + 2, (E, N, K // 64), -0.1, 0.1), O.BF16)
+    ex = (O.u32(key + 3, (P,)) % np.uint32(E)).astype(np.int32)
+    R, div = (T, top_k) if proj == "gate_up" else (P, 1)
+    x = O.from_f32(O.normal(key + 4, (R, K)), O.BF16)
+    got = _run(dev, x, w, s, b, ex, O.BF16, x_div=div)
+    for lo in (0, P - 1024):
+        sel = np.arange(lo, lo + 1024)
+        ref = O.gather_qmm(x, O.BF16, w, s, b, O.BF16, ex[sel], lhs=(sel // div).astype(np.int32))
+        _check(got[sel], ref, O.BF16, f"{proj} pairs {lo}..{lo + 1024}")
+
+
+def test_grouped_hilo_path_for_other_k(dev):
+    """Many pairs per expert with K not a multiple of 512 (9 groups): the
+    grouped call runs the hi/lo-plane kernel instead of the exact-product
+    one; gate/up style rows."""
+    T, top_k, E, N, K = 384, 8, 16, 192, 576
+    P = T * top_k
+    w = O.u32(2451, (E, N, K // 8))
+    s = O.from_f32(O.uniform(2452, (E, N, K // 64), 0.005, 0.02), O.BF16)
+    b = O.from_f32(O.uniform(2453, (E, N, K // 64), -0.1, 0.1), O.BF16)
+    ex = (O.u32(2454, (P,)) % np.uint32(E)).astype(np.int32)
+    x = O.from_f32(O.normal(2455, (T, K)), O.BF16)
+    got = _run(dev, x, w, s, b, ex, O.BF16, x_div=top_k)
+    ref = O.gather_qmm(x, O.BF16, w, s, b, O.BF16, ex, x_div=top_k)
+    _check(got, ref, O.BF16, "grouped hi/lo K=576")
+
+
 def test_grouped_path_routing_and_out_of_range(dev):
     """The grouped kernel keeps gather_qmm's routing rules: lhs rows, -1
     wrapping to the last expert, out-of-range experts and rows giving zero
