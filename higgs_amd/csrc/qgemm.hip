@@ -970,15 +970,17 @@ __global__ __launch_bounds__(WAVES * 64) void gather_hl_kernel(GatherArgs a) {
 // are exact products summed in f32, with acc += s C per group from four
 // independent MFMA chains (one per column tile). The bias term
 // sum_g (b - 128 s)[n, g] Sx_g[m] is one f32 MFMA (16 x 16 x 4) per tile and
-// 4 groups. LDS holds x (double-buffered, one barrier per group), its
-// per-group row sums, the block's scales and biases (8 groups at a time,
+// 4 groups. LDS holds x (four groups' buffers, one barrier per two groups),
+// its per-group row sums, the block's scales and biases (8 groups at a time,
 // double-buffered) and the pair list. Global loads are buffer loads at fixed
 // per-lane offsets; a row past the pass's last reads zeros through an
 // out-of-range offset, so the load sequence is the same on every path.
 // Measured at a 4096-token Qwen3-Next MoE prefill (40,960 pairs, top-10 of
-// 512): gate 234 us against 342 for the hi/lo kernel, down 280 against 414.
+// 512): gate 222 us against 342 for the hi/lo kernel, down 268 against 414
+// (one barrier per group instead of per two: 234 and 280).
 // Non-temporal x loads, requesting all scan rounds' ids at once, and issuing
 // the next pass's first loads before a pass's stores all measured slower.
+constexpr int kXpXB = 4;  // x buffers in LDS (two groups per barrier)
 constexpr int kXpWaves = 8, kXpT = 64 * kXpWaves;
 constexpr int kXpBN = 64 * kXpWaves;  // columns per block pass
 
@@ -987,7 +989,7 @@ __global__ __launch_bounds__(kXpT) void gather_xp_kernel(GatherArgs a) {
   constexpr int BM = 16 * RT, NT = 4;
   constexpr int XP = (BM * 8 + kXpT - 1) / kXpT;  // 16-byte x pieces per thread per group
   constexpr int RND = kGaRoundIds / kXpT;  // ids per thread per scan round
-  __shared__ __align__(16) uint16_t xs[2][BM][kQgPitch];
+  __shared__ __align__(16) uint16_t xs[kXpXB][BM][kQgPitch];
   __shared__ float sxs[8][BM];              // row sums, ring of 8 groups
   // scales and biases of 8 groups per column (double-buffered per 8 groups)
   __shared__ __align__(16) u32x4 ssb[2][kXpBN], bsb[2][kXpBN];
@@ -1095,7 +1097,7 @@ __global__ __launch_bounds__(kXpT) void gather_xp_kernel(GatherArgs a) {
     bsb[buf][tid] = breg;
   };
   auto publish_x = [&](const u32x4 (&q)[XP], int g) {
-    const int buf = g & 1;
+    const int buf = g & (kXpXB - 1);
 #pragma unroll
     for (int i = 0; i < XP; ++i) {
       const int c = tid + kXpT * i;
@@ -1174,7 +1176,7 @@ __global__ __launch_bounds__(kXpT) void gather_xp_kernel(GatherArgs a) {
           bw[t][1] = expand_codes_x4(w1, xm);
           sc[t] = stage_elem(ssb[sb], 64 * wave + 16 * t + l16, j);
         }
-        const int buf = g & 1;
+        const int buf = g & (kXpXB - 1);
 #pragma unroll
         for (int i = 0; i < RT; ++i) {
           if (i < rt) {  // uniform
@@ -1224,14 +1226,19 @@ __global__ __launch_bounds__(kXpT) void gather_xp_kernel(GatherArgs a) {
       publish_sb(0);
       fetch_sb(1 < C8 ? 1 : 0);
       publish_x(cx[0], 0);
+      publish_x(cx[1], 1);
+      fetch_x(cx[0], 2);
+      fetch_x(cx[1], 3);
       // two groups per unrolled body (G is a multiple of 8): the slots are
       // fixed registers; every fetch is unconditional (past the last group
       // it re-reads the last)
       for (int g0 = 0; g0 < G; g0 += 2) {
+        // x of groups g0 and g0 + 1 is in LDS; the readers of the two
+        // buffers refilled in this step (groups g0 - 2, g0 - 1) are done
+        __syncthreads();
 #pragma unroll
         for (int d = 0; d < 2; ++d) {
           const int g = g0 + d;
-          __syncthreads();  // group g's x and scales are in LDS; group g - 1's readers are done
           compute(cw[d], g);
           if ((g & 3) == 3) bias(g - 3);  // uniform
           if ((g & 7) == 7) {
@@ -1241,8 +1248,10 @@ __global__ __launch_bounds__(kXpT) void gather_xp_kernel(GatherArgs a) {
             const int c2 = (g >> 3) + 2;
             fetch_sb(c2 < C8 ? c2 : C8 - 1);
           }
-          if (g + 1 < G) publish_x(cx[d ^ 1], g + 1);
-          fetch_x(cx[d], g + 2 < G ? g + 2 : G - 1);
+          // this slot's x (group g + 2) goes to LDS and the slot is refilled
+          // with group g + 4; the codes slot, consumed above, with g + 2
+          if (g + 2 < G) publish_x(cx[d], g + 2);
+          fetch_x(cx[d], g + 4 < G ? g + 4 : G - 1);
           fetch_w(cw[d], g + 2 < G ? g + 2 : G - 1);
         }
       }
