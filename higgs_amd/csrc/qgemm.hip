@@ -728,6 +728,75 @@ __device__ inline int64_t ga_row(const GatherArgs& a, int64_t p) {
   return (r >= 0 && r < a.xrows) ? r : -1;
 }
 
+// One listing phase of the grouped kernels: the ids from pair `scan` on are
+// read kGaRoundIds per round (RND per thread, two rounds in flight: the next
+// round's ids are requested before the current round is compared, into the
+// other of two arrays, so no register copy waits for them) and expert e's
+// pairs appended to the LDS list, until the ids run out or the list could
+// overflow on the next round. A thread's matches are counted first; one
+// wave-wide prefix sum and one LDS atomic per wave reserve their slots. The
+// list order is free: every listed pair's output row is computed on its own.
+// Contains barriers: every thread of the block calls it. Returns the count.
+template <int RND>
+__device__ inline int ga_list_phase(const GatherArgs& a, __amdgpu_buffer_rsrc_t rid, int64_t e,
+                                    int64_t& scan, int tid, int* cnt, int32_t* list) {
+  const int lane = tid & 63;
+  // raw ids equal to e (and, for int32 ids, to e - E, which wraps to e)
+  const uint32_t e1 = (uint32_t)e, e2 = a.experts_i32 ? (uint32_t)(e - a.E) : (uint32_t)e;
+  const uint32_t pairs = (uint32_t)a.pairs;
+  auto load_round = [&](uint32_t (&r)[RND], int64_t base) {
+    const bool live = base < a.pairs;
+#pragma unroll
+    for (int c = 0; c < RND / 4; ++c) {
+      const uint32_t off = live ? (uint32_t)((base + RND * tid + 4 * c) * 4) : 0x80000000u;
+      const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rid, off, 0, 0));
+#pragma unroll
+      for (int k = 0; k < 4; ++k) r[4 * c + k] = v[k];
+    }
+  };
+  auto round = [&](const uint32_t (&ids)[RND]) {
+    const uint32_t p0 = (uint32_t)scan + RND * tid;
+    uint32_t mb = 0;
+#pragma unroll
+    for (int i = 0; i < RND; ++i)
+      if (p0 + i < pairs && (ids[i] == e1 || ids[i] == e2)) mb |= 1u << i;
+    const int c = __popc(mb);
+    int incl = c;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int t = __shfl_up(incl, d, 64);
+      if (lane >= d) incl += t;
+    }
+    const int tot = __shfl(incl, 63, 64);
+    if (tot > 0) {  // uniform per wave
+      int base = 0;
+      if (lane == 63) base = atomicAdd(cnt, tot);
+      base = __shfl(base, 63, 64);
+      int pos = base + incl - c;
+      while (mb) {
+        list[pos++] = (int32_t)(p0 + __builtin_ctz(mb));
+        mb &= mb - 1u;
+      }
+    }
+    scan += kGaRoundIds;
+    __syncthreads();
+  };
+  uint32_t ra[RND], rb[RND];
+  load_round(ra, scan);
+  __syncthreads();
+  if (tid == 0) *cnt = 0;
+  __syncthreads();
+  while (scan < a.pairs) {
+    if (*cnt > kGaCap - kGaRoundIds) break;  // uniform: read after the round's barrier
+    load_round(rb, scan + kGaRoundIds);
+    round(ra);
+    if (scan >= a.pairs || *cnt > kGaCap - kGaRoundIds) break;
+    load_round(ra, scan + kGaRoundIds);
+    round(rb);
+  }
+  return *cnt;
+}
+
 template <int WAVES>
 __global__ __launch_bounds__(WAVES * 64) void gather_hl_kernel(GatherArgs a) {
   // WAVES = 4: 2 x 2 waves of 64 x 64; WAVES = 8: 4 x 2 waves of 32 x 64
@@ -767,57 +836,13 @@ __global__ __launch_bounds__(WAVES * 64) void gather_hl_kernel(GatherArgs a) {
   // the expert ids as stored (converted where compared); thread tid reads ids
   // base + RND tid .. + RND - 1 of a round with 16-byte buffer loads (ids past
   // the last pair read zeros and are never listed)
-  auto id_of = [&](uint32_t raw) -> int64_t {
-    if (a.experts_i32) {
-      const int64_t v = (int32_t)raw;
-      return v < 0 ? v + a.E : v;
-    }
-    return (int64_t)raw;
-  };
   static_assert(RND % 4 == 0, "whole 16-byte id loads");
   const __amdgpu_buffer_rsrc_t rid = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<void*>(a.experts), (short)0, (int)(a.pairs * 4), 0x00020000);
-  // one round's ids, kept raw; the next round's are requested before the
-  // current round is compared, so the scan pays the load latency once
-  uint32_t cur[RND], nxt[RND];
-  auto load_round = [&](uint32_t (&r)[RND], int64_t base) {
-    const bool live = base < a.pairs;
-#pragma unroll
-    for (int c = 0; c < RND / 4; ++c) {
-      const uint32_t off = live ? (uint32_t)((base + RND * tid + 4 * c) * 4) : 0x80000000u;
-      const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rid, off, 0, 0));
-#pragma unroll
-      for (int k = 0; k < 4; ++k) r[4 * c + k] = v[k];
-    }
-  };
   int64_t scan = 0;
-  load_round(cur, 0);
   while (scan < a.pairs) {
-    // ---- fill the list from `scan` (kGaRoundIds ids per round, stop before overflow)
-    __syncthreads();
-    if (tid == 0) cnt = 0;
-    __syncthreads();
-    while (scan < a.pairs) {
-      if (cnt > kGaCap - kGaRoundIds) break;  // uniform: read after the round's barrier
-      load_round(nxt, scan + kGaRoundIds);
-#pragma unroll
-      for (int i = 0; i < RND; ++i) {
-        const int64_t p = scan + RND * tid + i;
-        const bool m = p < a.pairs && id_of(cur[i]) == e;
-        const uint64_t mask = __ballot(m);
-        if (mask) {  // uniform per wave
-          int base = 0;
-          if (lane == 0) base = atomicAdd(&cnt, __popcll(mask));
-          base = __shfl(base, 0, 64);
-          if (m) list[base + __popcll(mask & ((1ull << lane) - 1ull))] = (int32_t)p;
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < RND; ++i) cur[i] = nxt[i];
-      scan += kGaRoundIds;
-      __syncthreads();
-    }
-    const int rows = cnt;
+    // ---- fill the list from `scan` (stop before overflow)
+    const int rows = ga_list_phase<RND>(a, rid, e, scan, tid, &cnt, list);
 
     // ---- the listed pairs, kGaBM at a time, for each of this block's column tiles
     for (int nt = nt0; nt < nt1; ++nt)
@@ -976,7 +1001,7 @@ __global__ __launch_bounds__(WAVES * 64) void gather_hl_kernel(GatherArgs a) {
 // per-lane offsets; a row past the pass's last reads zeros through an
 // out-of-range offset, so the load sequence is the same on every path.
 // Measured at a 4096-token Qwen3-Next MoE prefill (40,960 pairs, top-10 of
-// 512): gate 222 us against 342 for the hi/lo kernel, down 268 against 414
+// 512): gate 219 us against 342 for the hi/lo kernel, down 262 against 414
 // (one barrier per group instead of per two: 234 and 280).
 // Non-temporal x loads, requesting all scan rounds' ids at once, and issuing
 // the next pass's first loads before a pass's stores all measured slower.
@@ -1017,28 +1042,8 @@ __global__ __launch_bounds__(kXpT) void gather_xp_kernel(GatherArgs a) {
     return;
   }
 
-  auto id_of = [&](uint32_t raw) -> int64_t {
-    if (a.experts_i32) {
-      const int64_t v = (int32_t)raw;
-      return v < 0 ? v + a.E : v;
-    }
-    return (int64_t)raw;
-  };
   static_assert(RND % 4 == 0, "whole 16-byte id loads");
   const __amdgpu_buffer_rsrc_t rid = buf_rsrc(a.experts, (uint32_t)(a.pairs * 4));
-  // one round's ids, kept raw; the next round's are requested before the
-  // current round is compared, so the scan pays the load latency once
-  uint32_t cur[RND], nxt[RND];
-  auto load_round = [&](uint32_t (&r)[RND], int64_t base) {
-    const bool live = base < a.pairs;
-#pragma unroll
-    for (int c = 0; c < RND / 4; ++c) {
-      const uint32_t off = live ? (uint32_t)((base + RND * tid + 4 * c) * 4) : 0x80000000u;
-      const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rid, off, 0, 0));
-#pragma unroll
-      for (int k = 0; k < 4; ++k) r[4 * c + k] = v[k];
-    }
-  };
 
   const uint32_t xbytes = (uint32_t)(((a.xrows - 1) * a.xs + a.K) * 2);
   const __amdgpu_buffer_rsrc_t rx = buf_rsrc(a.x, xbytes);
@@ -1117,32 +1122,8 @@ __global__ __launch_bounds__(kXpT) void gather_xp_kernel(GatherArgs a) {
 
   int64_t scan = 0;
   while (scan < a.pairs) {
-    // ---- list this expert's pairs from `scan` (kGaRoundIds ids per round)
-    load_round(cur, scan);
-    __syncthreads();
-    if (tid == 0) cnt = 0;
-    __syncthreads();
-    while (scan < a.pairs) {
-      if (cnt > kGaCap - kGaRoundIds) break;  // uniform: read after the round's barrier
-      load_round(nxt, scan + kGaRoundIds);
-#pragma unroll
-      for (int i = 0; i < RND; ++i) {
-        const int64_t p = scan + RND * tid + i;
-        const bool m = p < a.pairs && id_of(cur[i]) == e;
-        const uint64_t mask = __ballot(m);
-        if (mask) {  // uniform per wave
-          int base = 0;
-          if (lane == 0) base = atomicAdd(&cnt, __popcll(mask));
-          base = __shfl(base, 0, 64);
-          if (m) list[base + __popcll(mask & ((1ull << lane) - 1ull))] = (int32_t)p;
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < RND; ++i) cur[i] = nxt[i];
-      scan += kGaRoundIds;
-      __syncthreads();
-    }
-    const int rows = cnt;
+    // ---- list this expert's pairs from `scan` (stop before overflow)
+    const int rows = ga_list_phase<RND>(a, rid, e, scan, tid, &cnt, list);
 
     for (int nt = nt0; nt < nt1; ++nt)
     for (int t0 = 0; t0 < rows; t0 += BM) {
