@@ -109,6 +109,11 @@ __device__ inline void qmv_stage_x(const uint16_t* xrow, uint32_t* xs_perm, floa
 template <class S, int STEPS>
 __device__ inline float qmv_dot(const u32x4* codes, const uint32_t* sraw, const uint32_t* braw,
                                 const uint32_t* xs_perm, const float* hsum, int j) {
+  // the nibble mask and the exponent bits of 128 in registers: a
+  // three-operand and-or takes no literal on this target, and with literals
+  // the compiler splits it into a separate and and or
+  uint32_t nib = 0x000f000fu, one = 0x43004300u;
+  asm volatile("" : "+v"(nib), "+v"(one));
   float acc = 0.0f;
 #pragma unroll
   for (int s = 0; s < STEPS; ++s) {
@@ -124,10 +129,10 @@ __device__ inline float qmv_dot(const u32x4* codes, const uint32_t* sraw, const 
     for (int wi = 0; wi < 4; ++wi) {
       const uint32_t c = cs[wi];
       // (128 + q_i, 128 + q_{i+4}) as packed bf16, i = 0..3
-      d = dot2_bf16(xw[wi][0], (c & 0x000f000fu) | 0x43004300u, d);
-      d = dot2_bf16(xw[wi][1], ((c >> 4) & 0x000f000fu) | 0x43004300u, d);
-      d = dot2_bf16(xw[wi][2], ((c >> 8) & 0x000f000fu) | 0x43004300u, d);
-      d = dot2_bf16(xw[wi][3], ((c >> 12) & 0x000f000fu) | 0x43004300u, d);
+      d = dot2_bf16(xw[wi][0], (c & nib) | one, d);
+      d = dot2_bf16(xw[wi][1], ((c >> 4) & nib) | one, d);
+      d = dot2_bf16(xw[wi][2], ((c >> 8) & nib) | one, d);
+      d = dot2_bf16(xw[wi][3], ((c >> 12) & nib) | one, d);
     }
     const float hs = hsum[h];
     const float sv = S::lo(sraw[s]), bv = S::lo(braw[s]);
