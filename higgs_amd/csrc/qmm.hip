@@ -49,6 +49,7 @@ struct QmmArgs {
   int experts_i32;
   int64_t E, N, K;
   int group;
+  int gsh;          // log2(group): group is 32, 64 or 128
   int64_t pairs;
   int64_t p0;       // first pair of this launch (launches cover <= 65535 pairs)
   void* y;
@@ -167,7 +168,7 @@ __global__ __launch_bounds__(256) void qmv_bf16_kernel(QmmArgs a) {
   const int64_t nc = n < a.N ? n : a.N - 1;
   const int64_t ec = valid ? e : 0;
   const uint32_t* wrow = a.w + (ec * a.N + nc) * (K / 8);
-  const int gpr = K / a.group;
+  const int gpr = K >> a.gsh;
   const uint16_t* srow = reinterpret_cast<const uint16_t*>(a.sc) + (ec * a.N + nc) * gpr;
   const uint16_t* brow = reinterpret_cast<const uint16_t*>(a.bi) + (ec * a.N + nc) * gpr;
 
@@ -179,7 +180,7 @@ __global__ __launch_bounds__(256) void qmv_bf16_kernel(QmmArgs a) {
 #pragma unroll
   for (int s = 0; s < STEPS; ++s) {
     codes[s] = *reinterpret_cast<const u32x4*>(wrow + s * 16 + j * 4);
-    const int g = (s * 128 + j * 32) / a.group;
+    const int g = (s * 128 + j * 32) >> a.gsh;
     sraw[s] = srow[g];
     braw[s] = brow[g];
   }
@@ -230,7 +231,7 @@ __global__ __launch_bounds__(256) void qmv_swiglu_bf16_kernel(QmmArgs a, const u
   const uint16_t* ssel = reinterpret_cast<const uint16_t*>(is_up ? scu : a.sc);
   const uint16_t* bsel = reinterpret_cast<const uint16_t*>(is_up ? biu : a.bi);
   const uint32_t* wrow = wsel + (ec * a.N + nc) * (K / 8);
-  const int gpr = K / a.group;
+  const int gpr = K >> a.gsh;
   const uint16_t* srow = ssel + (ec * a.N + nc) * gpr;
   const uint16_t* brow = bsel + (ec * a.N + nc) * gpr;
 
@@ -239,7 +240,7 @@ __global__ __launch_bounds__(256) void qmv_swiglu_bf16_kernel(QmmArgs a, const u
 #pragma unroll
   for (int s = 0; s < STEPS; ++s) {
     codes[s] = *reinterpret_cast<const u32x4*>(wrow + s * 16 + j * 4);
-    const int g = (s * 128 + j * 32) / a.group;
+    const int g = (s * 128 + j * 32) >> a.gsh;
     sraw[s] = srow[g];
     braw[s] = brow[g];
   }
@@ -370,6 +371,7 @@ extern "C" int hgk_gather_qmm(int dtype, const void* x, int64_t x_rows, int64_t 
   a.x = x; a.xrows = x_rows; a.xs = x_row_stride; a.xdiv = x_row_div > 0 ? x_row_div : 1; a.lhs = lhs_indices;
   a.w = w; a.sc = scales; a.bi = biases; a.experts = rhs_indices; a.experts_i32 = rhs_dtype == DT_I32;
   a.E = n_experts; a.N = n; a.K = k; a.group = group_size; a.pairs = pairs; a.y = y;
+  a.gsh = group_size == 32 ? 5 : group_size == 64 ? 6 : 7;
   a.ys = y_row_stride;
   const hipStream_t s = as_stream(stream);
   // many pairs per expert (prefill): grouped by expert on the matrix cores
@@ -435,6 +437,7 @@ extern "C" int hgk_quantized_matmul(int dtype, const void* x, int64_t m, int64_t
   a.x = x; a.xrows = m; a.xs = x_row_stride; a.xdiv = 1; a.lhs = nullptr;
   a.w = w; a.sc = scales; a.bi = biases; a.experts = nullptr; a.experts_i32 = 0;
   a.E = 1; a.N = n; a.K = k; a.group = group_size; a.pairs = m; a.y = y; a.ys = y_row_stride;
+  a.gsh = group_size == 32 ? 5 : group_size == 64 ? 6 : 7;
   const bool vec_ok = dtype == DT_BF16 && aligned16(x) && x_row_stride % 8 == 0 && aligned16(w) &&
                       (reinterpret_cast<uintptr_t>(scales) & 1) == 0;
   if (vec_ok && launch_bf16<BF16>(a, s)) return launch_status(fn);
@@ -493,6 +496,7 @@ extern "C" int hgk_gather_qmm_swiglu(int dtype, const void* x, int64_t x_rows,
   a.w = w_gate; a.sc = scales_gate; a.bi = biases_gate; a.experts = rhs_indices;
   a.experts_i32 = rhs_dtype == DT_I32;
   a.E = n_experts; a.N = n; a.K = k; a.group = group_size; a.pairs = pairs; a.y = y;
+  a.gsh = group_size == 32 ? 5 : group_size == 64 ? 6 : 7;
   a.ys = y_row_stride;
   const hipStream_t s = as_stream(stream);
   switch (k) {
