@@ -56,6 +56,21 @@ def test_qwen3_next_decode_moe_shapes(dev, proj):
     _check(got, ref, O.BF16, proj)
 
 
+@pytest.mark.parametrize("N,group", [(300, 64), (1000, 32), (2112, 128)])
+def test_short_rows_ragged_column_blocks(dev, N, group):
+    """Short rows (K = 512, the down projection's shape class): row counts
+    that leave the last 64-row block partly filled, each group size, and
+    experts out of range."""
+    P, R, E, K = 96, 96, 12, 512
+    x, w, s, b, ex = _case(2380 + N + group, P, R, E, N, K, group=group)
+    ex = ex.copy()
+    ex[[3, 40]] = [E + 1, -2]  # out of range -> zero row; -2 wraps to E - 2
+    got = _run(dev, x, w, s, b, ex, O.BF16, group=group)
+    ref = O.gather_qmm(x, O.BF16, w, s, b, O.BF16, ex, group=group)
+    _check(got, ref, O.BF16, f"N={N} g={group}")
+    assert not got[3].any() and got[40].any()
+
+
 @pytest.mark.parametrize("K,group", [(1024, 64), (4096, 64), (2048, 32), (2048, 128), (512, 32)])
 def test_k_and_group_variants(dev, K, group):
     x, w, s, b, ex = _case(2320 + K + group, 37, 37, 9, 192, K, group=group)
