@@ -1001,9 +1001,13 @@ __global__ __launch_bounds__(WAVES * 64) void gather_hl_kernel(GatherArgs a) {
 // per-lane offsets; a row past the pass's last reads zeros through an
 // out-of-range offset, so the load sequence is the same on every path.
 // Measured at a 4096-token Qwen3-Next MoE prefill (40,960 pairs, top-10 of
-// 512): gate 219 us against 342 for the hi/lo kernel, down 244 against 414
-// (one barrier per group instead of per two: 234 and 280, the down figure
-// with its four column tiles in one block per expert).
+// 512): gate 190 us against 342 for the hi/lo kernel, down 224 against 414.
+// Passes of 112 rows (7 row tiles) rather than 96 took gate from 218 to
+// 190 us and down from 261 to 224. An expert holds about 80 pairs here, but
+// with 96 rows per pass those holding more than 96 took a second pass, and
+// the CUs running them set the launch's end. 128-row passes measured 191 us
+// for gate. (One barrier per group instead of per two: 234 and 280 at 96
+// rows.)
 // Non-temporal x loads, requesting all scan rounds' ids at once, and issuing
 // the next pass's first loads before a pass's stores all measured slower.
 constexpr int kXpXB = 4;  // x buffers in LDS (two groups per barrier)
@@ -1271,7 +1275,7 @@ bool gather_grouped_supported(int dtype, int sdt, int group_size, int bits, cons
 #define HGK_GATHER_XP 1
 #endif
 #ifndef HGK_XP_RT
-#define HGK_XP_RT 6
+#define HGK_XP_RT 7
 #endif
 
 // The exact-product grouped kernel takes K in units of 8 groups and addresses
@@ -1284,11 +1288,12 @@ bool gather_xp_fits(const GatherArgs& a) {
 
 void gather_xp_launch(const GatherArgs& a, hipStream_t s) {
   const int64_t ntiles = (a.N + kXpBN - 1) / kXpBN;
-  // column tiles split over about 2048 blocks in all: each block lists its
+  // column tiles split over about 1024 blocks in all: each block lists its
   // expert's pairs once for its tiles. At 512 experts and 4 tiles (the
-  // 2048-column down projection) 2 blocks per expert measured 243-244 us
-  // against 261-262 with 1 and 265 with 4.
-  int64_t gx = 2048 / (a.E + 1);
+  // 2048-column down projection) 1 block per expert measured 224-225 us,
+  // against 232 with 2 and 265 with 4 (with 96-row passes 2 had been best:
+  // 244 against 261).
+  int64_t gx = 1024 / (a.E + 1);
   gx = gx < 1 ? 1 : (gx > ntiles ? ntiles : gx);
   const int64_t tpg = (ntiles + gx - 1) / gx;
   gx = (ntiles + tpg - 1) / tpg;
