@@ -406,12 +406,13 @@ def wl_qwen3_next_qlinear(cx):
     return Workload("qwen3_next_qlinear", cfg, ks, nd, 64 + 4096)
 
 
-def wl_qwen3_next_moe_prefill(cx):
+def wl_qwen3_next_moe_prefill(cx, fused=False):
     """Qwen3-Next-80B-A3B routed experts over a 4096-token prefill: top-10 of
     512 experts (40,960 pairs, ~80 per expert), gate and up (512 x 2048)
     gather_qmm, SwiGLU, down (2048 x 512) gather_qmm, 4-bit group 64 -- the
     expert-grouped matrix-core path; flops = 2 x pairs x N x K per
-    projection."""
+    projection. fused: gate, up and SwiGLU as one hgk_gather_qmm_swiglu
+    launch."""
     torch = cx.torch
     T, top_k, E, D, I = 4096, 10, 512, 2048, 512
     P = T * top_k
@@ -434,10 +435,17 @@ def wl_qwen3_next_moe_prefill(cx):
         ks.append(k)
     act = [(outs["gate"][si], outs["up"][si], cx.empty((P, I), torch.bfloat16)) for si in range(ns)]
     ks.insert(2, k_glu(cx, "swiglu_moe_prefill", act, P, I, SILU))
-    cfg = {"workload": "qwen3-next-80b-a3b routed experts, 4096-token prefill", "tokens": T,
+    if fused:
+        sets = [(xs[si], exs[si], exd[si], act[si][2]) for si in range(ns)]
+        kf = k_qmm_swiglu(cx, "qmm_gate_up_swiglu_prefill", sets, tab["gate"], tab["up"], E, I, D,
+                          T, top_k)
+        kf.flops = 2 * 2 * P * I * D
+        ks = [kf, ks[3]]
+    cfg = {"workload": "qwen3-next-80b-a3b routed experts, 4096-token prefill" +
+           (", gate + up + SwiGLU in one launch" if fused else ""), "tokens": T,
            "experts": E, "top_k": top_k, "hidden": D, "expert_dim": I, "quant": "4-bit g64",
            "buffer_sets": ns}
-    return Workload("qwen3_next_moe_prefill", cfg, ks, ns, T)
+    return Workload("qwen3_next_moe_prefill" + ("_fused" if fused else ""), cfg, ks, ns, T)
 
 
 def k_gdn(cx, name, sets, wq, wk, alog, dtb, B, T, Hk, Dk, Hv, Dv):
@@ -724,6 +732,7 @@ WORKLOADS = {
     "qwen3_next_gdn": wl_qwen3_next_gdn,
     "qwen3_next_qlinear": wl_qwen3_next_qlinear,
     "qwen3_next_moe_prefill": wl_qwen3_next_moe_prefill,
+    "qwen3_next_moe_prefill_fused": lambda cx: wl_qwen3_next_moe_prefill(cx, fused=True),
     "qwen3_next_decode_layers": wl_qwen3_next_decode_layers,
     "qwen3_next_decode_layers_fused": lambda cx: wl_qwen3_next_decode_layers(cx, fused=True),
 }

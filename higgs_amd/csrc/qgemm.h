@@ -32,6 +32,10 @@ struct GatherArgs {
   int64_t E, N, K, pairs;
   uint16_t* y;
   int64_t ys;
+  // the up projection of the fused gate + up + SwiGLU form (null otherwise)
+  const uint32_t* w2;
+  const uint16_t* sc2;
+  const uint16_t* bi2;
 };
 
 // Pairs per expert (on average) from which the grouped kernel runs.
@@ -44,6 +48,9 @@ bool gather_grouped_supported(int dtype, int sdt, int group_size, int bits, cons
                               int64_t xs, const void* w, int64_t k, const void* experts,
                               int64_t pairs);
 void gather_grouped_launch(const GatherArgs& a, hipStream_t s);
+// swiglu(gate, up) of the grouped regime in one launch (w/sc/bi: gate, w2/sc2/
+// bi2: up, same shapes); false where the fused kernel does not apply.
+bool gather_swiglu_grouped_launch(const GatherArgs& a, hipStream_t s);
 
 // Rows of x at or above which the MFMA kernel runs (below: one GEMV per row).
 constexpr int64_t kQgemmMinRows = 16;

@@ -29,6 +29,7 @@
 // is double-buffered in LDS (one barrier per group) and the next group's x,
 // codes, scales and biases are loaded while the current group's MFMAs run.
 #include "../../include/higgs_hip.h"
+#include "hgk_act.h"
 #include "hgk_common.h"
 #include "hgk_host.h"
 #include "qgemm.h"
@@ -1014,9 +1015,14 @@ constexpr int kXpXB = 4;  // x buffers in LDS (two groups per barrier)
 constexpr int kXpWaves = 8, kXpT = 64 * kXpWaves;
 constexpr int kXpBN = 64 * kXpWaves;  // columns per block pass
 
-template <int RT>
+// SW: the fused gate + up + SwiGLU form. Waves 0-3 run the gate projection
+// and waves 4-7 the up projection of the same 256 columns; after a pass the
+// up waves leave their bf16 results in LDS and the gate waves write
+// swiglu(gate, up), rounded as the reference's three calls round it.
+template <int RT, bool SW>
 __global__ __launch_bounds__(kXpT) void gather_xp_kernel(GatherArgs a) {
   constexpr int BM = 16 * RT, NT = 4;
+  constexpr int BNO = SW ? kXpBN / 2 : kXpBN;  // output columns per pass
   constexpr int XP = (BM * 8 + kXpT - 1) / kXpT;  // 16-byte x pieces per thread per group
   constexpr int RND = kGaRoundIds / kXpT;  // ids per thread per scan round
   __shared__ __align__(16) uint16_t xs[kXpXB][BM][kQgPitch];
@@ -1030,14 +1036,14 @@ __global__ __launch_bounds__(kXpT) void gather_xp_kernel(GatherArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l16 = lane & 15, lg = lane >> 4;
   const int64_t e = blockIdx.y;
-  const int ntiles = (int)((a.N + kXpBN - 1) / kXpBN);
+  const int ntiles = (int)((a.N + BNO - 1) / BNO);
   const int tpg = (ntiles + (int)gridDim.x - 1) / (int)gridDim.x;
   const int nt0 = (int)blockIdx.x * tpg, nt1 = nt0 + tpg < ntiles ? nt0 + tpg : ntiles;
   const int G = (int)(a.K / 64);
 
   if (e == a.E) {
     // pairs whose expert is out of range: zero rows (this block's columns)
-    const int64_t c0 = (int64_t)nt0 * kXpBN, c1 = (int64_t)nt1 * kXpBN < a.N ? (int64_t)nt1 * kXpBN : a.N;
+    const int64_t c0 = (int64_t)nt0 * BNO, c1 = (int64_t)nt1 * BNO < a.N ? (int64_t)nt1 * BNO : a.N;
     for (int64_t p0 = 0; p0 < a.pairs; p0 += kXpT) {
       const int64_t p = p0 + tid;
       const int64_t ep = p < a.pairs ? ga_expert(a, p) : 0;
@@ -1052,24 +1058,28 @@ __global__ __launch_bounds__(kXpT) void gather_xp_kernel(GatherArgs a) {
 
   const uint32_t xbytes = (uint32_t)(((a.xrows - 1) * a.xs + a.K) * 2);
   const __amdgpu_buffer_rsrc_t rx = buf_rsrc(a.x, xbytes);
-  const __amdgpu_buffer_rsrc_t rw = buf_rsrc(a.w, (uint32_t)(a.E * a.N * a.K / 2));
-  const __amdgpu_buffer_rsrc_t rs = buf_rsrc(a.sc, (uint32_t)(a.E * a.N * G * 2));
-  const __amdgpu_buffer_rsrc_t rb = buf_rsrc(a.bi, (uint32_t)(a.E * a.N * G * 2));
+  // the up waves (SW, waves 4-7: also the threads staging the up columns'
+  // scales) read the up projection's arrays
+  const bool upw = SW && wave >= 4;
+  const __amdgpu_buffer_rsrc_t rw = buf_rsrc(upw ? a.w2 : a.w, (uint32_t)(a.E * a.N * a.K / 2));
+  const __amdgpu_buffer_rsrc_t rs = buf_rsrc(upw ? a.sc2 : a.sc, (uint32_t)(a.E * a.N * G * 2));
+  const __amdgpu_buffer_rsrc_t rb = buf_rsrc(upw ? a.bi2 : a.bi, (uint32_t)(a.E * a.N * G * 2));
   const int C8 = G / 8;
+  const int wcol = SW ? (wave & 3) : wave;  // the wave's 64-column slice of the pass
 
   // ---- per-pass addressing and loads (a pass: column chunk nt, rows t0 .. t0 + rp)
   uint32_t wo[NT], so, xo[XP];
   // this lane's columns of chunk nt: codes (words 2 lg, 2 lg + 1 of each
   // group); this thread's column of the block's scale/bias staging
   auto set_cols = [&](int nt) {
-    const int64_t n0 = (int64_t)nt * kXpBN + 64 * wave;
+    const int64_t n0 = (int64_t)nt * BNO + 64 * wcol;
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       const int64_t n = n0 + 16 * t + l16;
       const int64_t nc = n < a.N ? n : a.N - 1;
       wo[t] = (uint32_t)((e * a.N + nc) * (a.K / 2)) + 8u * lg;
     }
-    const int64_t sn = (int64_t)nt * kXpBN + tid;
+    const int64_t sn = (int64_t)nt * BNO + (SW ? (tid & (BNO - 1)) : tid);
     so = (uint32_t)((e * a.N + (sn < a.N ? sn : a.N - 1)) * G * 2);
   };
   // this thread's x pieces: piece c = tid + 512 i is row c / 8, bytes 16 (c % 8)
@@ -1134,7 +1144,7 @@ __global__ __launch_bounds__(kXpT) void gather_xp_kernel(GatherArgs a) {
     for (int t0 = 0; t0 < rows; t0 += BM) {
       const int rp = rows - t0 < BM ? rows - t0 : BM;  // rows of this pass
       const int rt = (rp + 15) >> 4;                   // live row tiles
-      const int64_t n0 = (int64_t)nt * kXpBN + 64 * wave;
+      const int64_t n0 = (int64_t)nt * BNO + 64 * wcol;
       set_cols(nt);
       set_rows(t0, rp);
       fetch_sb(0);
@@ -1242,18 +1252,62 @@ __global__ __launch_bounds__(kXpT) void gather_xp_kernel(GatherArgs a) {
         }
       }
 
+      if constexpr (SW) {
+        // the up results, rounded to bf16 as gather_qmm writes them, meet the
+        // gate waves' in LDS over the x buffers (every wave's reads of them
+        // are done at the barrier)
+        static_assert(BM * BNO * 2 <= (int)sizeof(xs), "up staging fits the x buffers");
+        uint16_t* ust = &xs[0][0][0];
+        __syncthreads();
+        if (wave >= 4) {
 #pragma unroll
-      for (int i = 0; i < RT; ++i) {
-        if (i >= rt) continue;
+          for (int i = 0; i < RT; ++i) {
+            if (i >= rt) continue;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int lr = i * 16 + 4 * lg + r;
-          if (lr >= rp) continue;
-          const int64_t p = list[t0 + lr];
+            for (int r = 0; r < 4; ++r) {
+              const int lr = i * 16 + 4 * lg + r;
 #pragma unroll
-          for (int t = 0; t < NT; ++t) {
-            const int64_t n = n0 + 16 * t + l16;
-            if (n < a.N) a.y[p * a.ys + n] = (uint16_t)(BF16::pack(acc[i][t][r], 0.0f) & 0xffffu);
+              for (int t = 0; t < NT; ++t)
+                ust[lr * BNO + 64 * wcol + 16 * t + l16] = (uint16_t)(BF16::pack(acc[i][t][r], 0.0f) & 0xffffu);
+            }
+          }
+        }
+        __syncthreads();
+        if (wave < 4) {
+#pragma unroll
+          for (int i = 0; i < RT; ++i) {
+            if (i >= rt) continue;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int lr = i * 16 + 4 * lg + r;
+              if (lr >= rp) continue;
+              const int64_t p = list[t0 + lr];
+#pragma unroll
+              for (int t = 0; t < NT; ++t) {
+                const int64_t n = n0 + 16 * t + l16;
+                const float gv = BF16::round(acc[i][t][r]);
+                const float uv = BF16::lo((uint32_t)ust[lr * BNO + 64 * wcol + 16 * t + l16]);
+                float o;
+                swiglu16<BF16, 1>(&gv, &uv, &o);
+                if (n < a.N) a.y[p * a.ys + n] = (uint16_t)(BF16::pack(o, 0.0f) & 0xffffu);
+              }
+            }
+          }
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < RT; ++i) {
+          if (i >= rt) continue;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int lr = i * 16 + 4 * lg + r;
+            if (lr >= rp) continue;
+            const int64_t p = list[t0 + lr];
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+              const int64_t n = n0 + 16 * t + l16;
+              if (n < a.N) a.y[p * a.ys + n] = (uint16_t)(BF16::pack(acc[i][t][r], 0.0f) & 0xffffu);
+            }
           }
         }
       }
@@ -1298,7 +1352,21 @@ void gather_xp_launch(const GatherArgs& a, hipStream_t s) {
   const int64_t tpg = (ntiles + gx - 1) / gx;
   gx = (ntiles + tpg - 1) / tpg;
   const dim3 grid((unsigned)gx, (unsigned)(a.E + 1));
-  hipLaunchKernelGGL((gather_xp_kernel<HGK_XP_RT>), grid, dim3(kXpT), 0, s, a);
+  hipLaunchKernelGGL((gather_xp_kernel<HGK_XP_RT, false>), grid, dim3(kXpT), 0, s, a);
+}
+
+bool gather_swiglu_grouped_launch(const GatherArgs& a, hipStream_t s) {
+  if (!HGK_GATHER_XP || !gather_xp_fits(a) || !a.w2 || !a.sc2 || !a.bi2 ||
+      (reinterpret_cast<uintptr_t>(a.w2) & 15) != 0)
+    return false;
+  const int64_t ntiles = (a.N + kXpBN / 2 - 1) / (kXpBN / 2);
+  int64_t gx = 1024 / (a.E + 1);
+  gx = gx < 1 ? 1 : (gx > ntiles ? ntiles : gx);
+  const int64_t tpg = (ntiles + gx - 1) / gx;
+  gx = (ntiles + tpg - 1) / tpg;
+  const dim3 grid((unsigned)gx, (unsigned)(a.E + 1));
+  hipLaunchKernelGGL((gather_xp_kernel<HGK_XP_RT, true>), grid, dim3(kXpT), 0, s, a);
+  return true;
 }
 
 void gather_grouped_launch(const GatherArgs& a, hipStream_t s) {

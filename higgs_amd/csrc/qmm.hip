@@ -481,15 +481,32 @@ extern "C" int hgk_gather_qmm_swiglu(int dtype, const void* x, int64_t x_rows,
     return fail(HGK_ERR_ARG, "%s: null pointer", fn);
   if (n_experts * n * k >= ((int64_t)1 << 42) || pairs * n >= ((int64_t)1 << 32) || pairs >= ((int64_t)1 << 31))
     return fail(HGK_ERR_UNSUPPORTED, "%s: problem too large", fn);
-  if (pairs >= kGatherMinPairsPerExpert * n_experts)
-    return fail(HGK_ERR_UNSUPPORTED,
-                "%s: %lld pairs over %lld experts is the grouped (prefill) regime: run gate and up "
-                "through hgk_gather_qmm and the activation through hgk_glu",
-                fn, (long long)pairs, (long long)n_experts);
   const auto odd = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 1) != 0; };
   if (!aligned16(x) || x_row_stride % 8 || !aligned16(w_gate) || !aligned16(w_up) ||
       odd(scales_gate) || odd(biases_gate) || odd(scales_up) || odd(biases_up))
     return fail(HGK_ERR_UNSUPPORTED, "%s: x and the weights must be 16-byte aligned", fn);
+  if (pairs >= kGatherMinPairsPerExpert * n_experts) {
+    // many pairs per expert (prefill): the grouped matrix-core kernel's fused
+    // form, where it applies
+    if (pairs > 0 && n_experts < 65535 &&
+        gather_grouped_supported(dtype, scales_dtype, group_size, bits, x, x_row_stride, w_gate, k,
+                                 rhs_indices, pairs)) {
+      GatherArgs g{};
+      g.x = static_cast<const uint16_t*>(x); g.xrows = x_rows; g.xs = x_row_stride;
+      g.xdiv = x_row_div > 0 ? x_row_div : 1; g.lhs = lhs_indices; g.w = w_gate;
+      g.sc = static_cast<const uint16_t*>(scales_gate); g.bi = static_cast<const uint16_t*>(biases_gate);
+      g.w2 = w_up; g.sc2 = static_cast<const uint16_t*>(scales_up);
+      g.bi2 = static_cast<const uint16_t*>(biases_up);
+      g.experts = rhs_indices; g.experts_i32 = rhs_dtype == DT_I32; g.E = n_experts; g.N = n; g.K = k;
+      g.pairs = pairs; g.y = static_cast<uint16_t*>(y); g.ys = y_row_stride;
+      if (gather_swiglu_grouped_launch(g, as_stream(stream))) return launch_status(fn);
+    }
+    return fail(HGK_ERR_UNSUPPORTED,
+                "%s: %lld pairs over %lld experts is the grouped (prefill) regime and the fused "
+                "grouped kernel does not take this call: run gate and up through hgk_gather_qmm and "
+                "the activation through hgk_glu",
+                fn, (long long)pairs, (long long)n_experts);
+  }
   if (pairs == 0) return HGK_OK;
   QmmArgs a{};
   a.x = x; a.xrows = x_rows; a.xs = x_row_stride; a.xdiv = x_row_div > 0 ? x_row_div : 1; a.lhs = lhs_indices;

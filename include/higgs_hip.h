@@ -267,10 +267,13 @@ int hgk_gather_qmm(int dtype, const void* x, int64_t x_rows, int64_t x_row_strid
  * bit-identical to the three calls (each projection rounded to bf16 as
  * gather_qmm writes it, then hgk_glu's SwiGLU). Operands as hgk_gather_qmm,
  * with two weight sets of the same shape [n_experts, n, k/8] and one expert
- * index per pair. The decode (one GEMV per pair) form only: bf16 x and
- * scales, k in {512, 1024, 2048, 4096}, 16-byte aligned x and weights, and
- * fewer than 16 pairs per expert on average; other calls return
- * HGK_ERR_UNSUPPORTED and run as hgk_gather_qmm twice plus hgk_glu.
+ * index per pair. Requires bf16 x and scales, k in {512, 1024, 2048, 4096}
+ * and 16-byte aligned x and weights. Below 16 pairs per expert on average
+ * (decode) it runs one GEMV per pair. At 16 or more (prefill) it runs the
+ * expert-grouped matrix-core kernel's fused form, which further needs group
+ * 64, expert ids 16-byte aligned and a pair count that is a multiple of 4.
+ * Other calls return HGK_ERR_UNSUPPORTED and run as hgk_gather_qmm twice plus
+ * hgk_glu.
  */
 int hgk_gather_qmm_swiglu(int dtype, const void* x, int64_t x_rows, int64_t x_row_stride,
                           int64_t x_row_div, const int32_t* lhs_indices, const uint32_t* w_gate,

@@ -309,10 +309,43 @@ def test_fused_gate_up_swiglu_decode(dev, K, group):
     _check(uh, ru, O.BF16, f"fused K={K} g={group}: up projection")
 
 
+def test_fused_gate_up_swiglu_grouped_prefill(dev):
+    """The 4096-token Qwen3-Next MoE prefill (top-10 of 512 experts, 40,960
+    pairs, N 512, K 2048) through the fused entry: the grouped matrix-core
+    kernel's fused form. It equals the reference's three calls run on the
+    device bit for bit, and the oracle's SwiGLU applied to the device's two
+    projections; out-of-range experts give zero rows. With group 32 the fused
+    grouped kernel does not apply and the Python form runs the three calls."""
+    T, top_k, E, N, K = 4096, 10, 512, 512, 2048
+    x, g, u, ex = _fused_case(4201, T, top_k, E, N, K)
+    ex[[7, 20000]] = [E, -E - 1]
+    got = to_host(_fused_dev(dev, x, g, u, ex, top_k))
+    d = lambda t: to_dev(t, O.BF16, dev)
+    gh = to_host(H.gather_qmm(d(x), words_dev(g[0], dev), d(g[1]), d(g[2]), to_dev(ex, O.I32, dev),
+                              x_row_div=top_k))
+    uh = to_host(H.gather_qmm(d(x), words_dev(u[0], dev), d(u[1]), d(u[2]), to_dev(ex, O.I32, dev),
+                              x_row_div=top_k))
+    three = O.glu(O.ACT_SILU, gh, uh, O.BF16)
+    assert np.array_equal(got, three), "fused grouped result differs from the three calls"
+    assert not got[[7, 20000]].any()
+    rows = np.r_[0:256, T * top_k - 256:T * top_k]
+    rg = O.gather_qmm(x, O.BF16, g[0], g[1], g[2], O.BF16, ex[rows], lhs=rows // top_k)
+    _check(gh[rows], rg, O.BF16, "grouped fused: gate projection (sampled pairs)")
+    # group 32: the fused grouped kernel does not take it
+    T2, E2, K2 = 512, 8, 1024
+    x2, g2, u2, ex2 = _fused_case(4211, T2, 4, E2, 256, K2, group=32)
+    got2 = to_host(_fused_dev(dev, x2, g2, u2, ex2, 4, group=32))
+    gh2 = to_host(H.gather_qmm(d(x2), words_dev(g2[0], dev), d(g2[1]), d(g2[2]),
+                               to_dev(ex2, O.I32, dev), group_size=32, x_row_div=4))
+    uh2 = to_host(H.gather_qmm(d(x2), words_dev(u2[0], dev), d(u2[1]), d(u2[2]),
+                               to_dev(ex2, O.I32, dev), group_size=32, x_row_div=4))
+    assert np.array_equal(got2, O.glu(O.ACT_SILU, gh2, uh2, O.BF16))
+
+
 def test_fused_gate_up_swiglu_routing_and_fallback(dev):
-    """Out-of-range experts give zero rows, as the three calls do; the grouped
-    (prefill) regime is refused by the fused entry and the Python form runs
-    the three calls there."""
+    """Out-of-range experts give zero rows, as the three calls do; in the
+    grouped (prefill) regime the fused entry runs the grouped kernel's fused
+    form, here with many passes per expert (~1000 pairs each)."""
     T, top_k, E, N, K = 8, 4, 6, 256, 512
     x, g, u, ex = _fused_case(4101, T, top_k, E, N, K)
     ex[[1, 5, 9]] = [E, -E - 1, 1 << 20]
