@@ -315,7 +315,9 @@ def test_fused_gate_up_swiglu_grouped_prefill(dev):
     kernel's fused form. It equals the reference's three calls run on the
     device bit for bit, and the oracle's SwiGLU applied to the device's two
     projections; out-of-range experts give zero rows. With group 32 the fused
-    grouped kernel does not apply and the Python form runs the three calls."""
+    grouped kernel does not apply and the Python form runs the three calls.
+    Rows routed through lhs indices, one out of range, match the three calls
+    too."""
     T, top_k, E, N, K = 4096, 10, 512, 512, 2048
     x, g, u, ex = _fused_case(4201, T, top_k, E, N, K)
     ex[[7, 20000]] = [E, -E - 1]
@@ -340,6 +342,22 @@ def test_fused_gate_up_swiglu_grouped_prefill(dev):
     uh2 = to_host(H.gather_qmm(d(x2), words_dev(u2[0], dev), d(u2[1]), d(u2[2]),
                                to_dev(ex2, O.I32, dev), group_size=32, x_row_div=4))
     assert np.array_equal(got2, O.glu(O.ACT_SILU, gh2, uh2, O.BF16))
+    # rows through lhs indices, one of them out of range (a zero row)
+    T3, E3, N3, K3 = 512, 16, 256, 512
+    P3 = T3 * 8
+    x3, g3, u3, ex3 = _fused_case(4221, T3, 8, E3, N3, K3)
+    lhs = ((np.arange(P3) * 37) % T3).astype(np.int32)
+    lhs[11] = T3
+    dl = to_dev(lhs, O.I32, dev)
+    got3 = to_host(H.gather_qmm_swiglu(d(x3), words_dev(g3[0], dev), d(g3[1]), d(g3[2]),
+                                       words_dev(u3[0], dev), d(u3[1]), d(u3[2]),
+                                       to_dev(ex3, O.I32, dev), lhs_indices=dl))
+    gh3 = to_host(H.gather_qmm(d(x3), words_dev(g3[0], dev), d(g3[1]), d(g3[2]),
+                               to_dev(ex3, O.I32, dev), lhs_indices=dl))
+    uh3 = to_host(H.gather_qmm(d(x3), words_dev(u3[0], dev), d(u3[1]), d(u3[2]),
+                               to_dev(ex3, O.I32, dev), lhs_indices=dl))
+    assert np.array_equal(got3, O.glu(O.ACT_SILU, gh3, uh3, O.BF16))
+    assert not got3[11].any() and got3[12].any()
 
 
 def test_fused_gate_up_swiglu_routing_and_fallback(dev):
