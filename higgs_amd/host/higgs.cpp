@@ -867,9 +867,10 @@ Array nn::SwitchMlpWeights::forward_gather(const Array& x, const Array& indices)
                             operands_text({{"x", &x}, {"indices", &indices}}));
   const int64_t T = x.dim(0), top_k = indices.dim(1);
   const Array idx = indices.reshape({T * top_k});
-  // gate, up and the SwiGLU in one launch where the fused decode kernel
-  // applies (same weights' shapes, bf16, few pairs per expert); otherwise the
-  // reference's three calls
+  // gate, up and the SwiGLU in one launch where a fused kernel applies (same
+  // weights' shapes, bf16: the decode GEMV at few pairs per expert, the
+  // grouped kernel's fused form at many); otherwise the reference's three
+  // calls
   Array act;
   bool fused = false;
   const Array& gw = gate_proj.weight;

@@ -259,7 +259,8 @@ struct SwitchMlpWeights {
   QLinear gate_proj, up_proj, down_proj;
   // x [T, D], indices [T, top_k] (Int32/Uint32) -> [T, top_k, D]: gate and up
   // gather_qmm, swiglu, down gather_qmm, as forward_gather does (gate, up and
-  // swiglu in one launch where the fused decode kernel applies).
+  // swiglu in one launch where a fused kernel applies: the decode GEMV, or
+  // the grouped matrix-core kernel's fused form at prefill).
   Array forward_gather(const Array& x, const Array& indices) const;
 };
 }  // namespace nn

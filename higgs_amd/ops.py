@@ -349,8 +349,9 @@ def gather_qmm_swiglu(x: torch.Tensor, w_gate: torch.Tensor, scales_gate: torch.
                       out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """swiglu(gather_qmm(x, gate...), gather_qmm(x, up...)) -- the gate/up half of
     SwitchMlpWeights::forward_gather (qwen3_next.rs:862-886) -- in one launch
-    where the fused decode kernel applies, else as the three calls. Returns
-    [P, N] in x's dtype."""
+    where a fused kernel applies (the per-pair decode kernel, or the grouped
+    matrix-core kernel's fused form at 16 or more pairs per expert), else as
+    the three calls. Returns [P, N] in x's dtype."""
     E, N = w_gate.shape[0], w_gate.shape[1]
     K = x.shape[1]
     idx = rhs_indices.reshape(-1).contiguous()
