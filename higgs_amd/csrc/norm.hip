@@ -225,13 +225,13 @@ namespace {
 template <class X, class Y>
 constexpr int unit_bytes() { return Y::kBytes > X::kBytes ? 8 : 16; }
 
-template <class X, class Y, class W, int LPR, int CPL, int MODE>
+template <class X, class Y, class W, int LPR, int CPL, int MODE, int UB = unit_bytes<X, Y>()>
 void launch_fast(const NormArgs& a, hipStream_t s) {
   constexpr int RPW = 64 / LPR;
   const int64_t waves = (a.rows + RPW - 1) / RPW;
   const int wpb = waves >= 4096 ? 4 : 1;  // small problems: spread over CUs
   const int64_t blocks = (waves + wpb - 1) / wpb;
-  hipLaunchKernelGGL((rms_norm_kernel<X, Y, W, LPR, CPL, MODE, unit_bytes<X, Y>()>),
+  hipLaunchKernelGGL((rms_norm_kernel<X, Y, W, LPR, CPL, MODE, UB>),
                      dim3((unsigned)blocks), dim3(64 * wpb), 0, s, a);
 }
 
@@ -274,14 +274,36 @@ bool launch_by_shape(const NormArgs& a, int nchunks, hipStream_t s) {
 
 // The vectorised kernels take weights in the activation type or in f32;
 // any other weight dtype goes to the generic kernel.
+// Rows too long for 8-byte units (more than 16 per lane: a 16-bit x with an
+// f32 output and n > 4096, e.g. hidden 4608 or 5376) take 16-byte units
+// instead, up to 16 per lane (n <= 8192 for a 16-bit x): each unit's output is
+// then two 16-byte stores rather than one.
+template <class X, class Y, class W, int MODE>
+bool launch_wide_units(const NormArgs& a, hipStream_t s) {
+  if constexpr (MODE == kGated || unit_bytes<X, Y>() == 16) {
+    return false;
+  } else {
+    const int cpl = (a.n / (16 / X::kBytes) + 63) / 64;
+    switch (cpl) {
+      case 9: case 10: launch_fast<X, Y, W, 64, 10, MODE, 16>(a, s); return true;
+      case 11: case 12: launch_fast<X, Y, W, 64, 12, MODE, 16>(a, s); return true;
+      case 13: case 14: launch_fast<X, Y, W, 64, 14, MODE, 16>(a, s); return true;
+      case 15: case 16: launch_fast<X, Y, W, 64, 16, MODE, 16>(a, s); return true;
+      default: return false;
+    }
+  }
+}
+
 template <class X, class Y, int MODE>
 void launch_xy(const NormArgs& a, bool vec_ok, hipStream_t s) {
   const int nchunks = a.n / (unit_bytes<X, Y>() / X::kBytes);
   if (vec_ok) {
     if (!a.w || a.wdt == X::kCode) {
       if (launch_by_shape<X, Y, X, MODE>(a, nchunks, s)) return;
+      if (a.n % (16 / X::kBytes) == 0 && launch_wide_units<X, Y, X, MODE>(a, s)) return;
     } else if (a.wdt == DT_F32) {
       if (launch_by_shape<X, Y, F32, MODE>(a, nchunks, s)) return;
+      if (a.n % (16 / X::kBytes) == 0 && launch_wide_units<X, Y, F32, MODE>(a, s)) return;
     }
   }
   launch_generic<X, Y, MODE>(a, s);

@@ -49,7 +49,7 @@ struct QembArgs {
   int group;
   float scale;
   int has_scale;
-  int fast_scale_ok;  // no output scale, or bf16/f16(scale) in [2^-20, 2^20]
+  int fast_scale_ok;  // no output scale, or an output scale in [2^-19, 2^19]
   void* out;  // h (may be null in the fused form)
   int64_t os;
   int64_t hidden;
@@ -91,9 +91,11 @@ __device__ inline float deq(uint32_t q, float s, float b) {
 // element by zero, so every intermediate must stay finite and normal: the
 // scale and bias ranges of deq_fast_ok guarantee that (bf16: 2^-100 <= |s| <
 // 2^100, b = +-0 or 2^-100 <= |b| < 2^126; f16: normal |s| < 2^12, |b| <
-// 2^11), the host admits output scales in [2^-20, 2^20] only, and a negative
-// scale beside a bias of -0 is excluded (q = 0 would give +0 where the
-// reference has -0). Rows with any other group take deq() instead.
+// 2^11), the host admits positive output scales in [2^-19, 2^19] only (a
+// negative one would turn a +0 element into -0 * (+0) + (+0) = +0 where the
+// reference has round(+0 * o) = -0), and a negative scale beside a bias of -0
+// is excluded (q = 0 would give +0 where the reference has -0). Rows with any
+// other group take deq() instead.
 template <class S> struct DeqK;
 template <> struct DeqK<BF16> {
   static constexpr uint32_t kMagic = 0x43004300u;  // bf16 128 in each half
@@ -500,12 +502,10 @@ extern "C" int hgk_quantized_embedding(const void* ids, int ids_dtype, int64_t n
   a.ids = ids; a.ids_i32 = ids_dtype == DT_I32; a.n = n_ids; a.wq = w_q; a.sc = scales;
   a.bi = biases; a.vocab = vocab; a.wpr = (int)(hidden / 8); a.gpr = (int)(hidden / group_size);
   a.group = group_size; a.scale = out_scale; a.has_scale = out_scale != 0.0f;
-  {
-    // the output scale as the scales dtype rounds it (|x| in [2^-20, 2^20]
-    // keeps every product of the dot2 form normal)
-    const float m = std::fabs(out_scale);
-    a.fast_scale_ok = !a.has_scale || (m >= 0x1p-19f && m <= 0x1p19f);
-  }
+  // the dot2 form takes positive output scales in [2^-19, 2^19]: every
+  // product stays normal, and no +0 element changes sign (a negative scale
+  // takes the element-by-element form, which gives the reference's -0)
+  a.fast_scale_ok = !a.has_scale || (out_scale >= 0x1p-19f && out_scale <= 0x1p19f);
   a.out = out; a.os = out_row_stride; a.hidden = hidden;
   const bool vec_ok = (reinterpret_cast<uintptr_t>(w_q) & 3u) == 0 && aligned16(out) &&
                       hidden % 8 == 0 && out_row_stride % 8 == 0;

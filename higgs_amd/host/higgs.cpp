@@ -809,8 +809,10 @@ Array gather_qmm(const Array& x, const Array& w, const Array& scales, const Arra
   if (x.ndim() != 2 || (x.dim(1) > 1 && x.strides()[1] != 1))
     fail(op, "x must be [rows, K] with a unit-stride last axis", ops);
   if (w.ndim() != 3 || w.dtype() != Dtype::Uint32 || !w.is_contiguous() || scales.ndim() != 3 ||
-      scales.shape() != biases.shape() || !scales.is_contiguous() || !biases.is_contiguous())
-    fail(op, "w must be contiguous Uint32 [E, N, K/8]; scales/biases [E, N, K/group]", ops);
+      scales.shape() != biases.shape() || !scales.is_contiguous() || !biases.is_contiguous() ||
+      scales.dtype() != biases.dtype())
+    fail(op, "w must be contiguous Uint32 [E, N, K/8]; scales/biases [E, N, K/group] of one dtype",
+         ops);
   if (!rhs_indices.is_contiguous() || (lhs_indices && !lhs_indices->is_contiguous()))
     fail(op, "indices must be contiguous", ops);
   const int64_t P = rhs_indices.size(), E = w.dim(0), N = w.dim(1), K = x.dim(1);
@@ -834,8 +836,9 @@ Array quantized_matmul(const Array& x, const Array& w, const Array& scales, cons
   if (!transpose) fail(op, "only transpose = true (weights stored [N, K]) is implemented", ops);
   if (x.ndim() < 1) fail(op, "x must have at least one axis", ops);
   if (w.ndim() != 2 || w.dtype() != Dtype::Uint32 || !w.is_contiguous() || scales.ndim() != 2 ||
-      scales.shape() != biases.shape() || !scales.is_contiguous() || !biases.is_contiguous())
-    fail(op, "w must be contiguous Uint32 [N, K/8]; scales/biases [N, K/group]", ops);
+      scales.shape() != biases.shape() || !scales.is_contiguous() || !biases.is_contiguous() ||
+      scales.dtype() != biases.dtype())
+    fail(op, "w must be contiguous Uint32 [N, K/8]; scales/biases [N, K/group] of one dtype", ops);
   const int64_t K = x.dim(-1), N = w.dim(0);
   if (bits <= 0 || w.dim(1) * 32 / bits != K) fail(op, "w's packed width does not match x's K", ops);
   Shape lead(x.shape().begin(), x.shape().end() - 1);
@@ -874,8 +877,13 @@ Array nn::SwitchMlpWeights::forward_gather(const Array& x, const Array& indices)
   Array act;
   bool fused = false;
   const Array& gw = gate_proj.weight;
+  // (one scales dtype reaches the kernel for both projections, so every
+  // scale and bias must share it)
+  const Dtype sdt = gate_proj.scales.dtype();
   const bool same = gw.shape() == up_proj.weight.shape() &&
                     gate_proj.scales.shape() == up_proj.scales.shape() &&
+                    gate_proj.biases.dtype() == sdt && up_proj.scales.dtype() == sdt &&
+                    up_proj.biases.dtype() == sdt &&
                     gate_proj.group_size == up_proj.group_size && gate_proj.bits == up_proj.bits;
   if (same && gw.ndim() == 3 && x.dtype() == Dtype::Bfloat16 && x.strides()[1] == 1 &&
       gw.is_contiguous() && up_proj.weight.is_contiguous() && gate_proj.scales.is_contiguous() &&

@@ -326,6 +326,8 @@ def gather_qmm(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: t
         raise HgkError(1, "x must be [rows, K] with a unit-stride last axis")
     if w.dim() != 3 or scales.dim() != 3 or scales.shape != biases.shape:
         raise HgkError(1, "w must be [E, N, K/8]; scales and biases [E, N, K/group]")
+    if scales.dtype != biases.dtype:
+        raise HgkError(1, "scales and biases must share a dtype")
     E, N = w.shape[0], w.shape[1]
     K = x.shape[1]
     P = rhs_indices.numel()
@@ -361,6 +363,10 @@ def gather_qmm_swiglu(x: torch.Tensor, w_gate: torch.Tensor, scales_gate: torch.
         out = torch.empty((P, N), dtype=x.dtype, device=x.device)
     if w_up.shape != w_gate.shape or scales_up.shape != scales_gate.shape:
         raise HgkError(1, "gate and up weights must have the same shapes")
+    for name, t in (("biases_gate", biases_gate), ("scales_up", scales_up), ("biases_up", biases_up)):
+        # one scales dtype reaches the kernel for both projections
+        if t.dtype != scales_gate.dtype:
+            raise HgkError(1, f"{name} dtype {t.dtype} differs from scales_gate's {scales_gate.dtype}")
     st = lib().hgk_gather_qmm_swiglu(
         dtype_code(x.dtype), _ptr(x), x.shape[0], x.stride(0), x_row_div, _ptr(lhs),
         _ptr(w_gate.contiguous()), _ptr(scales_gate.contiguous()), _ptr(biases_gate.contiguous()),
@@ -389,6 +395,8 @@ def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor,
         raise HgkError(2, "quantized_matmul: only transpose=True (weights stored [N, K]) is implemented")
     if w.dim() != 2 or scales.dim() != 2 or scales.shape != biases.shape:
         raise HgkError(1, "w must be [N, K/8]; scales and biases [N, K/group]")
+    if scales.dtype != biases.dtype:
+        raise HgkError(1, "scales and biases must share a dtype")
     K = x.shape[-1]
     N = w.shape[0]
     lead = x.shape[:-1]

@@ -160,3 +160,26 @@ def test_python_mirror_raises_on_missing_library(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "LIB_PATH", str(tmp_path / "missing.so"))
     with pytest.raises(_lib.HgkError):
         _lib.lib()
+
+
+def test_python_mirror_rejects_mixed_scale_and_bias_dtypes():
+    """One scales dtype reaches the kernels for every scale and bias, so the
+    host API refuses operands whose scales and biases disagree before any
+    device work (the fused gate + up + SwiGLU compares all four)."""
+    import torch
+
+    import higgs_amd as H
+
+    E, N, K, T, k = 4, 64, 512, 2, 2
+    w = torch.zeros((E, N, K // 8), dtype=torch.int32)
+    s16 = torch.zeros((E, N, K // 64), dtype=torch.bfloat16)
+    h16 = torch.zeros((E, N, K // 64), dtype=torch.float16)
+    x = torch.zeros((T, K), dtype=torch.bfloat16)
+    idx = torch.zeros((T * k,), dtype=torch.int32)
+    for sg, bg, su, bu in ((s16, s16, h16, h16), (s16, s16, s16, h16), (s16, h16, s16, s16)):
+        with pytest.raises(_lib.HgkError, match="dtype"):
+            H.gather_qmm_swiglu(x, w, sg, bg, w, su, bu, idx, x_row_div=k)
+    with pytest.raises(_lib.HgkError, match="share a dtype"):
+        H.gather_qmm(x, w, s16, h16, idx, x_row_div=k)
+    with pytest.raises(_lib.HgkError, match="share a dtype"):
+        H.quantized_matmul(x, w[0], s16[0], h16[0])

@@ -37,6 +37,9 @@ RMS_CASES = [
     (96, 4096, O.BF16, O.BF16, False, O.BF16, 1e-6),      # Qwen3-8B hidden
     (64, 3584, O.BF16, O.BF16, True, O.F32, 1e-6),        # Gemma (1+w), promoted f32 out
     (64, 3584, O.BF16, O.BF16, True, O.BF16, 1e-6),       # Gemma (1+w), bf16 out
+    (40, 4608, O.BF16, O.BF16, True, O.F32, 1e-6),        # Gemma-2-27B (1+w): 16-byte units
+    (40, 5376, O.BF16, O.BF16, True, O.F32, 1e-6),        # Gemma-3-27B (1+w): 16-byte units
+    (24, 8192, O.F16, O.F32, False, O.F32, 1e-5),         # f32 weight, f32 out, 16 units/lane
     (64, 2048, O.F32, O.F32, False, O.F32, 1e-5),
     (64, 2048, O.F16, O.F16, False, O.F16, 1e-5),
     (64, 2048, O.BF16, O.F32, False, O.F32, 1e-5),        # f32 weight promotes
@@ -488,7 +491,7 @@ def _bits16(key, shape, sdt, exp_lo, exp_hi, zero_frac=0.0):
 
 
 @pytest.mark.parametrize("sdt", [O.BF16, O.F16])
-@pytest.mark.parametrize("out_scale", [0.0, math.sqrt(3584.0)])
+@pytest.mark.parametrize("out_scale", [0.0, math.sqrt(3584.0), -math.sqrt(3584.0), -0.75])
 def test_qembed_any_scale_and_bias_values(dev, sdt, out_scale):
     """Rows whose scales and biases span every exponent the dot2 form takes
     (bf16: scales of either sign from 2^-100 to 2^100, biases +-0 or from
@@ -496,11 +499,12 @@ def test_qembed_any_scale_and_bias_values(dev, sdt, out_scale):
     normal scales below 2^12, biases below 2^11), rows of arbitrary 16-bit
     codes (zeros, subnormals, huge values, inf, NaN: those rows take the
     element-by-element form and overflow) and ordinary rows, with and without
-    the output scale. Bit-exact against the oracle (NaN positions compared as
-    a mask)."""
+    the output scale, positive or negative (a negative one turns row 7's +0
+    elements into -0). Bit-exact against the oracle, zero signs included (NaN
+    positions compared as a mask)."""
     V, Hd, n = 1536, 2048, 3000
     G = Hd // 64
-    key = 1950 + 10 * sdt + int(out_scale > 0)
+    key = 1950 + 10 * sdt + int(out_scale > 0) + 2 * int(out_scale < 0)
     wq = O.u32(key, (V, Hd // 8))
     s = O.from_f32(O.uniform(key + 1, (V, G), 0.005, 0.02), sdt)
     b = O.from_f32(O.uniform(key + 2, (V, G), -0.1, 0.1), sdt)
