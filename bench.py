@@ -49,9 +49,11 @@ class Kernel:
     back to torch's caching allocator, and graph capture (which empties that
     cache) would unmap it under the launches."""
 
-    def __init__(self, name, nbytes, fn, argsets, tokens=0, keep=(), cpu=None, flops=0):
+    def __init__(self, name, nbytes, fn, argsets, tokens=0, keep=(), cpu=None, flops=0,
+                 wbytes=None):
         self.name, self.bytes, self.fn, self.tokens = name, nbytes, fn, tokens
         self.flops = flops  # MFMA-bound kernels: algorithmic flops per launch
+        self.wbytes = wbytes  # of `bytes`, those written (the rest are read)
         self.argsets = [tuple(a) for a in argsets]
         self.keep = keep
         self.cpu = cpu  # (kind, params) for the oracle's timing of the same op
@@ -157,7 +159,8 @@ def k_embed(cx, name, sets, tabs, V, Hd, n, scale=0.0, group=64):
         args.append((_vp(ids), I32, n, _vp(wq), _vp(sc), _vp(bi), BF16, V, Hd, group, 4,
                      _f(scale), _vp(out), Hd, cx.stream))
     return Kernel(name, nbytes, cx.lib.hgk_quantized_embedding, args, n, keep=(sets, tabs),
-                  cpu=("qembed", dict(V=V, H=Hd, n=n, scale=scale, group=group)))
+                  cpu=("qembed", dict(V=V, H=Hd, n=n, scale=scale, group=group)),
+                  wbytes=n * Hd * 2)
 
 
 def k_rmsnorm(cx, name, sets, w, rows, n, eps, plus_one=0, ydt=BF16):
@@ -165,7 +168,8 @@ def k_rmsnorm(cx, name, sets, w, rows, n, eps, plus_one=0, ydt=BF16):
     args = [(_vp(x), BF16, n, _vp(w), BF16, plus_one, _f(eps), _vp(y), ydt, n, rows, n,
              cx.stream) for x, y in sets]
     return Kernel(name, nbytes, cx.lib.hgk_rms_norm, args, rows, keep=(sets, w),
-                  cpu=("rms", dict(rows=rows, n=n, eps=eps, plus_one=plus_one, ydt=ydt)))
+                  cpu=("rms", dict(rows=rows, n=n, eps=eps, plus_one=plus_one, ydt=ydt)),
+                  wbytes=rows * n * (4 if ydt == F32 else 2))
 
 
 def k_embed_norm(cx, name, sets, tabs, w, V, Hd, n, eps, scale=0.0, group=64, plus_one=0,
@@ -182,7 +186,8 @@ def k_embed_norm(cx, name, sets, tabs, w, V, Hd, n, eps, scale=0.0, group=64, pl
                      cx.stream))
     return Kernel(name, nbytes, cx.lib.hgk_quantized_embedding_rms_norm, args, n,
                   keep=(sets, tabs, w),
-                  cpu=("qembed_rms", dict(V=V, H=Hd, n=n, scale=scale, group=group, eps=eps)))
+                  cpu=("qembed_rms", dict(V=V, H=Hd, n=n, scale=scale, group=group, eps=eps)),
+                  wbytes=n * Hd * (2 + (4 if ydt == F32 else 2)))
 
 
 def k_add_rmsnorm(cx, name, sets, w, rows, n, eps):
@@ -191,7 +196,7 @@ def k_add_rmsnorm(cx, name, sets, w, rows, n, eps):
     args = [(BF16, _vp(x), n, _vp(r), n, _vp(w), BF16, 0, _f(eps), _vp(h), n, _vp(y), BF16, n,
              rows, n, cx.stream) for x, r, h, y in sets]
     return Kernel(name, nbytes, cx.lib.hgk_add_rms_norm, args, rows, keep=(sets, w),
-                  cpu=("add_rms", dict(rows=rows, n=n, eps=eps)))
+                  cpu=("add_rms", dict(rows=rows, n=n, eps=eps)), wbytes=2 * rows * n * 2)
 
 
 def k_glu(cx, name, sets, rows, n, act, ydt=BF16):
@@ -199,7 +204,8 @@ def k_glu(cx, name, sets, rows, n, act, ydt=BF16):
     args = [(act, BF16, _vp(g), n, _vp(u), n, _vp(o), ydt, n, rows, n, cx.stream)
             for g, u, o in sets]
     return Kernel(name, nbytes, cx.lib.hgk_glu, args, rows, keep=(sets,),
-                  cpu=("glu", dict(rows=rows, n=n, act=act, ydt=ydt)))
+                  cpu=("glu", dict(rows=rows, n=n, act=act, ydt=ydt)),
+                  wbytes=rows * n * (4 if ydt == F32 else 2))
 
 
 def k_qkrope(cx, name, sets, B, L, Hq, Hk, D, dims, base, freqs=None, wq=None, wk=None,
@@ -225,7 +231,8 @@ def k_qkrope(cx, name, sets, B, L, Hq, Hk, D, dims, base, freqs=None, wq=None, w
                   keep=(sets, wq, wk, offsets, fr, qs, ks, qos, kos),
                   cpu=("rope", dict(B=B, L=L, Hq=Hq, Hk=Hk, D=D, dims=dims, base=base,
                                     freqs=freqs, norm=wq is not None, eps=eps,
-                                    offsets=offsets is not None)))
+                                    offsets=offsets is not None)),
+                  wbytes=B * L * (Hq + Hk) * D * 2)
 
 
 def k_gated(cx, name, sets, w, rows, n, eps, zrow, zgroup, zgs):
@@ -233,7 +240,7 @@ def k_gated(cx, name, sets, w, rows, n, eps, zrow, zgroup, zgs):
     args = [(BF16, _vp(y), n, _vp(z), zrow, zgroup, zgs, _vp(w), BF16, _f(eps), _vp(o), BF16,
              n, rows, n, cx.stream) for y, z, o in sets]
     return Kernel(name, nbytes, cx.lib.hgk_gated_rms_norm, args, rows, keep=(sets, w),
-                  cpu=("gated", dict(rows=rows, n=n, eps=eps)))
+                  cpu=("gated", dict(rows=rows, n=n, eps=eps)), wbytes=rows * n * 2)
 
 
 def wl_llama_chain(cx):
@@ -862,7 +869,74 @@ def kernel_times(cx, wl, graph, per_group=20, groups=5):
             cu = copy_floor(cx, k.bytes, per_group, groups)
             per[-1]["copy_us"] = cu
             per[-1]["copy_over_kernel"] = cu / (avg * 1e3)
+            if k.wbytes is not None:
+                # the measured floors: an empty kernel at this kernel's own
+                # grid, and the streaming kernel at its read:write split
+                blocks, threads = launch_grid(cx, k)
+                per[-1]["grid"] = [blocks, threads]
+                per[-1]["empty_us"] = empty_floor(cx, blocks, threads, per_group, groups)
+                su = stream_floor(cx, k.bytes - k.wbytes, k.wbytes, per_group, groups)
+                per[-1]["stream_us"] = su
+                per[-1]["stream_over_kernel"] = su / (avg * 1e3)
     return per
+
+
+def launch_grid(cx, k):
+    """(workgroups, threads per workgroup) of one launch of kernel k, as the
+    library noted it."""
+    k.launch(0)
+    blocks, threads = C.c_int64(), C.c_int()
+    cx.check(cx.lib.hgk_last_launch_grid(C.byref(blocks), C.byref(threads)))
+    cx.torch.cuda.synchronize()
+    return blocks.value, threads.value
+
+
+def _time_groups(cx, go, per_group, groups):
+    """Average duration of one of `per_group` back-to-back launches made by
+    go(), over `groups` groups bracketed by HIP events on the bench stream."""
+    torch = cx.torch
+    he = HipEvents()
+    go()
+    torch.cuda.synchronize()
+    evs = he.create(groups + 1)
+    he.h.hipEventRecord(evs[0], cx.stream)
+    for i in range(groups):
+        go()
+        he.h.hipEventRecord(evs[i + 1], cx.stream)
+    torch.cuda.synchronize()
+    d = [he.elapsed_ms(evs[i], evs[i + 1]) / per_group for i in range(groups)]
+    he.destroy(evs)
+    return sum(d) / len(d) * 1e3
+
+
+def empty_floor(cx, blocks, threads, per_group=20, groups=5):
+    """Average duration of an empty kernel over the given grid: launch,
+    dispatch and drain of that many workgroups with no work in them."""
+    def go():
+        for _ in range(per_group):
+            cx.check(cx.lib.hgk_floor_empty(blocks, threads, cx.stream))
+    return _time_groups(cx, go, per_group, groups)
+
+
+def stream_floor(cx, read_bytes, write_bytes, per_group=20, groups=5):
+    """Average duration of the library's streaming kernel (16-byte lanes, four
+    units per thread, loads before stores, non-temporal stores, values
+    computed from the loaded ones) reading read_bytes and writing write_bytes,
+    source/destination pairs rotating over >= 1 GB."""
+    torch = cx.torch
+    rb = (int(read_bytes) + 15) // 16 * 16
+    wb = (int(write_bytes) + 15) // 16 * 16
+    npairs = max(2, math.ceil((1 << 30) / max(rb + wb, 1)))
+    bufs = [(cx.empty((max(rb, 16),), torch.uint8), cx.empty((max(wb, 16),), torch.uint8))
+            for _ in range(npairs)]
+
+    def go():
+        for i in range(per_group):
+            src, dst = bufs[i % npairs]
+            cx.check(cx.lib.hgk_floor_stream(_vp(src), rb, _vp(dst), wb, 4, cx.stream))
+    us = _time_groups(cx, go, per_group, groups)
+    del bufs
+    return us
 
 
 def copy_floor(cx, nbytes, per_group=20, groups=5):
@@ -1321,6 +1395,9 @@ def main(argv=None):
                 cpu_txt = (f"   cpu {cpu['gbs']:.2f} GB/s ({cpu['cores']} threads)" if cpu else "")
                 cp_txt = (f"   copy of the same bytes {k['copy_us']:.2f} us"
                           if "copy_us" in k else "")
+                if "stream_us" in k:
+                    cp_txt += (f"   stream {k['stream_us']:.2f} us   empty kernel "
+                               f"{k['empty_us']:.2f} us at {k['grid'][0]}x{k['grid'][1]}")
                 print(f"[table]    {k['kernel']:<24} {k['avg_us']:9.2f} us  {k['gbs']:7.0f} GB/s "
                       f"({k['frac_of_peak']:.1%}){cp_txt}{cpu_txt}", file=sys.stderr, flush=True)
         os.makedirs("gpurun_out", exist_ok=True)

@@ -68,6 +68,9 @@ PROTOTYPES = {
     "hgk_st_upload": (_int, [_vp, _i64, _vp, _i64, _vp]),
     "hgk_st_collect_files": (_int, [C.c_char_p, C.c_char_p, _i64, C.POINTER(_i64)]),
     "hgk_remap_quantized_key": (_int, [C.c_char_p, C.c_char_p, _i64]),
+    "hgk_last_launch_grid": (_int, [_i64p, C.POINTER(_int)]),
+    "hgk_floor_empty": (_int, [_i64, _int, _vp]),
+    "hgk_floor_stream": (_int, [_vp, _i64, _vp, _i64, _int, _vp]),
 }
 
 

@@ -14,6 +14,13 @@ namespace hgk {
 
 namespace {
 thread_local char g_last_error[512] = {0};
+thread_local int64_t g_last_blocks = 0;
+thread_local int g_last_threads = 0;
+}
+
+void note_launch(dim3 grid, dim3 block) {
+  g_last_blocks = (int64_t)grid.x * grid.y * grid.z;
+  g_last_threads = (int)(block.x * block.y * block.z);
 }
 
 int fail(int status, const char* fmt, ...) {
@@ -57,6 +64,14 @@ using namespace hgk;
 extern "C" const char* hgk_last_error(void) { return g_last_error; }
 
 extern "C" int hgk_abi_version(void) { return HGK_ABI_VERSION; }
+
+extern "C" int hgk_last_launch_grid(int64_t* blocks, int* threads_per_block) {
+  clear_error();
+  if (!blocks || !threads_per_block) return fail(HGK_ERR_ARG, "hgk_last_launch_grid: null output");
+  *blocks = g_last_blocks;
+  *threads_per_block = g_last_threads;
+  return HGK_OK;
+}
 
 // The one blocking call of the library: waits for the work queued on
 // `stream` (NULL = the device's null stream) and reports an asynchronous

@@ -1246,10 +1246,10 @@ bool launch_decode(const GdnArgs& a, hipStream_t s) {
   constexpr int RPL = 4;
   const dim3 grid((unsigned)((a.Dv + 16 * RPL - 1) / (16 * RPL)), (unsigned)a.Hv, (unsigned)a.B);
   switch (a.Dk) {
-    case 32: hipLaunchKernelGGL((gated_delta_decode_kernel<X, 2, NORM, RPL>), grid, dim3(256), 0, s, a); return true;
-    case 64: hipLaunchKernelGGL((gated_delta_decode_kernel<X, 4, NORM, RPL>), grid, dim3(256), 0, s, a); return true;
-    case 128: hipLaunchKernelGGL((gated_delta_decode_kernel<X, 8, NORM, RPL>), grid, dim3(256), 0, s, a); return true;
-    case 256: hipLaunchKernelGGL((gated_delta_decode_kernel<X, 16, NORM, RPL>), grid, dim3(256), 0, s, a); return true;
+    case 32: HGK_LAUNCH((gated_delta_decode_kernel<X, 2, NORM, RPL>), grid, dim3(256), 0, s, a); return true;
+    case 64: HGK_LAUNCH((gated_delta_decode_kernel<X, 4, NORM, RPL>), grid, dim3(256), 0, s, a); return true;
+    case 128: HGK_LAUNCH((gated_delta_decode_kernel<X, 8, NORM, RPL>), grid, dim3(256), 0, s, a); return true;
+    case 256: HGK_LAUNCH((gated_delta_decode_kernel<X, 16, NORM, RPL>), grid, dim3(256), 0, s, a); return true;
     default: return false;
   }
 }
@@ -1260,10 +1260,10 @@ bool launch_token_p(const GdnArgs& a, hipStream_t s) {
   const dim3 grid((unsigned)((a.Dv + ROWS - 1) / ROWS), (unsigned)a.Hv, (unsigned)a.B);
   const dim3 block(64 * WPB);
   switch (a.Dk) {
-    case 32: hipLaunchKernelGGL((gated_delta_token_kernel<X, P, 2, NORM, RPL>), grid, block, 0, s, a); return true;
-    case 64: hipLaunchKernelGGL((gated_delta_token_kernel<X, P, 4, NORM, RPL>), grid, block, 0, s, a); return true;
-    case 128: hipLaunchKernelGGL((gated_delta_token_kernel<X, P, 8, NORM, RPL>), grid, block, 0, s, a); return true;
-    case 256: hipLaunchKernelGGL((gated_delta_token_kernel<X, P, 16, NORM, RPL>), grid, block, 0, s, a); return true;
+    case 32: HGK_LAUNCH((gated_delta_token_kernel<X, P, 2, NORM, RPL>), grid, block, 0, s, a); return true;
+    case 64: HGK_LAUNCH((gated_delta_token_kernel<X, P, 4, NORM, RPL>), grid, block, 0, s, a); return true;
+    case 128: HGK_LAUNCH((gated_delta_token_kernel<X, P, 8, NORM, RPL>), grid, block, 0, s, a); return true;
+    case 256: HGK_LAUNCH((gated_delta_token_kernel<X, P, 16, NORM, RPL>), grid, block, 0, s, a); return true;
     default: return false;
   }
 }
@@ -1278,9 +1278,9 @@ bool launch_token_gn(const GdnArgs& a, hipStream_t s) {
   const dim3 block(64 * WPB);
   const bool p32 = a.pdt == DT_F32;
 #define HGK_GDN_GN(NPT)                                                                          \
-  if (p32) hipLaunchKernelGGL((gated_delta_token_kernel<X, F32, NPT, NORM, RPL, true>), grid,    \
-                              block, 0, s, a);                                                   \
-  else hipLaunchKernelGGL((gated_delta_token_kernel<X, X, NPT, NORM, RPL, true>), grid, block,  \
+  if (p32) HGK_LAUNCH((gated_delta_token_kernel<X, F32, NPT, NORM, RPL, true>), grid,    \
+                      block, 0, s, a);                                                   \
+  else HGK_LAUNCH((gated_delta_token_kernel<X, X, NPT, NORM, RPL, true>), grid, block,  \
                           0, s, a);                                                              \
   return true;
   switch (a.Dk) {
@@ -1308,10 +1308,10 @@ template <class X, bool NORM>
 bool launch_rows(const GdnArgs& a, hipStream_t s) {
   const dim3 grid((unsigned)((a.Dv + 7) / 8), (unsigned)a.Hv, (unsigned)a.B);
   switch (a.Dk) {
-    case 32: hipLaunchKernelGGL((gated_delta_row_kernel<X, 1, NORM>), grid, dim3(256), 0, s, a); return true;
-    case 64: hipLaunchKernelGGL((gated_delta_row_kernel<X, 2, NORM>), grid, dim3(256), 0, s, a); return true;
-    case 128: hipLaunchKernelGGL((gated_delta_row_kernel<X, 4, NORM>), grid, dim3(256), 0, s, a); return true;
-    case 256: hipLaunchKernelGGL((gated_delta_row_kernel<X, 8, NORM>), grid, dim3(256), 0, s, a); return true;
+    case 32: HGK_LAUNCH((gated_delta_row_kernel<X, 1, NORM>), grid, dim3(256), 0, s, a); return true;
+    case 64: HGK_LAUNCH((gated_delta_row_kernel<X, 2, NORM>), grid, dim3(256), 0, s, a); return true;
+    case 128: HGK_LAUNCH((gated_delta_row_kernel<X, 4, NORM>), grid, dim3(256), 0, s, a); return true;
+    case 256: HGK_LAUNCH((gated_delta_row_kernel<X, 8, NORM>), grid, dim3(256), 0, s, a); return true;
     default: return false;
   }
 }
@@ -1320,10 +1320,10 @@ template <class X, bool NORM>
 bool launch_chunks(const GdnArgs& a, hipStream_t s) {
   const dim3 grid((unsigned)((a.Dv + kRows - 1) / kRows), (unsigned)a.Hv, (unsigned)a.B);
   switch (a.Dk) {
-    case 32: hipLaunchKernelGGL((gated_delta_chunk_kernel<X, 2, NORM>), grid, dim3(256), 0, s, a); return true;
-    case 64: hipLaunchKernelGGL((gated_delta_chunk_kernel<X, 4, NORM>), grid, dim3(256), 0, s, a); return true;
-    case 128: hipLaunchKernelGGL((gated_delta_chunk_kernel<X, 8, NORM>), grid, dim3(256), 0, s, a); return true;
-    case 256: hipLaunchKernelGGL((gated_delta_chunk_kernel<X, 16, NORM>), grid, dim3(256), 0, s, a); return true;
+    case 32: HGK_LAUNCH((gated_delta_chunk_kernel<X, 2, NORM>), grid, dim3(256), 0, s, a); return true;
+    case 64: HGK_LAUNCH((gated_delta_chunk_kernel<X, 4, NORM>), grid, dim3(256), 0, s, a); return true;
+    case 128: HGK_LAUNCH((gated_delta_chunk_kernel<X, 8, NORM>), grid, dim3(256), 0, s, a); return true;
+    case 256: HGK_LAUNCH((gated_delta_chunk_kernel<X, 16, NORM>), grid, dim3(256), 0, s, a); return true;
     default: return false;
   }
 }
@@ -1348,7 +1348,7 @@ bool launch_x(const GdnArgs& a, hipStream_t s, bool aligned) {
   if constexpr (X::kCode == DT_BF16 && NORM) {
     if (wy_fits(a)) {
       const dim3 grid((unsigned)(a.Dv / kWyRows), (unsigned)a.Hv, (unsigned)a.B);
-      hipLaunchKernelGGL(gated_delta_wy_kernel, grid, dim3(512), 0, s, a);
+      HGK_LAUNCH(gated_delta_wy_kernel, grid, dim3(512), 0, s, a);
       return true;
     }
   }

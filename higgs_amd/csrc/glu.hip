@@ -191,12 +191,12 @@ void launch(const GluArgs& a0, bool vec_ok, int64_t rows, int64_t n, hipStream_t
       a.total = (uint32_t)(rows * (n / 4));
       if (a.total >= 256u * 4u * 1024u) {
         const unsigned blocks = (a.total + 1024u - 1u) / 1024u;
-        if (a.contig) hipLaunchKernelGGL((glu_wide_kernel<X, Y, ACT, 4, true>), dim3(blocks), dim3(256), 0, s, a);
-        else hipLaunchKernelGGL((glu_wide_kernel<X, Y, ACT, 4, false>), dim3(blocks), dim3(256), 0, s, a);
+        if (a.contig) HGK_LAUNCH((glu_wide_kernel<X, Y, ACT, 4, true>), dim3(blocks), dim3(256), 0, s, a);
+        else HGK_LAUNCH((glu_wide_kernel<X, Y, ACT, 4, false>), dim3(blocks), dim3(256), 0, s, a);
       } else {
         const unsigned blocks = (a.total + 511u) / 512u;
-        if (a.contig) hipLaunchKernelGGL((glu_wide_kernel<X, Y, ACT, 2, true>), dim3(blocks), dim3(256), 0, s, a);
-        else hipLaunchKernelGGL((glu_wide_kernel<X, Y, ACT, 2, false>), dim3(blocks), dim3(256), 0, s, a);
+        if (a.contig) HGK_LAUNCH((glu_wide_kernel<X, Y, ACT, 2, true>), dim3(blocks), dim3(256), 0, s, a);
+        else HGK_LAUNCH((glu_wide_kernel<X, Y, ACT, 2, false>), dim3(blocks), dim3(256), 0, s, a);
       }
       return;
     }
@@ -205,18 +205,18 @@ void launch(const GluArgs& a0, bool vec_ok, int64_t rows, int64_t n, hipStream_t
   if (vec_ok) {
     if (a.total >= 256u * 4u * 1024u) {
       const unsigned blocks = (a.total + 1024u - 1u) / 1024u;
-      if (a.contig) hipLaunchKernelGGL((glu_kernel<X, Y, ACT, 4, true>), dim3(blocks), dim3(256), 0, s, a);
-      else hipLaunchKernelGGL((glu_kernel<X, Y, ACT, 4, false>), dim3(blocks), dim3(256), 0, s, a);
+      if (a.contig) HGK_LAUNCH((glu_kernel<X, Y, ACT, 4, true>), dim3(blocks), dim3(256), 0, s, a);
+      else HGK_LAUNCH((glu_kernel<X, Y, ACT, 4, false>), dim3(blocks), dim3(256), 0, s, a);
     } else {
       const unsigned blocks = (a.total + 255u) / 256u;
-      if (a.contig) hipLaunchKernelGGL((glu_kernel<X, Y, ACT, 1, true>), dim3(blocks), dim3(256), 0, s, a);
-      else hipLaunchKernelGGL((glu_kernel<X, Y, ACT, 1, false>), dim3(blocks), dim3(256), 0, s, a);
+      if (a.contig) HGK_LAUNCH((glu_kernel<X, Y, ACT, 1, true>), dim3(blocks), dim3(256), 0, s, a);
+      else HGK_LAUNCH((glu_kernel<X, Y, ACT, 1, false>), dim3(blocks), dim3(256), 0, s, a);
     }
     return;
   }
   const int64_t blocks = std::min<int64_t>((n * rows + 255) / 256, (int64_t)1 << 20);
-  hipLaunchKernelGGL((glu_generic_kernel<X, Y, ACT>), dim3((unsigned)blocks), dim3(256), 0, s,
-                     a, n, rows);
+  HGK_LAUNCH((glu_generic_kernel<X, Y, ACT>), dim3((unsigned)blocks), dim3(256), 0, s,
+             a, n, rows);
 }
 
 template <int ACT>

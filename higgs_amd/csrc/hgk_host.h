@@ -42,4 +42,20 @@ inline int promote(int a, int b) { return a == b ? a : 0; }
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
+// Remember the grid of the launch about to be made by this thread
+// (hgk_last_launch_grid reports it).
+void note_launch(dim3 grid, dim3 block);
+
+}  // namespace hgk
+
+// Every kernel launch of the library goes through this: the launch, with its
+// grid noted first.
+#define HGK_LAUNCH(kernel, grid, block, shmem, stream, ...)                 \
+  do {                                                                      \
+    ::hgk::note_launch(dim3(grid), dim3(block));                            \
+    hipLaunchKernelGGL(kernel, grid, block, shmem, stream, ##__VA_ARGS__);  \
+  } while (0)
+
+namespace hgk {
+
 }  // namespace hgk

@@ -231,16 +231,16 @@ void launch_fast(const NormArgs& a, hipStream_t s) {
   const int64_t waves = (a.rows + RPW - 1) / RPW;
   const int wpb = waves >= 4096 ? 4 : 1;  // small problems: spread over CUs
   const int64_t blocks = (waves + wpb - 1) / wpb;
-  hipLaunchKernelGGL((rms_norm_kernel<X, Y, W, LPR, CPL, MODE, UB>),
-                     dim3((unsigned)blocks), dim3(64 * wpb), 0, s, a);
+  HGK_LAUNCH((rms_norm_kernel<X, Y, W, LPR, CPL, MODE, UB>),
+             dim3((unsigned)blocks), dim3(64 * wpb), 0, s, a);
 }
 
 template <class X, class Y, int MODE>
 void launch_generic(const NormArgs& a, hipStream_t s) {
   const int wpb = a.rows >= 4096 ? 4 : 1;
   const int64_t blocks = (a.rows + wpb - 1) / wpb;
-  hipLaunchKernelGGL((rms_norm_generic_kernel<X, Y, MODE>), dim3((unsigned)blocks),
-                     dim3(64 * wpb), 0, s, a);
+  HGK_LAUNCH((rms_norm_generic_kernel<X, Y, MODE>), dim3((unsigned)blocks),
+             dim3(64 * wpb), 0, s, a);
 }
 
 // Pick (LPR, CPL) for a row of `nchunks` units; false -> generic.

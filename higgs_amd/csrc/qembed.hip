@@ -447,12 +447,12 @@ void launch_fast(const QembArgs& a, int steps, hipStream_t s) {
   const int wpb = a.n >= 1024 ? 4 : 1;
   const int64_t waves = std::min<int64_t>(a.n, (int64_t)resident_waves());
   const dim3 g((unsigned)((waves + wpb - 1) / wpb)), b(64 * wpb);
-  if (steps <= 1) hipLaunchKernelGGL((qembed_kernel<S, 1, PERM>), g, b, 0, s, a);
-  else if (steps <= 2) hipLaunchKernelGGL((qembed_kernel<S, 2, PERM>), g, b, 0, s, a);
-  else if (steps <= 4) hipLaunchKernelGGL((qembed_kernel<S, 4, PERM>), g, b, 0, s, a);
-  else if (steps <= 7) hipLaunchKernelGGL((qembed_kernel<S, 7, PERM>), g, b, 0, s, a);
-  else if (steps <= 8) hipLaunchKernelGGL((qembed_kernel<S, 8, PERM>), g, b, 0, s, a);
-  else hipLaunchKernelGGL((qembed_kernel<S, 16, PERM>), g, b, 0, s, a);
+  if (steps <= 1) HGK_LAUNCH((qembed_kernel<S, 1, PERM>), g, b, 0, s, a);
+  else if (steps <= 2) HGK_LAUNCH((qembed_kernel<S, 2, PERM>), g, b, 0, s, a);
+  else if (steps <= 4) HGK_LAUNCH((qembed_kernel<S, 4, PERM>), g, b, 0, s, a);
+  else if (steps <= 7) HGK_LAUNCH((qembed_kernel<S, 7, PERM>), g, b, 0, s, a);
+  else if (steps <= 8) HGK_LAUNCH((qembed_kernel<S, 8, PERM>), g, b, 0, s, a);
+  else HGK_LAUNCH((qembed_kernel<S, 16, PERM>), g, b, 0, s, a);
 }
 
 template <class S>
@@ -464,7 +464,7 @@ void launch(const QembArgs& a, bool vec_ok, bool perm_ok, hipStream_t s) {
     return;
   }
   const int64_t blocks = std::min<int64_t>((a.n * a.hidden + 255) / 256, (int64_t)1 << 20);
-  hipLaunchKernelGGL((qembed_generic_kernel<S>), dim3((unsigned)blocks), dim3(256), 0, s, a);
+  HGK_LAUNCH((qembed_generic_kernel<S>), dim3((unsigned)blocks), dim3(256), 0, s, a);
 }
 
 }  // namespace
@@ -526,12 +526,12 @@ bool launch_norm_fast(const QembArgs& a, hipStream_t s) {
   const int steps = (a.wpr + 63) / 64;
   const int wpb = a.n >= 1024 ? 4 : 1;
   const dim3 g((unsigned)((a.n + wpb - 1) / wpb)), b(64 * wpb);
-  if (steps <= 1) hipLaunchKernelGGL((qembed_norm_kernel<S, 1, W, Y>), g, b, 0, s, a);
-  else if (steps <= 2) hipLaunchKernelGGL((qembed_norm_kernel<S, 2, W, Y>), g, b, 0, s, a);
-  else if (steps <= 4) hipLaunchKernelGGL((qembed_norm_kernel<S, 4, W, Y>), g, b, 0, s, a);
-  else if (steps <= 7) hipLaunchKernelGGL((qembed_norm_kernel<S, 7, W, Y>), g, b, 0, s, a);
-  else if (steps <= 8) hipLaunchKernelGGL((qembed_norm_kernel<S, 8, W, Y>), g, b, 0, s, a);
-  else if (steps <= 16) hipLaunchKernelGGL((qembed_norm_kernel<S, 16, W, Y>), g, b, 0, s, a);
+  if (steps <= 1) HGK_LAUNCH((qembed_norm_kernel<S, 1, W, Y>), g, b, 0, s, a);
+  else if (steps <= 2) HGK_LAUNCH((qembed_norm_kernel<S, 2, W, Y>), g, b, 0, s, a);
+  else if (steps <= 4) HGK_LAUNCH((qembed_norm_kernel<S, 4, W, Y>), g, b, 0, s, a);
+  else if (steps <= 7) HGK_LAUNCH((qembed_norm_kernel<S, 7, W, Y>), g, b, 0, s, a);
+  else if (steps <= 8) HGK_LAUNCH((qembed_norm_kernel<S, 8, W, Y>), g, b, 0, s, a);
+  else if (steps <= 16) HGK_LAUNCH((qembed_norm_kernel<S, 16, W, Y>), g, b, 0, s, a);
   else return false;
   return true;
 }
@@ -543,8 +543,8 @@ void launch_norm(const QembArgs& a, bool vec_ok, hipStream_t s) {
     if (a.nwdt == DT_F32 && launch_norm_fast<S, F32, Y>(a, s)) return;
   }
   const int wpb = a.n >= 1024 ? 4 : 1;
-  hipLaunchKernelGGL((qembed_norm_generic_kernel<S, Y>), dim3((unsigned)((a.n + wpb - 1) / wpb)),
-                     dim3(64 * wpb), 0, s, a);
+  HGK_LAUNCH((qembed_norm_generic_kernel<S, Y>), dim3((unsigned)((a.n + wpb - 1) / wpb)),
+             dim3(64 * wpb), 0, s, a);
 }
 
 }  // namespace

@@ -1352,7 +1352,7 @@ void gather_xp_launch(const GatherArgs& a, hipStream_t s) {
   const int64_t tpg = (ntiles + gx - 1) / gx;
   gx = (ntiles + tpg - 1) / tpg;
   const dim3 grid((unsigned)gx, (unsigned)(a.E + 1));
-  hipLaunchKernelGGL((gather_xp_kernel<HGK_XP_RT, false>), grid, dim3(kXpT), 0, s, a);
+  HGK_LAUNCH((gather_xp_kernel<HGK_XP_RT, false>), grid, dim3(kXpT), 0, s, a);
 }
 
 bool gather_swiglu_grouped_launch(const GatherArgs& a, hipStream_t s) {
@@ -1365,7 +1365,7 @@ bool gather_swiglu_grouped_launch(const GatherArgs& a, hipStream_t s) {
   const int64_t tpg = (ntiles + gx - 1) / gx;
   gx = (ntiles + tpg - 1) / tpg;
   const dim3 grid((unsigned)gx, (unsigned)(a.E + 1));
-  hipLaunchKernelGGL((gather_xp_kernel<HGK_XP_RT, true>), grid, dim3(kXpT), 0, s, a);
+  HGK_LAUNCH((gather_xp_kernel<HGK_XP_RT, true>), grid, dim3(kXpT), 0, s, a);
   return true;
 }
 
@@ -1386,7 +1386,7 @@ void gather_grouped_launch(const GatherArgs& a, hipStream_t s) {
   gx = (ntiles + tpg - 1) / tpg;
   const dim3 grid((unsigned)gx, (unsigned)(a.E + 1));
   // 8 waves (2 per SIMD) measured 1.44x faster than 4 waves of 64 x 64 tiles
-  hipLaunchKernelGGL((gather_hl_kernel<8>), grid, dim3(512), 0, s, a);
+  HGK_LAUNCH((gather_hl_kernel<8>), grid, dim3(512), 0, s, a);
 }
 
 
@@ -1394,9 +1394,9 @@ template <int MT>
 void decode_launch_mt(const QgemmArgs& a, int nt, hipStream_t s) {
   const dim3 grid((unsigned)((a.N + 16 * nt - 1) / (16 * nt))), block(kDecThreads);
   switch (nt) {
-    case 1: hipLaunchKernelGGL((qgemm_decode_kernel<MT, 1, 1>), grid, block, 0, s, a); break;
-    case 2: hipLaunchKernelGGL((qgemm_decode_kernel<MT, 2, 1>), grid, block, 0, s, a); break;
-    default: hipLaunchKernelGGL((qgemm_decode_kernel<MT, 3, 1>), grid, block, 0, s, a); break;
+    case 1: HGK_LAUNCH((qgemm_decode_kernel<MT, 1, 1>), grid, block, 0, s, a); break;
+    case 2: HGK_LAUNCH((qgemm_decode_kernel<MT, 2, 1>), grid, block, 0, s, a); break;
+    default: HGK_LAUNCH((qgemm_decode_kernel<MT, 3, 1>), grid, block, 0, s, a); break;
   }
 }
 
@@ -1428,7 +1428,7 @@ void decode_launch(const QgemmArgs& a, hipStream_t s) {
     const int64_t tiles = (a.N + 16 * NT - 1) / (16 * NT);
     if (2 * tiles >= kCUs) {
       const dim3 grid((unsigned)(((tiles + 7) / 8) * 16)), block(kDecThreads);
-      hipLaunchKernelGGL((qgemm_decode_kernel<2, NT, 2>), grid, block, 0, s, a);
+      HGK_LAUNCH((qgemm_decode_kernel<2, NT, 2>), grid, block, 0, s, a);
       return;
     }
   }
@@ -1454,11 +1454,11 @@ void qgemm_launch(const QgemmArgs& a, hipStream_t s) {
   if (a.M <= 64 && decode_fits(a)) {
     decode_launch(a, s);
   } else if (a.M <= 512) {
-    hipLaunchKernelGGL(qgemm_kernel<64>, dim3(gx, (unsigned)((a.M + 63) / 64)), dim3(256), 0, s, a);
+    HGK_LAUNCH(qgemm_kernel<64>, dim3(gx, (unsigned)((a.M + 63) / 64)), dim3(256), 0, s, a);
   } else {
     // 8 waves of 64 x 64 measured faster than 4 waves of 128 x 64
-    hipLaunchKernelGGL((qgemm_hl_kernel<4, 4>), dim3(gx, (unsigned)((a.M + kHlBM - 1) / kHlBM)),
-                       dim3(512), 0, s, a);
+    HGK_LAUNCH((qgemm_hl_kernel<4, 4>), dim3(gx, (unsigned)((a.M + kHlBM - 1) / kHlBM)),
+               dim3(512), 0, s, a);
   }
 }
 

@@ -297,7 +297,7 @@ void launch_bf16_k(QmmArgs a, hipStream_t s) {
     a.p0 = p0;
     const int64_t np = a.pairs - p0 < 65535 ? a.pairs - p0 : 65535;
     const dim3 grid((unsigned)((a.N + 63) / 64), (unsigned)np);
-    hipLaunchKernelGGL((qmv_bf16_kernel<S, STEPS>), grid, dim3(256), 0, s, a);
+    HGK_LAUNCH((qmv_bf16_kernel<S, STEPS>), grid, dim3(256), 0, s, a);
   }
 }
 
@@ -318,7 +318,7 @@ void launch_swiglu_k(QmmArgs a, const uint32_t* wu, const void* su, const void* 
     a.p0 = p0;
     const int64_t np = a.pairs - p0 < 65535 ? a.pairs - p0 : 65535;
     const dim3 grid((unsigned)((a.N + 31) / 32), (unsigned)np);
-    hipLaunchKernelGGL((qmv_swiglu_bf16_kernel<BF16, STEPS>), grid, dim3(256), 0, s, a, wu, su, bu);
+    HGK_LAUNCH((qmv_swiglu_bf16_kernel<BF16, STEPS>), grid, dim3(256), 0, s, a, wu, su, bu);
   }
 }
 
@@ -327,7 +327,7 @@ void launch_generic(const QmmArgs& a, hipStream_t s) {
   const int64_t items = a.pairs * a.N;
   // a grid of at most 2^20 blocks (2^28 work-items), well inside HIP's limit
   const int64_t blocks = std::min<int64_t>((items + 3) / 4, (int64_t)1 << 20);
-  hipLaunchKernelGGL((qmv_generic_kernel<X, S>), dim3((unsigned)blocks), dim3(256), 0, s, a);
+  HGK_LAUNCH((qmv_generic_kernel<X, S>), dim3((unsigned)blocks), dim3(256), 0, s, a);
 }
 
 }  // namespace

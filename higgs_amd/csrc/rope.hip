@@ -575,9 +575,9 @@ void launch_fast(RopeArgs& a, hipStream_t s) {
   const unsigned blocks = (a.tokens + tpb - 1) / tpb;
   const size_t shmem = 2u * tpb * a.half * sizeof(float);
   if (fast_index_ok(a))
-    hipLaunchKernelGGL((rope_kernel<X, LPR, NORM, true>), dim3(blocks), dim3(256), shmem, s, a);
+    HGK_LAUNCH((rope_kernel<X, LPR, NORM, true>), dim3(blocks), dim3(256), shmem, s, a);
   else
-    hipLaunchKernelGGL((rope_kernel<X, LPR, NORM, false>), dim3(blocks), dim3(256), shmem, s, a);
+    HGK_LAUNCH((rope_kernel<X, LPR, NORM, false>), dim3(blocks), dim3(256), shmem, s, a);
 }
 
 template <class X, int LPR, int R, bool NORM>
@@ -591,9 +591,9 @@ void launch_lane(RopeArgs& a, hipStream_t s) {
   const unsigned blocks = (a.tokens + tpb - 1) / tpb;
   const size_t shmem = 2u * tpb * a.half * sizeof(float);
   if (fast_index_ok(a))
-    hipLaunchKernelGGL((rope_lane_kernel<X, LPR, R, NORM, true>), dim3(blocks), dim3(256), shmem, s, a);
+    HGK_LAUNCH((rope_lane_kernel<X, LPR, R, NORM, true>), dim3(blocks), dim3(256), shmem, s, a);
   else
-    hipLaunchKernelGGL((rope_lane_kernel<X, LPR, R, NORM, false>), dim3(blocks), dim3(256), shmem, s, a);
+    HGK_LAUNCH((rope_lane_kernel<X, LPR, R, NORM, false>), dim3(blocks), dim3(256), shmem, s, a);
 }
 
 template <class X, int LPR, bool NORM>
@@ -658,8 +658,8 @@ void launch_x(RopeArgs& a, bool vec_ok, hipStream_t s) {
   }
   const int64_t rows = (int64_t)a.tokens * a.hsum;
   const int wpb = 4;
-  hipLaunchKernelGGL((rope_generic_kernel<X, NORM>), dim3((unsigned)((rows + wpb - 1) / wpb)),
-                     dim3(64 * wpb), 0, s, a);
+  HGK_LAUNCH((rope_generic_kernel<X, NORM>), dim3((unsigned)((rows + wpb - 1) / wpb)),
+             dim3(64 * wpb), 0, s, a);
 }
 
 bool tensor_aligned(const void* x, const int64_t* st, int V) {

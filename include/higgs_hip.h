@@ -390,6 +390,24 @@ int hgk_st_collect_files(const char* model_dir, char* out, int64_t cap, int64_t*
  * the key has no quantized form. */
 int hgk_remap_quantized_key(const char* key, char* out, int64_t cap);
 
+/* ------------------------------------------------------------------------
+ * Measurement references (no counterpart in the reference: the benchmark's
+ * floors). They compute nothing; they time what a launch and a pure stream
+ * of bytes cost on this part, so that an op kernel's duration can be set
+ * beside them at its own grid and byte counts.
+ * ------------------------------------------------------------------------ */
+/* The grid of the last kernel the calling thread launched through this
+ * library: workgroups (x*y*z) and threads per workgroup (0, 0 before any). */
+int hgk_last_launch_grid(int64_t* blocks, int* threads_per_block);
+/* An empty kernel over `blocks` workgroups of `threads_per_block` threads. */
+int hgk_floor_empty(int64_t blocks, int threads_per_block, void* stream);
+/* Reads read_bytes from src and writes write_bytes to dst (both multiples of
+ * 16, 16-byte aligned buffers) in one pass: units_per_thread (1, 2, 4 or 8)
+ * 16-byte units per thread, all loads before the stores, non-temporal
+ * stores. The written bytes are a function of the read ones. */
+int hgk_floor_stream(const void* src, int64_t read_bytes, void* dst, int64_t write_bytes,
+                     int units_per_thread, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
