@@ -70,6 +70,9 @@ def lib():
             "or_norm_rope": (_i32, [_i32, _vp, _vp, _vp, _vp, _i64, _i64, _i64,
                                     _i64, _vp, _i32, _f32, _i32, _vp, _f32,
                                     C.c_int32, _vp]),
+            "or_norm_rope_trig": (_i32, [_i32, _vp, _vp, _vp, _vp, _i64, _i64, _i64,
+                                         _i64, _vp, _i32, _f32, _i32, _vp, _f32,
+                                         C.c_int32, _vp, _i32]),
             "or_glu": (_i32, [_i32, _i32, _vp, _i64, _vp, _i64, _vp, _i32, _i64,
                               _i64, _i64]),
             "or_gated_rms_norm": (_i32, [_i32, _vp, _i64, _vp, _i64, _vp, _i32,
@@ -262,11 +265,17 @@ def llama3_freqs(base, dims, factor, low, high, original_max_pos) -> np.ndarray:
     return f
 
 
+TRIG_LIBM, TRIG_F64 = 0, 1
+
+
 def norm_rope(x, x_dt, *, dims, inv_freq, scale=1.0, offset=0, offsets=None,
-              norm_w=None, w_dt=None, eps=1e-6, out=None, out_strides=None):
+              norm_w=None, w_dt=None, eps=1e-6, out=None, out_strides=None, trig=TRIG_LIBM):
     """x: 4-D storage array viewed as [B, L, H, D] (any element strides with a
     unit stride on D). Returns y, by default a contiguous [B, L, H, D] array;
-    pass ``out``/``out_strides`` (elements, for b/l/h) for other layouts."""
+    pass ``out``/``out_strides`` (elements, for b/l/h) for other layouts.
+    trig: TRIG_LIBM takes cos/sin from libm's f32 cosf/sinf (MLX's CPU rope),
+    TRIG_F64 the f32 rounding of f64 cos/sin of the same angle (the device's
+    evaluation)."""
     B, L, H, D = x.shape
     assert x.strides[3] == x.itemsize
     t = promote(x_dt, w_dt) if norm_w is not None else x_dt
@@ -279,9 +288,9 @@ def norm_rope(x, x_dt, *, dims, inv_freq, scale=1.0, offset=0, offsets=None,
     inv = np.ascontiguousarray(inv_freq, np.float32)
     offs = None if offsets is None else np.ascontiguousarray(offsets, np.int32)
     base_ptr = x.__array_interface__["data"][0]
-    _check(lib().or_norm_rope(x_dt, C.c_void_p(base_ptr), _p(xs), _p(out), _p(ys),
-                              B, L, H, D, _p(norm_w), 0 if w_dt is None else w_dt,
-                              eps, dims, _p(inv), scale, offset, _p(offs)),
+    _check(lib().or_norm_rope_trig(x_dt, C.c_void_p(base_ptr), _p(xs), _p(out), _p(ys),
+                                   B, L, H, D, _p(norm_w), 0 if w_dt is None else w_dt,
+                                   eps, dims, _p(inv), scale, offset, _p(offs), trig),
            "norm_rope")
     return out
 

@@ -311,6 +311,30 @@ int or_norm_rope(int x_dt, const void* x, const int64_t xs[3], void* y,
                  const void* norm_w, int w_dt, float eps, int dims,
                  const float* inv_freq, float scale, int32_t offset,
                  const int32_t* offsets) {
+  return or_norm_rope_trig(x_dt, x, xs, y, ys, B, L, H, D, norm_w, w_dt, eps, dims, inv_freq,
+                           scale, offset, offsets, OR_TRIG_LIBM);
+}
+
+/* cos/sin of the f32 angle th: libm's f32 cosf/sinf (MLX's CPU evaluation),
+ * or the f32 rounding of the f64 cos/sin of th (the device kernels' choice).
+ * The two agree except where the f32 functions miss the correctly rounded
+ * value by their last bit. */
+static inline void rope_trig(float th, int trig, float* c, float* s) {
+  if (trig == OR_TRIG_F64) {
+    *c = (float)cos((double)th);
+    *s = (float)sin((double)th);
+  } else {
+    *c = cosf(th);
+    *s = sinf(th);
+  }
+}
+
+int or_norm_rope_trig(int x_dt, const void* x, const int64_t xs[3], void* y,
+                      const int64_t ys[3], int64_t B, int64_t L, int64_t H, int64_t D,
+                      const void* norm_w, int w_dt, float eps, int dims,
+                      const float* inv_freq, float scale, int32_t offset,
+                      const int32_t* offsets, int trig) {
+  if (trig != OR_TRIG_LIBM && trig != OR_TRIG_F64) return 1;
   if (!x || !y || !inv_freq || B < 0 || L < 0 || H < 0 || D <= 0) return 1;
   if (dims <= 0 || dims > D || (dims & 1)) return 1;
   if (D > 4096 || dims > 1024) return 2; /* per-thread scratch rows below */
@@ -326,9 +350,10 @@ int or_norm_rope(int x_dt, const void* x, const int64_t xs[3], void* y,
       int32_t off = offsets ? offsets[b] : offset;
       float pos = ((float)l + (float)off) * scale;
       for (int i = 0; i < half; ++i) {
-        float th = pos * inv_freq[i];
-        cs[i] = rnd(cosf(th), t);
-        sn[i] = rnd(sinf(th), t);
+        float th = pos * inv_freq[i], c, sv;
+        rope_trig(th, trig, &c, &sv);
+        cs[i] = rnd(c, t);
+        sn[i] = rnd(sv, t);
       }
       for (int64_t h = 0; h < H; ++h) {
         int64_t xb = b * xs[0] + l * xs[1] + h * xs[2];

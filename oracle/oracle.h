@@ -99,6 +99,18 @@ int or_norm_rope(int x_dt, const void* x, const int64_t xs[3],
                  int dims, const float* inv_freq, float scale,
                  int32_t offset, const int32_t* offsets);
 
+/* The same with a choice of cos/sin evaluation: OR_TRIG_LIBM is or_norm_rope
+ * (libm's f32 cosf/sinf, as MLX's CPU rope), OR_TRIG_F64 takes the f32
+ * rounding of the f64 cos/sin of the same f32 angle, the device kernels'
+ * evaluation. */
+enum { OR_TRIG_LIBM = 0, OR_TRIG_F64 = 1 };
+int or_norm_rope_trig(int x_dt, const void* x, const int64_t xs[3],
+                      void* y, const int64_t ys[3],
+                      int64_t B, int64_t L, int64_t H, int64_t D,
+                      const void* norm_w, int w_dt, float eps,
+                      int dims, const float* inv_freq, float scale,
+                      int32_t offset, const int32_t* offsets, int trig);
+
 int or_glu(int act, int x_dt, const void* gate, int64_t g_row_stride,
            const void* up, int64_t u_row_stride,
            void* out, int out_dt, int64_t o_row_stride,

@@ -71,3 +71,83 @@ def assert_close(got, ref, dt, *, max_ulp=1, what="", rtol=None, atol=None, max_
 
 def exact_frac(got, ref, dt) -> float:
     return float((ulp_dist(np.asarray(got), np.asarray(ref), dt) == 0).mean())
+
+
+def check_rope_parity(got, ref_libm, ref_dev, dt, what=""):
+    """The RoPE bar, with no allowance for stray elements.
+
+    ref_dev is the oracle with the device's cos/sin evaluation (f32 of f64
+    cos/sin); ref_libm the oracle with libm's f32 cosf/sinf, as MLX's CPU rope.
+    Against ref_dev every element must be within 1 ulp (or atol 1e-3) for
+    16-bit outputs, within rtol 1e-5 for f32. Against ref_libm every element
+    outside that bar must sit where the two oracles themselves differ, i.e.
+    where a cos/sin value rounds differently. Returns a one-line summary."""
+    got, ref_libm, ref_dev = np.asarray(got), np.asarray(ref_libm), np.asarray(ref_dev)
+    if dt == 0:
+        assert_close(got, ref_dev, dt, rtol=F32_RTOL, atol=0.0, what=what)
+        g = got.astype(np.float64)
+        r = ref_libm.astype(np.float64)
+        beyond = ~np.isclose(g, r, rtol=F32_RTOL, atol=0.0)
+        differ = ref_libm.view(np.uint32) != ref_dev.view(np.uint32)
+    else:
+        assert_close(got, ref_dev, dt, max_ulp=1, what=what)
+        import oracle
+
+        d = ulp_dist(got, ref_libm, dt)
+        diff = np.abs(oracle.to_f32(got, dt) - oracle.to_f32(ref_libm, dt))
+        beyond = (d > 1) & (diff > BF16_ATOL)
+        differ = ref_libm != ref_dev
+    unexplained = beyond & ~differ
+    worst = int(ulp_dist(got, ref_libm, dt)[beyond].max()) if beyond.any() else 0
+    assert not unexplained.any(), (
+        f"{what}: {int(unexplained.sum())} elements outside the bar against the libm oracle where "
+        f"the two oracles agree (first at {np.argwhere(unexplained)[0]})")
+    return (f"exact vs device-trig oracle {exact_frac(got, ref_dev, dt):.6f}, max ulp "
+            f"{int(ulp_dist(got, ref_dev, dt).max()) if got.size else 0}; vs libm oracle "
+            f"{int(beyond.sum())} of {got.size} beyond the bar (worst {worst} ulp), all where "
+            f"the oracles' cos/sin differ ({int(differ.sum())} such elements)")
+
+
+def check_geglu_f32(got, ref, g, u, what="", chunk=1 << 22):
+    """The f32 GeGLU bar. The reference composes 0.5 g (1 + tanh(k0 (g + k1
+    g^3))) u in f32; for negative g the sum 1 + tanh(.) cancels, and tanhf's
+    error (at most 2 ulp, 2^-23 near -1) comes through it as an absolute error
+    of up to 2^-24 |g u| in the reference's own value. The device evaluates g /
+    (1 + e^(-2x)), which does not cancel. Bar: every element within
+    rtol 1e-5 plus 2^-23 |g u| (twice that bound), and within rtol 1e-5 alone
+    wherever g >= -2 (where 1 + tanh >= 0.045, so the cancellation moves the
+    reference by less than 3e-6 relative). g and u are the f32 inputs.
+    Returns a one-line summary with the worst ratio to the bar."""
+    got, ref = np.asarray(got).reshape(-1), np.asarray(ref).reshape(-1)
+    g, u = np.asarray(g).reshape(-1), np.asarray(u).reshape(-1)
+    worst, worst_at, worst_mild, worst_neg, n_neg = 0.0, -1, 0.0, 0.0, 0
+    for lo in range(0, got.size, chunk):
+        sl = slice(lo, lo + chunk)
+        gg, uu = g[sl].astype(np.float64), u[sl].astype(np.float64)
+        r = ref[sl].astype(np.float64)
+        err = np.abs(got[sl].astype(np.float64) - r)
+        tol = F32_RTOL * np.abs(r) + 2.0 ** -23 * np.abs(gg * uu)
+        over = err > tol
+        assert not over.any(), (
+            f"{what}: {int(over.sum())} elements outside rtol 1e-5 + 2^-23|g u|, first at "
+            f"{lo + int(np.argmax(over))}: got {got[lo + int(np.argmax(over))]!r} "
+            f"ref {ref[lo + int(np.argmax(over))]!r}")
+        ratio = np.where(tol > 0, err / np.where(tol > 0, tol, 1.0), 0.0)
+        if ratio.max() > worst:
+            worst, worst_at = float(ratio.max()), lo + int(np.argmax(ratio))
+        # relative errors are reported where the reference is not zero (for
+        # g < -2 the reference's 1 + tanh may round to exactly 0)
+        rel = np.where(r != 0, err / np.where(r != 0, np.abs(r), 1.0), 0.0)
+        mild = gg >= -2.0
+        bad = mild & (err > F32_RTOL * np.abs(r))
+        assert not bad.any(), (
+            f"{what}: {int(bad.sum())} elements with g >= -2 outside rtol 1e-5, first at "
+            f"{lo + int(np.argmax(bad))}")
+        if mild.any():
+            worst_mild = max(worst_mild, float(rel[mild].max()))
+        if (~mild).any():
+            worst_neg = max(worst_neg, float(rel[~mild].max()))
+            n_neg += int((~mild).sum())
+    return (f"worst ratio to the bar {worst:.3f} (element {worst_at}); g >= -2: worst "
+            f"relative error {worst_mild:.3g}; g < -2: {n_neg} elements, worst relative error "
+            f"{worst_neg:.3g} where the reference is not 0")

@@ -13,9 +13,12 @@ size in test_gpu_parity.py):
                      ids; (1+w) RMSNorm to f32 [16384, 3584]; q and k RoPE at
                      head_dim 256, 4 x 4096; GeGLU to f32 [16384, 14336]
 
-Bars: bf16 within 1 ulp (RMSNorm at least 99.99 % and RoPE at least 99.9 %
-bit-identical), f32 outputs within rtol 1e-5 (atol 1e-6), SwiGLU and the
-embedding bit-exact.
+Bars: bf16 within 1 ulp (RMSNorm at least 99.99 % bit-identical); RoPE within
+1 ulp on every element of the oracle with the device's cos/sin evaluation,
+with every difference from the libm oracle beyond that bar where the two
+oracles' cos/sin differ; the f32 norm within rtol 1e-5 (atol 1e-6); GeGLU f32
+within rtol 1e-5 plus the rounding error of the reference's own 1 + tanh
+(2^-23 |gate x up|); SwiGLU and the embedding bit-exact.
 """
 from __future__ import annotations
 
@@ -27,7 +30,7 @@ import torch
 
 import higgs_amd as H
 import oracle as O
-from bits import assert_close, exact_frac, ulp_dist
+from bits import assert_close, check_geglu_f32, check_rope_parity, exact_frac, ulp_dist
 from gpu_util import tdtype, to_dev, to_host, words_dev
 
 pytestmark = pytest.mark.gpu
@@ -81,8 +84,11 @@ def _qk_rope(dev, *, B, L, Hq, Hk, D, dims, base=None, freqs=None, norm=False, e
         wk = O.from_f32(O.normal(key + 3, (D,), 1.0, 0.02), O.BF16)
     inv = O.rope_inv_freq(0.0 if freqs is not None else base, dims, freqs)
     kw = dict(dims=dims, inv_freq=inv, eps=eps)
-    rq = O.norm_rope(q, O.BF16, norm_w=wq, w_dt=O.BF16 if norm else None, **kw)
-    rk = O.norm_rope(k, O.BF16, norm_w=wk, w_dt=O.BF16 if norm else None, **kw)
+    trigs = (O.TRIG_LIBM, O.TRIG_F64)
+    rq = [O.norm_rope(q, O.BF16, norm_w=wq, w_dt=O.BF16 if norm else None, trig=t, **kw)
+          for t in trigs]
+    rk = [O.norm_rope(k, O.BF16, norm_w=wk, w_dt=O.BF16 if norm else None, trig=t, **kw)
+          for t in trigs]
     qo, ko = H.qk_norm_rope(to_dev(q, O.BF16, dev), to_dev(k, O.BF16, dev),
                             None if wq is None else to_dev(wq, O.BF16, dev),
                             None if wk is None else to_dev(wk, O.BF16, dev), eps, dims,
@@ -94,10 +100,12 @@ def _qk_rope(dev, *, B, L, Hq, Hk, D, dims, base=None, freqs=None, norm=False, e
     return (gq, rq), (gk, rk)
 
 
-def _check_rope(got, ref, what):
-    _report(what, got, ref, O.BF16)
-    assert_close(got, ref, O.BF16, max_ulp=1, what=what, max_bad_frac=1e-5)
-    assert exact_frac(got, ref, O.BF16) >= 0.999
+def _check_rope(got, refs, what):
+    """Every element within 1 bf16 ulp of the oracle with the device's cos/sin
+    evaluation; against the libm oracle, every element outside that bar sits
+    where the two oracles' cos/sin differ."""
+    print(f"[bench-shape] {what}: " + check_rope_parity(got, refs[0], refs[1], O.BF16, what),
+          flush=True)
 
 
 def test_llama32_chain_fused_qk_rope(dev):
@@ -141,8 +149,9 @@ def test_gemma2_prefill_geglu_f32_out(dev):
     ref = O.glu(O.ACT_GELU_TANH, g, u, O.BF16, out_dt=O.F32)
     got = to_host(H.gelu_approximate_mul(to_dev(g, O.BF16, dev), to_dev(u, O.BF16, dev),
                                          out_dtype=torch.float32))
-    _report("gemma geglu f32 [16384,14336]", got, ref, O.F32)
-    assert_close(got, ref, O.F32, rtol=1e-5, atol=1e-6, what="gemma geglu f32")
+    print("[bench-shape] gemma geglu f32 [16384,14336]: " +
+          check_geglu_f32(got, ref, O.to_f32(g, O.BF16), O.to_f32(u, O.BF16), "gemma geglu f32"),
+          flush=True)
 
 
 def test_gemma2_prefill_embedding_scaled(dev):

@@ -235,6 +235,42 @@ def test_rope_f32_matches_float64_and_invariants():
     np.testing.assert_allclose(n1, n0, rtol=1e-5, atol=1e-6)
 
 
+ROPE_TRIG_CASES = [
+    # base (None: llama3 freqs), dims, positions (range or sampled offsets)
+    (None, 64, np.arange(0, 1024)),                          # Llama-3.2-1B, llama3 scaling
+    (1e6, 128, np.arange(0, 2048)),                          # Qwen3-8B
+    (1e4, 256, np.arange(0, 4096)),                          # Gemma-2-9B
+    (1e7, 64, np.arange(1, 32769)),                          # Qwen3-Next offsets
+]
+
+
+@pytest.mark.parametrize("case", ROPE_TRIG_CASES, ids=lambda c: f"dims{c[1]}-n{len(c[2])}")
+def test_rope_trig_modes_pinned_to_float64(case):
+    """The oracle's two cos/sin evaluations, read back exactly through an f32
+    rotation of x = (1, 0) pairs (y1 = c, y2 = s), at the configurations'
+    positions: the f64 mode is bit for bit the f32 rounding of torch's float64
+    cos/sin of the f32 angle (f32(position) times the f32 inverse frequency),
+    and the libm mode lies within one f32 ulp of it."""
+    base, dims, pos = case
+    if base is None:
+        inv = O.rope_inv_freq(0.0, dims, O.llama3_freqs(500000.0, dims, 32.0, 1.0, 4.0, 8192.0))
+    else:
+        inv = O.rope_inv_freq(base, dims)
+    half = dims // 2
+    n = len(pos)
+    x = np.zeros((n, 1, 1, dims), np.float32)  # one sequence per position
+    x[..., :half] = 1.0
+    offs = pos.astype(np.int32)
+    th = torch.from_numpy(pos.astype(np.float32))[:, None] * torch.from_numpy(inv)[None, :]
+    want_c = torch.cos(th.double()).float().numpy()
+    want_s = torch.sin(th.double()).float().numpy()
+    y64 = O.norm_rope(x, O.F32, dims=dims, inv_freq=inv, offsets=offs, trig=O.TRIG_F64)
+    assert np.array_equal(y64[:, 0, 0, :half], want_c)
+    assert np.array_equal(y64[:, 0, 0, half:], want_s)
+    ylm = O.norm_rope(x, O.F32, dims=dims, inv_freq=inv, offsets=offs, trig=O.TRIG_LIBM)
+    assert ulp_dist(ylm, y64, O.F32).max() <= 1
+
+
 def test_rope_position_zero_is_identity_bitexact():
     for dt in (O.BF16, O.F32):
         x = O.from_f32(O.normal(42, (1, 1, 8, 64)), dt)
@@ -656,3 +692,44 @@ def test_gated_delta_norm_weights_and_rounding():
     y2, s2 = O.gated_delta(qn, kn, *args, state=inp["state"])
     assert np.array_equal(y1, y2) and np.array_equal(s1, s2)
     assert y1.dtype == np.uint16 and s1.dtype == np.uint16
+
+
+def test_geglu_f32_bar_admits_an_accurate_evaluation_and_rejects_a_slip():
+    """The f32 GeGLU bar (tests/bits.py) holds for an accurate evaluation that
+    does not cancel, g / (1 + e^(-2x)) in float64 rounded once to f32, against
+    the oracle's MLX composition, over gates from -9 to 9; and it rejects the
+    same evaluation with a dropped cubic term."""
+    from bits import check_geglu_f32
+
+    g = np.linspace(-9.0, 9.0, 200001).astype(np.float32)
+    u = O.normal(77, (g.size,)) * np.float32(3.0)
+    ref = O.glu(O.ACT_GELU_TANH, g[None, :], u[None, :], O.F32)[0]
+    g64, u64 = g.astype(np.float64), u.astype(np.float64)
+    k0, k1 = math.sqrt(2.0 / math.pi), 0.044715
+
+    def dev_like(cubic):
+        x = k0 * (g64 + cubic * k1 * g64 ** 3)
+        return (g64 / (1.0 + np.exp(-2.0 * x)) * u64).astype(np.float32)
+
+    check_geglu_f32(dev_like(1.0), ref, g, u, "accurate")
+    with pytest.raises(AssertionError):
+        check_geglu_f32(dev_like(0.0), ref, g, u, "no cubic term")
+
+
+def test_rope_parity_check_ties_libm_differences_to_the_tables():
+    """tests/bits.check_rope_parity: the device-trig oracle itself passes, its
+    libm differences are all at elements where the tables differ; a 2-ulp
+    slip on one element fails."""
+    from bits import check_rope_parity
+
+    x = O.from_f32(O.normal(81, (2, 512, 4, 128)), O.BF16)
+    inv = O.rope_inv_freq(1e6, 128)
+    offs = np.array([7, 30000], np.int32)
+    rl = O.norm_rope(x, O.BF16, dims=128, inv_freq=inv, offsets=offs, trig=O.TRIG_LIBM)
+    rd = O.norm_rope(x, O.BF16, dims=128, inv_freq=inv, offsets=offs, trig=O.TRIG_F64)
+    check_rope_parity(rd, rl, rd, O.BF16, "device-trig oracle")
+    bad = rd.copy()
+    i = np.unravel_index(np.argmax(np.abs(O.to_f32(rd, O.BF16))), rd.shape)
+    bad[i] = np.uint16(int(bad[i]) + 2)
+    with pytest.raises(AssertionError):
+        check_rope_parity(bad, rl, rd, O.BF16, "slip")
