@@ -576,45 +576,118 @@ def wl_gemma2(cx):
     return Workload("gemma2_9b_prefill", cfg, ks, ns, T, cpu_sample=cpu_sample_gemma)
 
 
-def wl_qwen3_next_decode(cx):
-    """48-layer op sequence of continuous-batching decode (64 sequences)."""
+def _decode_sequence_sets(cx, S=64, n_layers=48):
+    """Buffers of the 48-layer decode op sequence (64 sequences, one new token
+    each), one set per rotation slot: per layer the input_layernorm (residual
+    add + RMSNorm over hidden 2048, the residual chained from the previous
+    layer), the gated RMSNorm (36 linear-attention layers: y [64, 32, 128], z
+    read in place from in_proj_qkvz [64, 16, 768]) or the q/k RMSNorm +
+    partial RoPE (12 full-attention layers: q the first 256 of each 512-wide
+    block of [64, 16, 512], k [64, 2, 256], 64 rotated dims, theta 1e7,
+    offsets uniform in 1..32768), the post_attention_layernorm (add + RMSNorm)
+    and the routed experts' SwiGLU [64, 10, 512]. The projections' outputs are
+    random stand-ins. Returns (sets, weights, offsets, bytes per sequence)."""
     torch = cx.torch
-    S, Hd, nk, vpk, dv, Hq, Hk, D, E, I = 64, 2048, 16, 2, 128, 16, 2, 256, 10, 512
+    Hd, nk, vpk, dv, Hq, Hk, D, E, I = 2048, 16, 2, 128, 16, 2, 256, 10, 512
     offs = torch.randint(1, 32769, (S,), dtype=torch.int32, device=cx.dev, generator=cx.gen)
-    per_layer = S * Hd * 4 + S * 32 * dv * 6 + S * (Hq * 512 + Hq * D + Hk * D * 2) * 2 + S * E * I * 6
-    ns = nsets_for(per_layer * 48, 1 << 30)
-    wn = cx.randn((Hd,), torch.bfloat16, 1.0, 0.02)
-    wg = cx.randn((dv,), torch.bfloat16, 1.0, 0.02)
-    wq = cx.randn((D,), torch.bfloat16, 1.0, 0.02)
-    wk = cx.randn((D,), torch.bfloat16, 1.0, 0.02)
+    wts = dict(w_in=cx.randn((Hd,), torch.bfloat16, 1.0, 0.02),
+               w_post=cx.randn((Hd,), torch.bfloat16, 1.0, 0.02),
+               wg=cx.randn((dv,), torch.bfloat16, 1.0, 0.02),
+               wq=cx.randn((D,), torch.bfloat16, 1.0, 0.02),
+               wk=cx.randn((D,), torch.bfloat16, 1.0, 0.02))
+    norm_b = 4 * S * Hd * 2 + Hd * 2
+    per_seq = 0
+    for layer in range(n_layers):
+        per_seq += 2 * norm_b + S * E * I * 6
+        per_seq += (S * (Hq * D + Hk * D) * 4 + 2 * D * 2 + S * 4 if layer % 4 == 3
+                    else 3 * S * nk * vpk * dv * 2 + dv * 2)
+    ns = nsets_for(per_seq, 1 << 30)
+    sets = []
+    for _ in range(ns):
+        h = cx.randn((S, Hd), torch.bfloat16)
+        layers = []
+        for layer in range(n_layers):
+            d = dict(x=h, r_prev=cx.randn((S, Hd), torch.bfloat16),
+                     r_attn=cx.randn((S, Hd), torch.bfloat16),
+                     h_a=cx.empty((S, Hd), torch.bfloat16), y_a=cx.empty((S, Hd), torch.bfloat16),
+                     h_b=cx.empty((S, Hd), torch.bfloat16), y_b=cx.empty((S, Hd), torch.bfloat16),
+                     gate=cx.randn((S, E, I), torch.bfloat16), up=cx.randn((S, E, I), torch.bfloat16),
+                     act=cx.empty((S, E, I), torch.bfloat16))
+            if layer % 4 == 3:
+                d["q"] = cx.randn((S, Hq, 2 * D), torch.bfloat16)[:, :, :D]
+                d["k"] = cx.randn((S, Hk, D), torch.bfloat16)
+                d["qo"] = cx.empty((S, Hq, D), torch.bfloat16)
+                d["ko"] = cx.empty((S, Hk, D), torch.bfloat16)
+            else:
+                d["y"] = cx.randn((S, nk * vpk, dv), torch.bfloat16)
+                d["z"] = cx.randn((S, nk, 768), torch.bfloat16)[:, :, 512:].unflatten(-1, (vpk, dv))
+                d["go"] = cx.empty((S, nk * vpk, dv), torch.bfloat16)
+            layers.append(d)
+            h = d["h_b"]
+        sets.append(layers)
+    return sets, wts, offs, per_seq
+
+
+def _decode_cfg(S, n_layers, launches, ns):
+    return {"workload": "qwen3-next-80b-a3b decode op sequence", "sequences": S, "layers": n_layers,
+            "hidden": 2048, "value_heads": 32, "head_v_dim": 128, "q_heads": 16, "kv_heads": 2,
+            "head_dim": 256, "rotary_dims": 64, "experts_per_token": 10, "expert_dim": 512,
+            "hidden_norms": "residual add + rmsnorm", "launches": launches, "buffer_sets": ns}
+
+
+def wl_qwen3_next_decode(cx):
+    """48-layer op sequence of continuous-batching decode (64 sequences) as
+    192 separate launches, replayed as captured graphs."""
+    torch = cx.torch
+    S = 64
+    sets, W, offs, per_seq = _decode_sequence_sets(cx, S)
+    ns = len(sets)
     kernels = []
     for layer in range(48):
-        n1 = [(cx.randn((S, Hd), torch.bfloat16), cx.empty((S, Hd), torch.bfloat16)) for _ in range(ns)]
-        n2 = [(cx.randn((S, Hd), torch.bfloat16), cx.empty((S, Hd), torch.bfloat16)) for _ in range(ns)]
-        kernels.append(k_rmsnorm(cx, "rms_norm", n1, wn, S, Hd, 1e-6))
+        L = [st[layer] for st in sets]
+        n1 = [(d["x"], d["r_prev"], d["h_a"], d["y_a"]) for d in L]
+        kernels.append(k_add_rmsnorm(cx, "add_rms_norm", n1, W["w_in"], S, 2048, 1e-6))
         if layer % 4 == 3:
-            rp = [(cx.randn((S, 1, Hq, 512), torch.bfloat16), cx.randn((S, 1, Hk, D), torch.bfloat16),
-                   cx.empty((S, Hq, 1, D), torch.bfloat16), cx.empty((S, Hk, 1, D), torch.bfloat16))
-                  for _ in range(ns)]
-            kernels.append(k_qkrope(cx, "qk_norm_partial_rope", rp, S, 1, Hq, Hk, D, 64, 1e7,
-                                    wq=wq, wk=wk, eps=1e-6, offsets=offs, q_block=512))
+            rp = [(d["q"].unsqueeze(1), d["k"].unsqueeze(1), d["qo"], d["ko"]) for d in L]
+            kernels.append(k_qkrope(cx, "qk_norm_partial_rope", rp, S, 1, 16, 2, 256, 64, 1e7,
+                                    wq=W["wq"], wk=W["wk"], eps=1e-6, offsets=offs, q_block=512))
         else:
-            gs = []
-            for _ in range(ns):
-                qkvz = cx.randn((S, nk, 768), torch.bfloat16)
-                gs.append((cx.randn((S * nk * vpk, dv), torch.bfloat16), qkvz[:, :, 512:],
-                           cx.empty((S * nk * vpk, dv), torch.bfloat16)))
-            kernels.append(k_gated(cx, "gated_rms_norm", gs, wg, S * nk * vpk, dv, 1e-6, dv, vpk, 768))
-        kernels.append(k_rmsnorm(cx, "rms_norm", n2, wn, S, Hd, 1e-6))
-        gl = [(cx.randn((S * E, I), torch.bfloat16), cx.randn((S * E, I), torch.bfloat16),
-               cx.empty((S * E, I), torch.bfloat16)) for _ in range(ns)]
-        kernels.append(k_glu(cx, "swiglu_experts", gl, S * E, I, SILU))
-    cfg = {"workload": "qwen3-next-80b-a3b decode op sequence", "sequences": S, "layers": 48,
-           "hidden": Hd, "value_heads": 32, "head_v_dim": dv, "q_heads": Hq, "kv_heads": Hk,
-           "head_dim": D, "rotary_dims": 64, "experts_per_token": E, "expert_dim": I,
-           "buffer_sets": ns}
-    return Workload("qwen3_next_decode", cfg, kernels, ns, S, graph=True,
-                    cpu_sample=cpu_sample_ops)
+            gs = [(d["y"], d["z"].flatten(-2), d["go"]) for d in L]
+            kernels.append(k_gated(cx, "gated_rms_norm", gs, W["wg"], S * 32, 128, 1e-6, 128, 2, 768))
+        n2 = [(d["h_a"], d["r_attn"], d["h_b"], d["y_b"]) for d in L]
+        kernels.append(k_add_rmsnorm(cx, "add_rms_norm", n2, W["w_post"], S, 2048, 1e-6))
+        gl = [(d["gate"], d["up"], d["act"]) for d in L]
+        kernels.append(k_glu(cx, "swiglu_experts", gl, S * 10, 512, SILU))
+    return Workload("qwen3_next_decode", _decode_cfg(S, 48, len(kernels), ns), kernels, ns, S,
+                    graph=True, cpu_sample=cpu_sample_ops)
+
+
+def wl_qwen3_next_decode_opseq(cx):
+    """The same 48-layer op sequence (same ops, same buffers) in one launch:
+    one workgroup per sequence walks the 192 ops in the layer loop's order,
+    each op waiting for the previous op's stores (hgk_op_list_run)."""
+    from higgs_amd.ops import OpSequence
+    torch = cx.torch
+    S = 64
+    sets, W, offs, per_seq = _decode_sequence_sets(cx, S)
+    seqs, args = [], []
+    for layers in sets:
+        seq = OpSequence(torch.bfloat16, cx.dev)
+        for d in layers:
+            seq.add_rms_norm(d["x"], d["r_prev"], W["w_in"], 1e-6, d["y_a"], d["h_a"])
+            if "q" in d:
+                seq.qk_norm_rope(d["q"], d["k"], W["wq"], W["wk"], 1e-6, 64, 1e7, d["qo"], d["ko"],
+                                 offsets=offs)
+            else:
+                seq.gated_rms_norm(d["y"], d["z"], W["wg"], 1e-6, d["go"])
+            seq.add_rms_norm(d["h_a"], d["r_attn"], W["w_post"], 1e-6, d["y_b"], d["h_b"])
+            seq.glu(SILU, d["gate"], d["up"], d["act"])
+        seq.upload()
+        seqs.append(seq)
+        args.append((BF16, _vp(seq._list), len(seq), S, cx.stream))
+    k = Kernel("op_sequence_48_layers", per_seq, cx.lib.hgk_op_list_run, args, S,
+               keep=(sets, W, offs, seqs))
+    return Workload("qwen3_next_decode_opseq", _decode_cfg(S, 48, 1, len(sets)), [k], len(sets), S)
 
 
 def k_qmm_swiglu(cx, name, sets, tab_g, tab_u, E, N, K, T, top_k, group=64):
@@ -733,6 +806,7 @@ WORKLOADS = {
     "qwen3_8b_prefill": wl_qwen3_prefill,
     "gemma2_9b_prefill": wl_gemma2,
     "qwen3_next_decode": wl_qwen3_next_decode,
+    "qwen3_next_decode_opseq": wl_qwen3_next_decode_opseq,
     "llama32_1b_chain_fused": wl_llama_chain_fused,
     "block_boundary_add_rms_norm": wl_block_boundary,
     "qwen3_next_moe_decode": wl_qwen3_next_moe_decode,

@@ -19,6 +19,22 @@ _vp, _i64, _int, _f32, _i32 = C.c_void_p, C.c_int64, C.c_int, C.c_float, C.c_int
 _i64p = C.POINTER(C.c_int64)
 _f32p = C.POINTER(C.c_float)
 
+class HgkOp(C.Structure):
+    """hgk_op of include/higgs_hip.h (one op of a decode step's op sequence)."""
+    _fields_ = [("kind", C.c_int), ("rows", C.c_int), ("n", C.c_int), ("eps", C.c_float),
+                ("x", C.c_void_p), ("x_tok", C.c_int64), ("x_row", C.c_int64),
+                ("r", C.c_void_p), ("r_tok", C.c_int64), ("r_row", C.c_int64),
+                ("z_group_rows", C.c_int64), ("z_group_stride", C.c_int64),
+                ("w", C.c_void_p), ("w2", C.c_void_p),
+                ("y", C.c_void_p), ("y_tok", C.c_int64), ("y_row", C.c_int64),
+                ("h", C.c_void_p), ("h_tok", C.c_int64), ("h_row", C.c_int64),
+                ("act", C.c_int), ("k_heads", C.c_int), ("dims", C.c_int), ("base", C.c_float),
+                ("freqs", C.POINTER(C.c_float)), ("scale", C.c_float),
+                ("offsets", C.c_void_p), ("offset", C.c_int32)]
+
+
+OP_RMS_NORM, OP_ADD_RMS_NORM, OP_GATED_RMS_NORM, OP_QK_NORM_ROPE, OP_GLU = 0, 1, 2, 3, 4
+
 # name -> (restype, argtypes); kept in the order of include/higgs_hip.h
 PROTOTYPES = {
     "hgk_last_error": (C.c_char_p, []),
@@ -57,6 +73,9 @@ PROTOTYPES = {
                                           _vp, _vp, _f32, _i64, _i64, _i64, _i64, _i64, _vp,
                                           _vp, _vp, _i64, _i64, _i64, _vp, _int, _f32, _vp,
                                           _vp]),
+    "hgk_op_list_bytes": (_i64, [_int]),
+    "hgk_op_list_upload": (_int, [_int, C.POINTER(HgkOp), _int, _vp, _i64, _vp]),
+    "hgk_op_list_run": (_int, [_int, _vp, _int, _i64, _vp]),
     "hgk_st_open": (_int, [C.c_char_p, C.POINTER(_vp)]),
     "hgk_st_close": (None, [_vp]),
     "hgk_st_count": (_i64, [_vp]),

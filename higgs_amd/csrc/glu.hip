@@ -44,30 +44,6 @@ struct GluArgs {
   int contig;      // all three tensors densely packed
 };
 
-template <class X, int ACT>
-__device__ inline float glu1(float g, float u) {
-  if constexpr (ACT == HGK_ACT_SILU) {
-    if constexpr (X::kBytes == 2) {
-      float o;
-      swiglu16<X, 1>(&g, &u, &o);
-      return o;
-    } else {
-      const float sg = X::round(mlx_sigmoid(g));
-      const float s = X::round(g * sg);
-      return X::round(s * u);
-    }
-  } else {
-    // exp(-2*k0*(g + k1*g^3)) = exp2(g * (c1 + c2*g^2)) with k0 = sqrt(2/pi),
-    // k1 = 0.044715, c1 = -2*k0*log2(e), c2 = c1*k1: three VALU operations
-    // before the exp2 instead of six
-    const float c1 = -2.302208198144325f, c2 = -0.1029432395800235f;
-    const float z = g * __builtin_fmaf(g * g, c2, c1);
-    const float e = __builtin_amdgcn_exp2f(z);
-    const float gl = g * __builtin_amdgcn_rcpf(1.0f + e);
-    return gl * u;
-  }
-}
-
 // Element offsets of chunk q in gate, up and out (rows of cpr chunks).
 template <int V, bool CONTIG>
 __device__ inline void glu_offsets(const GluArgs& a, uint32_t q, int64_t& go, int64_t& uo,

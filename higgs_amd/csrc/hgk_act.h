@@ -63,4 +63,32 @@ __device__ inline void swiglu16(const float* g, const float* u, float* o) {
   for (int e = 0; e < N; ++e) o[e] = X::round(X::round(g[e] * X::round(sg[e])) * u[e]);
 }
 
+// One GLU output before its rounding to the output type: SwiGLU (as above,
+// for 16-bit and f32 inputs) or GeGLU, which runs in f32: 0.5*g*(1+tanh(k0*(g
+// + k1*g^3))) * u evaluated as g / (1 + exp(-2*k0*(g + k1*g^3))) * u with the
+// hardware exp2 and reciprocal.
+template <class X, int ACT>
+__device__ inline float glu1(float g, float u) {
+  if constexpr (ACT == 0) {  // HGK_ACT_SILU
+    if constexpr (X::kBytes == 2) {
+      float o;
+      swiglu16<X, 1>(&g, &u, &o);
+      return o;
+    } else {
+      const float sg = X::round(mlx_sigmoid(g));
+      const float s = X::round(g * sg);
+      return X::round(s * u);
+    }
+  } else {
+    // exp(-2*k0*(g + k1*g^3)) = exp2(g * (c1 + c2*g^2)) with k0 = sqrt(2/pi),
+    // k1 = 0.044715, c1 = -2*k0*log2(e), c2 = c1*k1: three VALU operations
+    // before the exp2 instead of six
+    const float c1 = -2.302208198144325f, c2 = -0.1029432395800235f;
+    const float z = g * __builtin_fmaf(g * g, c2, c1);
+    const float e = __builtin_amdgcn_exp2f(z);
+    const float gl = g * __builtin_amdgcn_rcpf(1.0f + e);
+    return gl * u;
+  }
+}
+
 }  // namespace hgk

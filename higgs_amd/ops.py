@@ -20,6 +20,8 @@ Each function keeps the reference call's name and argument meaning:
     QuantizedEmbedding(...).forward_rms_norm(ids, w, eps)
                                              embed_tokens + the first input_layernorm
                                              (transformer.rs:494, 407)
+    OpSequence                               a decode step's per-layer ops in one launch
+                                             (the layer loop, qwen3_next.rs:1508-1547)
 
 Errors surface as HgkError (the reference returns Err(Exception::custom(..))).
 Every op enqueues on torch's current CUDA/HIP stream and never synchronises.
@@ -32,8 +34,9 @@ from typing import Optional, Sequence
 
 import torch
 
-from ._lib import (ACT_GELU_TANH, ACT_SILU, BF16, F16, F32, I32, U32, HgkError, check,
-                   f32_array, i64_array, lib)
+from ._lib import (ACT_GELU_TANH, ACT_SILU, BF16, F16, F32, I32, OP_ADD_RMS_NORM, OP_GATED_RMS_NORM,
+                   OP_GLU, OP_QK_NORM_ROPE, OP_RMS_NORM, U32, HgkError, HgkOp, check, f32_array,
+                   i64_array, lib)
 
 _DT = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16, torch.int32: I32}
 if hasattr(torch, "uint32"):
@@ -555,3 +558,149 @@ def gemma_embed_scale(hidden: int) -> float:
     """sqrt(hidden) as the reference computes it (f32), before the cast to the
     activation dtype that the kernel applies."""
     return float(math.sqrt(float(hidden)))
+
+
+# ---------------------------------------------------------------- op sequence
+def _tok_rows(t: torch.Tensor, what: str):
+    """(rows, n, token stride, row stride) of a [T, n] or [T, rows, n] view
+    with a unit-stride last axis."""
+    if t.stride(-1) != 1 and t.shape[-1] > 1:
+        raise HgkError(1, f"{what}: the last axis must have unit stride")
+    if t.dim() == 2:
+        return 1, t.shape[1], t.stride(0), t.shape[1]
+    if t.dim() == 3:
+        return t.shape[1], t.shape[2], t.stride(0), t.stride(1)
+    raise HgkError(1, f"{what}: expected [tokens, n] or [tokens, rows, n]")
+
+
+class OpSequence:
+    """A decode step's per-layer ops -- input_layernorm (residual add +
+    RMSNorm), the gated RMSNorm or q/k RMSNorm + RoPE, post_attention_layernorm,
+    the experts' SwiGLU, layer after layer as the loop of qwen3_next.rs:1508-1547
+    calls them -- recorded once, uploaded once, then run over a batch of tokens
+    in one launch (hgk_op_list_upload / hgk_op_list_run). Every operand is a
+    view whose first axis is the token; the recorded addresses are used at
+    every run, so the tensors must stay alive and in place (this object keeps
+    references to them). Results are the same bits as the separate calls."""
+
+    def __init__(self, dtype: torch.dtype, device):
+        if dtype not in (torch.bfloat16, torch.float16):
+            raise HgkError(2, "OpSequence: bf16 or f16 only")
+        self.dtype, self.device = dtype, torch.device(device)
+        self._ops, self._keep, self._list, self._uploaded = [], [], None, 0
+
+    def _check(self, *ts):
+        for t in ts:
+            if t is not None and t.dtype != self.dtype:
+                raise HgkError(1, f"OpSequence: operand dtype {t.dtype}, list dtype {self.dtype}")
+        self._keep.extend(t for t in ts if t is not None)
+
+    def __len__(self):
+        return len(self._ops)
+
+    def rms_norm(self, x, weight, eps, y):
+        """y = rms_norm(x, weight, eps) (weight may be None)."""
+        self._check(x, weight, y)
+        rows, n, xt, xr = _tok_rows(x, "x")
+        _, _, yt, yr = _tok_rows(y, "y")
+        self._ops.append(HgkOp(kind=OP_RMS_NORM, rows=rows, n=n, eps=eps, x=x.data_ptr(), x_tok=xt,
+                               x_row=xr, w=None if weight is None else weight.data_ptr(),
+                               y=y.data_ptr(), y_tok=yt, y_row=yr))
+        return self
+
+    def add_rms_norm(self, x, r, weight, eps, y, h=None):
+        """h = x + r (written when h is given); y = rms_norm(h, weight, eps)."""
+        self._check(x, r, weight, y, h)
+        rows, n, xt, xr = _tok_rows(x, "x")
+        _, _, rt, rr = _tok_rows(r, "r")
+        _, _, yt, yr = _tok_rows(y, "y")
+        ht, hr = (0, 0) if h is None else _tok_rows(h, "h")[2:]
+        self._ops.append(HgkOp(kind=OP_ADD_RMS_NORM, rows=rows, n=n, eps=eps, x=x.data_ptr(),
+                               x_tok=xt, x_row=xr, r=r.data_ptr(), r_tok=rt, r_row=rr,
+                               w=None if weight is None else weight.data_ptr(), y=y.data_ptr(),
+                               y_tok=yt, y_row=yr, h=None if h is None else h.data_ptr(),
+                               h_tok=ht, h_row=hr))
+        return self
+
+    def gated_rms_norm(self, x, z, weight, eps, y):
+        """y = swiglu(z, rms_norm(x, weight, eps)). x, y: [T, rows, n]; z:
+        [T, rows, n] or [T, groups, rows_per_group, n] (e.g. the z slice of
+        in_proj_qkvz, read in place)."""
+        self._check(x, z, weight, y)
+        rows, n, xt, xr = _tok_rows(x, "x")
+        _, _, yt, yr = _tok_rows(y, "y")
+        if z.dim() == 4:
+            if z.shape[1] * z.shape[2] != rows or z.shape[3] != n or z.stride(3) != 1:
+                raise HgkError(1, "z must be [T, groups, rows_per_group, n] covering x's rows")
+            zt, zr, zg, zgs = z.stride(0), z.stride(2), z.shape[2], z.stride(1)
+        else:
+            _, _, zt, zr = _tok_rows(z, "z")
+            zg, zgs = 0, 0
+        self._ops.append(HgkOp(kind=OP_GATED_RMS_NORM, rows=rows, n=n, eps=eps, x=x.data_ptr(),
+                               x_tok=xt, x_row=xr, r=z.data_ptr(), r_tok=zt, r_row=zr,
+                               z_group_rows=zg, z_group_stride=zgs, w=weight.data_ptr(),
+                               y=y.data_ptr(), y_tok=yt, y_row=yr))
+        return self
+
+    def qk_norm_rope(self, q, k, q_weight, k_weight, eps, dims, base, q_out, k_out, *,
+                     scale=1.0, offset=0, offsets=None, freqs=None):
+        """q/k RMSNorm (weights may be None) and RoPE of one new token per
+        sequence at position offsets[t] (or offset) times scale: q [T, Hq, D]
+        (a head may sit in a wider block, as Qwen3-Next's q), k [T, Hk, D];
+        outputs q_out [T, Hq, D], k_out [T, Hk, D] (any token/head strides)."""
+        self._check(q, k, q_weight, k_weight, q_out, k_out)
+        hq, D, qt, qr = _tok_rows(q, "q")
+        hk, _, kt, kr = _tok_rows(k, "k")
+        _, _, yt, yr = _tok_rows(q_out, "q_out")
+        _, _, ht, hr = _tok_rows(k_out, "k_out")
+        if offsets is not None:
+            if offsets.dtype != torch.int32 or offsets.device != q.device:
+                raise HgkError(1, "offsets must be int32 on q's device")
+            self._keep.append(offsets)
+        fr = _freqs_arg(freqs)
+        if fr is not None:
+            self._keep.append(fr)
+        self._ops.append(HgkOp(kind=OP_QK_NORM_ROPE, rows=hq, n=D, eps=eps, x=q.data_ptr(),
+                               x_tok=qt, x_row=qr, r=k.data_ptr(), r_tok=kt, r_row=kr,
+                               w=None if q_weight is None else q_weight.data_ptr(),
+                               w2=None if k_weight is None else k_weight.data_ptr(),
+                               y=q_out.data_ptr(), y_tok=yt, y_row=yr, h=k_out.data_ptr(),
+                               h_tok=ht, h_row=hr, k_heads=hk, dims=dims,
+                               base=0.0 if base is None else base, freqs=fr, scale=scale,
+                               offsets=None if offsets is None else offsets.data_ptr(),
+                               offset=offset))
+        return self
+
+    def glu(self, act, gate, up, y):
+        """y = act(gate) * up (ACT_SILU: swiglu; ACT_GELU_TANH: GeGLU)."""
+        self._check(gate, up, y)
+        rows, n, gt, gr = _tok_rows(gate, "gate")
+        _, _, ut, ur = _tok_rows(up, "up")
+        _, _, yt, yr = _tok_rows(y, "y")
+        self._ops.append(HgkOp(kind=OP_GLU, rows=rows, n=n, act=act, x=gate.data_ptr(), x_tok=gt,
+                               x_row=gr, r=up.data_ptr(), r_tok=ut, r_row=ur, y=y.data_ptr(),
+                               y_tok=yt, y_row=yr))
+        return self
+
+    def upload(self):
+        """Writes the recorded ops into a device list (done by run() when
+        ops were added since the last upload)."""
+        n = len(self._ops)
+        if n == 0:
+            raise HgkError(1, "OpSequence: no ops")
+        nbytes = lib().hgk_op_list_bytes(n)
+        if nbytes < 0:
+            raise HgkError(1, f"OpSequence: {n} ops is too many")
+        self._list = torch.empty(((nbytes + 15) // 16 * 16,), dtype=torch.uint8, device=self.device)
+        arr = (HgkOp * n)(*self._ops)
+        check(lib().hgk_op_list_upload(dtype_code(self.dtype), arr, n, _ptr(self._list),
+                                       self._list.numel(), _stream(self.device)))
+        self._uploaded = n
+        return self
+
+    def run(self, tokens: int):
+        """Every op over tokens 0..tokens-1, in one launch on the current stream."""
+        if self._uploaded != len(self._ops):
+            self.upload()
+        check(lib().hgk_op_list_run(dtype_code(self.dtype), _ptr(self._list), self._uploaded,
+                                    tokens, _stream(self.device)))

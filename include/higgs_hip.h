@@ -349,6 +349,89 @@ int hgk_gated_delta_gated_norm(int dtype, const void* q, const void* k, const vo
                                float norm_eps, void* out, void* stream);
 
 /* ------------------------------------------------------------------------
+ * A decode step's per-layer op sequence in one launch.
+ *
+ * Replaces the chain of separate calls the layer loop makes for every
+ * sequence of a continuous batch (crates/higgs-models/src/qwen3_next.rs:
+ * 1508-1547, driven by crates/higgs-engine/src/batch_engine.rs:395-403):
+ * input_layernorm (residual add + RMSNorm), the gated RMSNorm of a
+ * linear-attention layer or the q/k RMSNorm + (partial) RoPE of a
+ * full-attention layer, post_attention_layernorm (add + RMSNorm) and the
+ * experts' SwiGLU, layer after layer. The ops between them (projections,
+ * attention, the recurrence) are not in the list; their outputs are the ops'
+ * inputs.
+ *
+ * One workgroup per token walks the ops in order; each op waits for the
+ * previous op's stores to reach L2 before it loads. Every op is row-wise, so
+ * token t reads only token t's rows. Results are the same bits as the
+ * separate calls (hgk_rms_norm, hgk_add_rms_norm, hgk_gated_rms_norm,
+ * hgk_qk_norm_rope with one position per token, hgk_glu).
+ *
+ * Operand addressing (elements): row r of token t of operand P lies at
+ * P + t * P_tok + r * P_row; the innermost axis is unit-stride. Every
+ * operand and weight is 16-byte aligned and every stride a multiple of 8
+ * elements. Activations, weights and outputs share the list's dtype (bf16 or
+ * f16).
+ * ------------------------------------------------------------------------ */
+typedef enum {
+  HGK_OP_RMS_NORM = 0,       /* y = rms_norm(x, w, eps); w may be NULL */
+  HGK_OP_ADD_RMS_NORM = 1,   /* h = x + r (written if h != NULL); y = rms_norm(h, w, eps) */
+  HGK_OP_GATED_RMS_NORM = 2, /* y = silu(z) * rms_norm(x, w, eps), z = operand r, its row
+                              * k at (k / z_group_rows) * z_group_stride + (k % z_group_rows)
+                              * r_row from the token's base (as hgk_gated_rms_norm) */
+  HGK_OP_QK_NORM_ROPE = 3,   /* q = operand x (rows = q heads), k = operand r (k_heads rows),
+                              * outputs y (q) and h (k); optional norm weights w (q), w2 (k);
+                              * rotation as hgk_qk_norm_rope at position offsets[t] (or offset)
+                              * times scale; head_dim n a power of two in 32..512, dims a
+                              * multiple of 16 */
+  HGK_OP_GLU = 4             /* y = act(gate) * up, gate = operand x, up = operand r */
+} hgk_op_kind;
+
+#define HGK_OP_LIST_MAX 4096
+
+typedef struct {
+  int kind;     /* hgk_op_kind */
+  int rows;     /* rows per token (the q heads for HGK_OP_QK_NORM_ROPE) */
+  int n;        /* elements per row (head_dim for HGK_OP_QK_NORM_ROPE), a multiple of 8;
+                 * norms: n <= 8192; GLU: rows * n <= 8192 */
+  float eps;
+  const void* x;
+  int64_t x_tok, x_row;
+  const void* r;
+  int64_t r_tok, r_row;
+  int64_t z_group_rows, z_group_stride; /* HGK_OP_GATED_RMS_NORM; z_group_rows <= 0: one group */
+  const void* w;
+  const void* w2;
+  void* y;
+  int64_t y_tok, y_row;
+  void* h;
+  int64_t h_tok, h_row;
+  int act;                /* HGK_OP_GLU: hgk_act */
+  int k_heads;            /* HGK_OP_QK_NORM_ROPE */
+  int dims;               /* rotated dims */
+  float base;             /* as hgk_rope_inv_freq: base, or freqs [dims/2] (host memory) */
+  const float* freqs;
+  float scale;
+  const int32_t* offsets; /* device [tokens] or NULL (then `offset` for every token) */
+  int32_t offset;
+} hgk_op;
+
+/* Bytes of device memory an op list of n_ops ops takes (-1 if n_ops is not in
+ * 1..HGK_OP_LIST_MAX). */
+int64_t hgk_op_list_bytes(int n_ops);
+/* Checks the ops, computes each RoPE op's frequencies, and writes the list
+ * into dev_list (caller-owned device memory of hgk_op_list_bytes(n_ops)
+ * bytes, 16-byte aligned), copying on `stream`; the copy has completed when
+ * the call returns. The list keeps the operand addresses, not their data. */
+int hgk_op_list_upload(int dtype, const hgk_op* ops, int n_ops, void* dev_list,
+                       int64_t dev_bytes, void* stream);
+/* Runs the first n_ops ops of an uploaded list over `tokens` tokens in one
+ * launch. dtype must be the one the list was uploaded with; a list that was
+ * not written by hgk_op_list_upload for that dtype and at least n_ops ops is
+ * not walked (the launch does nothing). */
+int hgk_op_list_run(int dtype, const void* dev_list, int n_ops, int64_t tokens, void* stream);
+
+/* ------------------------------------------------------------------------
  * Checkpoint files: the safetensors files MLX 4-bit checkpoints ship in
  * (u32-packed `.weight`, bf16/f16 `.scales`/`.biases`, bf16 norm weights).
  * Replaces Array::load_safetensors as used by load_quantized_safetensors_weights

@@ -183,3 +183,61 @@ def test_python_mirror_rejects_mixed_scale_and_bias_dtypes():
         H.gather_qmm(x, w, s16, h16, idx, x_row_div=k)
     with pytest.raises(_lib.HgkError, match="share a dtype"):
         H.quantized_matmul(x, w[0], s16[0], h16[0])
+
+
+def test_op_list_layout_and_validation_without_a_device():
+    """hgk_op as ctypes lays it out is the C struct (sizeof and field offsets
+    from a C compile of the header); hgk_op_list_upload names the op index and
+    the offending field values (which also shows the fields land where the
+    library reads them); the run's argument checks come before any HIP call."""
+    import shutil
+    import tempfile
+
+    from higgs_amd._lib import HgkOp
+    L = _lib.lib()
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc:
+        src = ("#include <stdio.h>\n#include <stddef.h>\n#include \"higgs_hip.h\"\n"
+               "int main(void){printf(\"%zu\", sizeof(hgk_op));")
+        fields = [f[0] for f in HgkOp._fields_]
+        for f in fields:
+            src += f"printf(\" %zu\", offsetof(hgk_op, {f}));"
+        src += "return 0;}\n"
+        with tempfile.TemporaryDirectory() as d:
+            open(os.path.join(d, "l.c"), "w").write(src)
+            subprocess.run([cc, "-I", os.path.join(ROOT, "include"), os.path.join(d, "l.c"), "-o",
+                            os.path.join(d, "l")], check=True)
+            got = [int(v) for v in subprocess.run([os.path.join(d, "l")], capture_output=True,
+                                                  text=True, check=True).stdout.split()]
+        assert got == [C.sizeof(HgkOp)] + [getattr(HgkOp, f).offset for f in fields]
+    assert L.hgk_op_list_bytes(0) == -1 and L.hgk_op_list_bytes(4097) == -1
+    assert L.hgk_op_list_bytes(192) > 192 * 200
+    fake = C.c_void_p(1 << 20)
+    ok = dict(x=1 << 20, x_tok=2048, y=1 << 21, y_tok=2048, r=1 << 22, r_tok=2048, h=1 << 23,
+              h_tok=2048, w=1 << 24)
+
+    def upload(*ops, dtype=1):
+        arr = (HgkOp * len(ops))(*ops)
+        st = L.hgk_op_list_upload(dtype, arr, len(ops), fake, 1 << 30, None)
+        return st, L.hgk_last_error().decode()
+
+    good = HgkOp(kind=1, rows=1, n=2048, eps=1e-6, **ok)
+    st, msg = upload(good, HgkOp(kind=0, rows=3, n=12, **ok))
+    assert st == 1 and "op 1" in msg and "rows=3" in msg and "n=12" in msg
+    st, msg = upload(good, good, HgkOp(kind=3, rows=16, n=256, dims=40, k_heads=2, base=1e7, **ok))
+    assert st == 2 and "op 2" in msg and "rotated dims 40" in msg
+    st, msg = upload(HgkOp(kind=3, rows=16, n=192, dims=64, k_heads=2, base=1e7, **ok))
+    assert st == 2 and "head_dim 192" in msg
+    st, msg = upload(HgkOp(kind=4, rows=10, n=512, act=7, **ok))
+    assert st == 1 and "activation 7" in msg
+    st, msg = upload(HgkOp(kind=2, rows=32, n=128, eps=1e-6, **{**ok, "w": None}))
+    assert st == 1 and "needs a weight" in msg
+    st, msg = upload(HgkOp(kind=1, rows=1, n=2048, eps=1e-6, **{**ok, "x_tok": 2047}))
+    assert st == 1 and "whole 16-byte units" in msg
+    st, msg = upload(good, dtype=0)
+    assert st == 2 and "bf16 or f16" in msg
+    assert L.hgk_op_list_run(0, fake, 1, 64, None) == 2
+    assert L.hgk_op_list_run(1, None, 1, 64, None) == 1
+    assert L.hgk_op_list_run(1, fake, 0, 64, None) == 1
+    assert L.hgk_op_list_run(1, fake, 4, -1, None) == 1
+    assert L.hgk_op_list_run(1, fake, 4, 0, None) == 0  # nothing to run: no launch
