@@ -189,6 +189,9 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
   constexpr int V = Vec<X>::N;
   constexpr int RB = kRopeBatch;
   constexpr int slots = 256 / LPR;
+  // the square root and division of a batch's four rows are done once per
+  // quad of lanes (lane j finishes row j % 4) and broadcast by DPP
+  constexpr bool SHARED = NORM && RB == 4 && LPR >= 4;
   extern __shared__ float smem[];
   float* cs = smem;
   float* sn = smem + a.tpb * a.half;
@@ -253,6 +256,43 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
   __syncthreads();
 
   for (int base = slot;;) {
+    // the batch's rms scales: every lane holds every row's sum; with SHARED,
+    // lane j of each quad finishes row j % 4 and the quad shares the results
+    float rsk[RB];
+    if constexpr (NORM) {
+      double ssk[RB];
+#pragma unroll
+      for (int k = 0; k < RB; ++k) {
+        double ss = 0.0;
+#pragma unroll
+        for (int e = 0; e < V; ++e) {
+          const double v = (double)elem<X>(d0[k], e);
+          ss = __builtin_fma(v, v, ss);
+        }
+#pragma unroll
+        for (int e = 0; e < V; ++e) {
+          const double v = (double)elem<X>(d1[k], e);
+          ss = __builtin_fma(v, v, ss);
+        }
+        ssk[k] = group_sum<LPR>(ss);
+      }
+      if constexpr (SHARED) {
+        const int q = j & 3;
+        double mine = ssk[0];
+        mine = q == 1 ? ssk[1] : mine;
+        mine = q == 2 ? ssk[2] : mine;
+        mine = q == 3 ? ssk[3] : mine;
+        const float r = rms_scale(mine, a.inv_d, a.eps);
+        const int ri = __builtin_bit_cast(int, r);
+        rsk[0] = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, ri, 0x00, 0xF, 0xF, true));
+        rsk[1] = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, ri, 0x55, 0xF, 0xF, true));
+        rsk[2] = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, ri, 0xAA, 0xF, 0xF, true));
+        rsk[3] = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, ri, 0xFF, 0xF, 0xF, true));
+      } else {
+#pragma unroll
+        for (int k = 0; k < RB; ++k) rsk[k] = rms_scale(ssk[k], a.inv_d, a.eps);
+      }
+    }
 #pragma unroll
     for (int k = 0; k < RB; ++k) {
       const int r = base + k * slots;
@@ -267,13 +307,7 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
       if constexpr (NORM) {
         const bool has = isk ? (a.t[1].nw != nullptr) : (a.t[0].nw != nullptr);
         if (has) {  // uniform across the row's lane group
-          double ss = 0.0;
-#pragma unroll
-          for (int e = 0; e < V; ++e) ss = __builtin_fma((double)v0[e], (double)v0[e], ss);
-#pragma unroll
-          for (int e = 0; e < V; ++e) ss = __builtin_fma((double)v1[e], (double)v1[e], ss);
-          ss = group_sum<LPR>(ss);
-          const float rs = rms_scale(ss, a.inv_d, a.eps);
+          const float rs = rsk[k];
           const u32x4 wa = isk ? w0k : w0q, wb = isk ? w1k : w1q;
 #pragma unroll
           for (int e = 0; e < V; e += 2) {  // roundings paired: one conversion per two

@@ -429,13 +429,19 @@ def test_qembed_codes_bitexact_and_variants(dev):
     (300, 3584, 9000, 64, O.F16, 0),    # 56 groups: one load per row, permuted
     (300, 2048, 8193, 64, O.BF16, 1),   # scales/biases 2-byte aligned only
     (300, 8192, 8500, 128, O.BF16, 0),  # 16 steps a row, permuted
+    # 16384 ids and more: four rows in flight per wave (permuted loads only)
+    (300, 3584, 16387, 64, O.F16, 0),   # f16, a ragged last stride of tokens
+    (300, 2048, 20000, 32, O.BF16, 0),  # 64 groups a row
+    (300, 1024, 16384, 128, O.BF16, 0), # 2 steps a row
+    (300, 2048, 16384, 64, O.BF16, 1),  # 2-byte aligned: the one-token kernel
 ])
 def test_qembed_row_load_forms(dev, V, Hd, n, group, sdt, offset):
     """Both ways of loading a row's scales and biases (one 32-bit load per
     lane plus a cross-lane permute when the row's groups fit one register and
     are 4-byte aligned, else a 16-bit load per step), each with more ids than
     the chip keeps waves resident, so every wave runs the pipelined loop over
-    several tokens. Bit-exact against the oracle."""
+    several tokens; from 16384 ids, the kernel that keeps four rows in flight
+    per wave. Bit-exact against the oracle."""
     key = 1870 + group + Hd
     wq = O.u32(key, (V, Hd // 8))
     s = O.from_f32(O.uniform(key + 1, (V, Hd // group), 0.005, 0.02), sdt)
