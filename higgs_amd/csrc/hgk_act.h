@@ -63,6 +63,24 @@ __device__ inline void swiglu16(const float* g, const float* u, float* o) {
   for (int e = 0; e < N; ++e) o[e] = X::round(X::round(g[e] * X::round(sg[e])) * u[e]);
 }
 
+// The sigmoids of two values of a 16-bit type X, rounded to X, as MLX's exact
+// sigmoid rounds them: the hardware exp2 / reciprocal form where it provably
+// rounds the same way (sigmoid16_fast), the exact form elsewhere.
+template <class X>
+__device__ inline void sigmoid2_rounded(float z0, float z1, float& s0, float& s1) {
+  if constexpr (X::kBytes == 2) {
+    bool f0, f1;
+    s0 = sigmoid16_fast<X>(z0, &f0);
+    s1 = sigmoid16_fast<X>(z1, &f1);
+    if (f0) s0 = mlx_sigmoid(z0);
+    if (f1) s1 = mlx_sigmoid(z1);
+  } else {
+    s0 = mlx_sigmoid(z0);
+    s1 = mlx_sigmoid(z1);
+  }
+  round2<X>(s0, s1);
+}
+
 // One GLU output before its rounding to the output type: SwiGLU (as above,
 // for 16-bit and f32 inputs) or GeGLU, which runs in f32: 0.5*g*(1+tanh(k0*(g
 // + k1*g^3))) * u evaluated as g / (1 + exp(-2*k0*(g + k1*g^3))) * u with the

@@ -13,11 +13,14 @@
 // Arithmetic follows MLX's CPU composition (fast::rms_norm fallback):
 //   r = 1 / sqrt(f32(sum(x*x)) * f32(1/n) + eps)   (sum accumulated in f64)
 //   n = round_T(x * r);  y = round_T(n * w')        (T = promote(x, w'))
-// and, gated, out = round_T(round_T(z * round_T(sigmoid(z))) * y).
+// and, gated, out = round_T(round_T(z * round_T(sigmoid(z))) * y), the
+// rounded sigmoid taken from the hardware exp2 / reciprocal form wherever it
+// provably rounds like MLX's exact one (sigmoid2_rounded).
 // The residual form first forms h = round_X(x + r) (MLX's add), writes h and
 // normalises it: the block boundary `h = x.add(residual); norm(h)` of
 // transformer.rs:413-415 in one pass.
 #include "../../include/higgs_hip.h"
+#include "hgk_act.h"
 #include "hgk_common.h"
 #include "hgk_host.h"
 
@@ -159,8 +162,8 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(NormArgs a) {
       if constexpr (GATED) {
         if (rx) round2<X>(n0, n1);
         const float z0 = elem<X>(zr[c], e), z1 = elem<X>(zr[c], e + 1);
-        float s0 = mlx_sigmoid(z0), s1 = mlx_sigmoid(z1);
-        round2<X>(s0, s1);
+        float s0, s1;
+        sigmoid2_rounded<X>(z0, z1, s0, s1);
         float g0 = z0 * s0, g1 = z1 * s1;
         round2<X>(g0, g1);
         n0 = g0 * n0;

@@ -114,19 +114,6 @@ __device__ inline double row_sum(double v, double* part) {
   }
 }
 
-// The rounded sigmoid of two 16-bit values, as MLX's exact sigmoid rounds
-// them: the hardware exp2 / reciprocal form where it provably rounds the same
-// way (sigmoid16_fast), the exact one where it may not.
-template <class X>
-__device__ inline void sigmoid2(float z0, float z1, float& s0, float& s1) {
-  bool f0, f1;
-  s0 = sigmoid16_fast<X>(z0, &f0);
-  s1 = sigmoid16_fast<X>(z1, &f1);
-  if (f0) s0 = mlx_sigmoid(z0);
-  if (f1) s1 = mlx_sigmoid(z1);
-  round2<X>(s0, s1);
-}
-
 // RMSNorm / add + RMSNorm / gated RMSNorm over the token's rows: G lanes per
 // row (G a power of two, 4..1024), one 16-byte unit per lane, 1024 / G rows
 // per pass (a token's 32 head rows of 128 in one pass). rms_norm_kernel's
@@ -185,7 +172,7 @@ __device__ void op_norm(const DevOp& op, int64_t t, double* part) {
         round2<X>(n0, n1);
         const float z0 = elem<X>(zr, e), z1 = elem<X>(zr, e + 1);
         float s0, s1;
-        sigmoid2<X>(z0, z1, s0, s1);
+        sigmoid2_rounded<X>(z0, z1, s0, s1);
         float g0 = z0 * s0, g1 = z1 * s1;
         round2<X>(g0, g1);
         n0 = g0 * n0;
