@@ -719,12 +719,14 @@ def k_gdn_gated(cx, name, sets, wq, wk, alog, dtb, wn, B, Hk, Dk, Hv, Dv, zrow, 
 
 def wl_qwen3_next_decode_layers(cx, fused=False):
     """One decode step of 64 sequences through the 48 Qwen3-Next-80B-A3B
-    layers' per-layer kernels around the dense projections: per layer a
-    hidden RMSNorm [64, 2048]; for the 36 linear-attention layers the
+    layers' per-layer kernels around the dense projections: per layer the
+    input_layernorm as residual add + RMSNorm [64, 2048] (the residual stream
+    chained from layer to layer, qwen3_next.rs:1539-1540); for the 36
+    linear-attention layers the
     gated-delta recurrence (Hk 16, Dk 128, Hv 32, Dv 128, fused q/k norm, the
     state updated in place) and its gated output norm (z read in place from
     in_proj_qkvz), for the 12 full-attention layers the q/k-norm + partial
-    RoPE; a second hidden RMSNorm; the routed experts' gate and up
+    RoPE; the post_attention_layernorm (add + RMSNorm); the routed experts' gate and up
     gather_qmm (top-10 of 512, 512 x 2048, 4-bit) and SwiGLU. Unfused: the
     reference's separate calls (7 launches per linear-attention layer).
     Fused: recurrence + gated norm in one launch and gate + up + SwiGLU in
@@ -748,10 +750,13 @@ def wl_qwen3_next_decode_layers(cx, fused=False):
     r = lambda shape, lo, hi: (torch.rand(shape, device=cx.dev, generator=cx.gen) * (hi - lo) + lo
                                ).to(torch.bfloat16)
     kernels = []
+    h = cx.randn((S, Hd), torch.bfloat16)  # the residual stream, chained through the layers
     for layer in range(48):
-        n1 = [(cx.randn((S, Hd), torch.bfloat16), cx.empty((S, Hd), torch.bfloat16))]
-        n2 = [(cx.randn((S, Hd), torch.bfloat16), cx.empty((S, Hd), torch.bfloat16))]
-        kernels.append(k_rmsnorm(cx, "rms_norm", n1, wn, S, Hd, 1e-6))
+        h_a, h_b = cx.empty((S, Hd), torch.bfloat16), cx.empty((S, Hd), torch.bfloat16)
+        n1 = [(h, cx.randn((S, Hd), torch.bfloat16), h_a, cx.empty((S, Hd), torch.bfloat16))]
+        n2 = [(h_a, cx.randn((S, Hd), torch.bfloat16), h_b, cx.empty((S, Hd), torch.bfloat16))]
+        h = h_b
+        kernels.append(k_add_rmsnorm(cx, "add_rms_norm", n1, wn, S, Hd, 1e-6))
         if layer % 4 == 3:
             rp = [(cx.randn((S, 1, Hq, 512), torch.bfloat16), cx.randn((S, 1, Hkv, D), torch.bfloat16),
                    cx.empty((S, Hq, 1, D), torch.bfloat16), cx.empty((S, Hkv, 1, D), torch.bfloat16))]
@@ -774,7 +779,7 @@ def wl_qwen3_next_decode_layers(cx, fused=False):
                 o = cx.empty((S * Hv, Dv), torch.bfloat16)
                 kernels.append(k_gated(cx, "gated_rms_norm", [(y, z, o)], wg, S * Hv, Dv, 1e-6,
                                        Dv, 2, 768))
-        kernels.append(k_rmsnorm(cx, "rms_norm", n2, wn, S, Hd, 1e-6))
+        kernels.append(k_add_rmsnorm(cx, "add_rms_norm", n2, wn, S, Hd, 1e-6))
         ex = torch.stack([torch.randperm(E, generator=g)[:top_k] for _ in range(S)]).reshape(-1).to(
             torch.int32)
         exd = ex.to(cx.dev)

@@ -122,28 +122,41 @@ __device__ inline bool deq_fast_ok(uint32_t s16, uint32_t b16) {
   }
 }
 
-// One word's 8 outputs, packed in S (out[k] = elements 2k, 2k + 1).
-template <class S>
-__device__ inline u32x4 deq_word_fast(uint32_t c, uint32_t s16, float sv, float bv, bool has_scale,
-                                      uint32_t o16) {
+// Constants of the dot2 form, held in registers for the whole kernel (made
+// once by DeqRegs::make): (1, 0) and (0, 1), the code mask and magic, and -0.
+// Given 0x00003f80 as an immediate, this compiler encodes it as the inline
+// constant 1.0, which the hardware reads in a dot2 as a different pair
+// (measured: the product then took the high element); a three-operand
+// and-or takes no literal here, so the mask and magic in registers let the
+// code extraction be one v_and_or_b32.
+struct DeqRegs {
+  uint32_t one_lo, one_hi, mask, magic;
+  float nzero;
+  template <class S>
+  __device__ static inline DeqRegs make() {
+    DeqRegs r{DeqK<S>::kOne, DeqK<S>::kOne << 16, 0x000f000fu, DeqK<S>::kMagic, -0.0f};
+    asm volatile("" : "+v"(r.one_lo), "+v"(r.one_hi), "+v"(r.mask), "+v"(r.magic), "+v"(r.nzero));
+    return r;
+  }
+};
+
+// One word's 8 outputs, packed in S (out[k] = elements 2k, 2k + 1); HS: the
+// output scale o16 applies.
+template <class S, bool HS>
+__device__ inline u32x4 deq_word_fast(uint32_t c, uint32_t s16, float sv, float bv, uint32_t o16,
+                                      const DeqRegs& R) {
   const uint32_t slo = s16, shi = s16 << 16, olo = o16, ohi = o16 << 16;
-  // (1, 0) and (0, 1) live in registers: given 0x00003f80 as an immediate,
-  // this compiler encodes it as the inline constant 1.0, which the hardware
-  // reads in v_dot2c_f32_bf16 as a different pair (measured: the product
-  // then took the high element)
-  uint32_t one_lo = DeqK<S>::kOne, one_hi = DeqK<S>::kOne << 16;
-  asm volatile("" : "+v"(one_lo), "+v"(one_hi));
   const float nks = -DeqK<S>::kOff * sv;
   float v[8];
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
-    const uint32_t q = ((c >> (4 * k)) & 0x000f000fu) | DeqK<S>::kMagic;  // codes k, k + 4
+    const uint32_t q = ((c >> (4 * k)) & R.mask) | R.magic;  // codes k, k + 4
     const uint32_t p = S::pack(dot2_16<S>(q, slo, nks), dot2_16<S>(q, shi, nks));
-    float v0 = dot2_16<S>(p, one_lo, bv), v1 = dot2_16<S>(p, one_hi, bv);
-    if (has_scale) {
+    float v0 = dot2_16<S>(p, R.one_lo, bv), v1 = dot2_16<S>(p, R.one_hi, bv);
+    if constexpr (HS) {
       const uint32_t w = S::pack(v0, v1);
-      v0 = dot2_16<S>(w, olo, -0.0f);
-      v1 = dot2_16<S>(w, ohi, -0.0f);
+      v0 = dot2_16<S>(w, olo, R.nzero);
+      v1 = dot2_16<S>(w, ohi, R.nzero);
     }
     v[k] = v0;
     v[k + 4] = v1;
@@ -254,6 +267,7 @@ __global__ __launch_bounds__(256) void qembed_kernel(QembArgs a) {
   if (t >= a.n) return;  // whole wave leaves together
   const float osc = S::round(a.scale);
   const uint32_t o16 = S::pack(osc, 0.0f) & 0xffffu;
+  const DeqRegs R = DeqRegs::make<S>();
   QembRow<S, STEPS, PERM> cur, nxt;
   cur.load(a, t, lane);
   for (;;) {
@@ -270,7 +284,8 @@ __global__ __launch_bounds__(256) void qembed_kernel(QembArgs a) {
       if (w >= a.wpr) continue;
       char* op = reinterpret_cast<char*>(a.out) + (t * a.os + (int64_t)w * 8) * S::kBytes;
       if (fast) {
-        u32x4 o = deq_word_fast<S>(cur.codes[s], s16, sv, bv, a.has_scale, o16);
+        u32x4 o = a.has_scale ? deq_word_fast<S, true>(cur.codes[s], s16, sv, bv, o16, R)
+                              : deq_word_fast<S, false>(cur.codes[s], s16, sv, bv, o16, R);
         if (!cur.valid) o = u32x4{0u, 0u, 0u, 0u};
         __builtin_nontemporal_store(o, reinterpret_cast<u32x4*>(op));
         continue;
@@ -297,7 +312,7 @@ __global__ __launch_bounds__(256) void qembed_kernel(QembArgs a) {
 // so the wave keeps TPW rows of reads in flight (with one token in flight per
 // wave, the reads of 16384 random rows come back too slowly to keep the write
 // stream busy).
-template <class S, int STEPS, int TPW>
+template <class S, int STEPS, int TPW, bool HS>
 __global__ __launch_bounds__(256) void qembed_rows_kernel(QembArgs a, int64_t nwaves) {
   const int lane = threadIdx.x & 63;
   const int64_t w = (int64_t)blockIdx.x * (blockDim.x >> 6) +
@@ -311,6 +326,7 @@ __global__ __launch_bounds__(256) void qembed_rows_kernel(QembArgs a, int64_t nw
   }
   const float osc = S::round(a.scale);
   const uint32_t o16 = S::pack(osc, 0.0f) & 0xffffu;
+  const DeqRegs R = DeqRegs::make<S>();
   QembRow<S, STEPS, true> rows[TPW];
 #pragma clang loop unroll(full)
   for (int k = 0; k < TPW; ++k) {
@@ -323,6 +339,17 @@ __global__ __launch_bounds__(256) void qembed_rows_kernel(QembArgs a, int64_t nw
     const int64_t t = w + (int64_t)k * nwaves;
     const bool live = t < a.n;  // uniform over the wave
     const QembRow<S, STEPS, true>& cur = rows[k];
+    if (!cur.valid) {  // an id outside the table: a row of zeros (uniform over the wave)
+#pragma clang loop unroll(full)
+      for (int s = 0; s < STEPS; ++s) {
+        const int wd = s * 64 + lane;
+        if (live && wd < a.wpr)
+          __builtin_nontemporal_store(u32x4{0u, 0u, 0u, 0u},
+                                      reinterpret_cast<u32x4*>(reinterpret_cast<char*>(a.out) +
+                                                               (t * a.os + (int64_t)wd * 8) * S::kBytes));
+      }
+      continue;
+    }
     const bool fast = HGK_QEMB_DOT2 && a.fast_scale_ok && cur.fast_row(a, lane);
 #pragma clang loop unroll(full)
     for (int s = 0; s < STEPS; ++s) {
@@ -333,8 +360,7 @@ __global__ __launch_bounds__(256) void qembed_rows_kernel(QembArgs a, int64_t nw
       if (!live || wd >= a.wpr) continue;
       char* op = reinterpret_cast<char*>(a.out) + (t * a.os + (int64_t)wd * 8) * S::kBytes;
       if (fast) {
-        u32x4 o = deq_word_fast<S>(cur.codes[s], s16, sv, bv, a.has_scale, o16);
-        if (!cur.valid) o = u32x4{0u, 0u, 0u, 0u};
+        const u32x4 o = deq_word_fast<S, HS>(cur.codes[s], s16, sv, bv, o16, R);
         __builtin_nontemporal_store(o, reinterpret_cast<u32x4*>(op));
         continue;
       }
@@ -343,8 +369,8 @@ __global__ __launch_bounds__(256) void qembed_rows_kernel(QembArgs a, int64_t nw
       for (int nib = 0; nib < 8; ++nib) {
         const uint32_t q = (cur.codes[s] >> (4 * nib)) & 0xfu;
         float x = deq<S>(q, sv, bv);
-        x = a.has_scale ? S::round(x * osc) : x;
-        v[nib] = cur.valid ? x : 0.0f;
+        x = HS ? S::round(x * osc) : x;
+        v[nib] = x;
       }
       store_elems<S, 8>(a.out, t * a.os + (int64_t)wd * 8, v);
     }
@@ -504,15 +530,15 @@ __global__ __launch_bounds__(256) void qembed_norm_generic_kernel(QembArgs a) {
 
 namespace {
 
-template <class S, int TPW>
+template <class S, int TPW, bool HS>
 void launch_rows(const QembArgs& a, int steps, hipStream_t s) {
   const int64_t nwaves = (a.n + TPW - 1) / TPW;
   const dim3 g((unsigned)((nwaves + 3) / 4)), b(256);
-  if (steps <= 1) HGK_LAUNCH((qembed_rows_kernel<S, 1, TPW>), g, b, 0, s, a, nwaves);
-  else if (steps <= 2) HGK_LAUNCH((qembed_rows_kernel<S, 2, TPW>), g, b, 0, s, a, nwaves);
-  else if (steps <= 4) HGK_LAUNCH((qembed_rows_kernel<S, 4, TPW>), g, b, 0, s, a, nwaves);
-  else if (steps <= 7) HGK_LAUNCH((qembed_rows_kernel<S, 7, TPW>), g, b, 0, s, a, nwaves);
-  else HGK_LAUNCH((qembed_rows_kernel<S, 8, TPW>), g, b, 0, s, a, nwaves);
+  if (steps <= 1) HGK_LAUNCH((qembed_rows_kernel<S, 1, TPW, HS>), g, b, 0, s, a, nwaves);
+  else if (steps <= 2) HGK_LAUNCH((qembed_rows_kernel<S, 2, TPW, HS>), g, b, 0, s, a, nwaves);
+  else if (steps <= 4) HGK_LAUNCH((qembed_rows_kernel<S, 4, TPW, HS>), g, b, 0, s, a, nwaves);
+  else if (steps <= 7) HGK_LAUNCH((qembed_rows_kernel<S, 7, TPW, HS>), g, b, 0, s, a, nwaves);
+  else HGK_LAUNCH((qembed_rows_kernel<S, 8, TPW, HS>), g, b, 0, s, a, nwaves);
 }
 
 template <class S, bool PERM>
@@ -536,7 +562,8 @@ void launch(const QembArgs& a, bool vec_ok, bool perm_ok, hipStream_t s) {
   // waves (measured at 16384 tokens of 256000 x 3584: 6 % faster than one
   // token in flight; at 4096 tokens, with 1024 waves, 45 % slower)
   if (vec_ok && perm_ok && steps <= 8 && a.n >= 2 * (int64_t)resident_waves()) {
-    launch_rows<S, 4>(a, steps, s);
+    if (a.has_scale) launch_rows<S, 4, true>(a, steps, s);
+    else launch_rows<S, 4, false>(a, steps, s);
     return;
   }
   if (vec_ok && steps <= 16) {
