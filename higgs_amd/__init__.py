@@ -6,7 +6,7 @@ quantized_matmul / gather_qmm projections and the GatedDeltaNet recurrence),
 exposed
 through the C ABI in include/higgs_hip.h and mirrored here for Python callers.
 """
-from ._lib import HgkError, LIB_PATH, lib  # noqa: F401
+from ._lib import ACT_GELU_TANH, ACT_SILU, HgkError, LIB_PATH, lib  # noqa: F401
 from .ops import (OpSequence, QuantizedEmbedding, add_rms_norm, gated_rms_norm, gelu_approximate_mul,  # noqa: F401
                   fused_gate_up_swiglu, gather_qmm, gather_qmm_swiglu, gated_delta,
                   gated_delta_gated_norm, gdn_qk_norm_weights,
