@@ -68,23 +68,6 @@ struct F32 {
   __device__ static float round(float a) { return a; }
 };
 
-// a.lo * b.lo + a.hi * b.hi + c for two packed pairs of a 16-bit type T
-// (v_dot2_f32_bf16 / v_dot2_f32_f16), in f32. With one pair element zero it
-// is a product straight from the packed form, with no unpacking; where the
-// products and the sum are exact in f32 (16-bit significands), the result is
-// exactly the IEEE value.
-template <class T>
-__device__ inline float dot2_16(uint32_t a, uint32_t b, float c);
-template <>
-__device__ inline float dot2_16<BF16>(uint32_t a, uint32_t b, float c) {
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b),
-                                         c, false);
-}
-template <>
-__device__ inline float dot2_16<F16>(uint32_t a, uint32_t b, float c) {
-  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b), c, false);
-}
-
 // Elements of T per 16-byte chunk.
 template <class T> struct Vec { static constexpr int N = 16 / T::kBytes; };
 

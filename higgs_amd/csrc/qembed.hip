@@ -5,12 +5,12 @@
 //   scales [vocab, hidden/group]      bf16 or f16
 //   biases [vocab, hidden/group]      same dtype as scales
 // One wave64 owns one token: at step s lane i reads packed word s*64 + i
-// (8 codes) and its group's scale/bias and writes those 8 outputs, so every
-// load instruction reads 256 contiguous bytes of the row and every store
-// writes 1 KB contiguous (a lane owning 16 contiguous bytes of codes and
-// 64 bytes of output measured 2.5x slower: each instruction then touched
-// every line of the row). The table is never dequantized as a whole
-// (QEmbedding::forward does that on every call in the reference).
+// (8 codes) and writes those 8 outputs, so every load instruction reads 256
+// contiguous bytes of the row and every store writes 1 KB contiguous (a lane
+// owning 16 contiguous bytes of codes and 64 bytes of output measured 2.5x
+// slower: each instruction then touched every line of the row). The table is
+// never dequantized as a whole (QEmbedding::forward does that on every call
+// in the reference).
 //
 // Arithmetic (MLX dequantize, S = scales dtype):
 //   v = round_S(round_S(q * s) + b);  optionally v = round_S(v * round_S(scale))
@@ -30,12 +30,6 @@
 
 namespace hgk {
 
-// Dequantize with dot2 products where the row's scales and biases allow it
-// (0 keeps the element-by-element form everywhere, for comparisons).
-#ifndef HGK_QEMB_DOT2
-#define HGK_QEMB_DOT2 1
-#endif
-
 struct QembArgs {
   const void* ids;
   int ids_i32;
@@ -49,7 +43,7 @@ struct QembArgs {
   int group;
   float scale;
   int has_scale;
-  int fast_scale_ok;  // no output scale, or an output scale in [2^-19, 2^19]
+  int group_shift;  // log2(group / 8): packed words per group
   void* out;  // h (may be null in the fused form)
   int64_t os;
   int64_t hidden;
@@ -77,303 +71,125 @@ __device__ inline float deq(uint32_t q, float s, float b) {
   return S::round(S::round((float)q * s) + b);
 }
 
-// The same dequantization of one packed word (8 codes, one group) from the
-// packed forms, with dot2 products: a code enters as the 16-bit number
-// K + q (K = 128 for bf16, 1024 for f16: two bit operations per pair of
-// codes), and
-//   q s         = dot2((K + q_i, K + q_i+4), (s, 0)) - K s     (exact in f32)
-//   round(q s) + b = dot2(P, (1, 0)) + b                        (P = the rounded pair)
-//   round(v) * o   = dot2(V, (o, 0)) - 0                        (o = the output scale)
-// Each product has at most 22 significant bits and each sum is exact, so
-// every value is the IEEE one before its rounding to S; the roundings are
-// the packing conversions. About half the VALU work of unpacking and
-// multiplying element by element. A dot2 also multiplies the pair's other
-// element by zero, so every intermediate must stay finite and normal: the
-// scale and bias ranges of deq_fast_ok guarantee that (bf16: 2^-100 <= |s| <
-// 2^100, b = +-0 or 2^-100 <= |b| < 2^126; f16: normal |s| < 2^12, |b| <
-// 2^11), the host admits positive output scales in [2^-19, 2^19] only (a
-// negative one would turn a +0 element into -0 * (+0) + (+0) = +0 where the
-// reference has round(+0 * o) = -0), and a negative scale beside a bias of -0
-// is excluded (q = 0 would give +0 where the reference has -0). Rows with any
-// other group take deq() instead.
-template <class S> struct DeqK;
-template <> struct DeqK<BF16> {
-  static constexpr uint32_t kMagic = 0x43004300u;  // bf16 128 in each half
-  static constexpr float kOff = 128.0f;
-  static constexpr uint32_t kOne = 0x3f80u;
-};
-template <> struct DeqK<F16> {
-  static constexpr uint32_t kMagic = 0x64006400u;  // f16 1024 in each half
-  static constexpr float kOff = 1024.0f;
-  static constexpr uint32_t kOne = 0x3c00u;
-};
+// The gather: one wave per token, through a table of the row's values.
+//
+// A 4-bit code takes 16 values, so each group of the row has 16 possible
+// outputs. The wave first builds them -- lane g computes group g's 16 values
+// with the exact element formula deq() (and the output scale), 8 pairs with
+// one packed rounding each -- and writes them to its region of LDS (32 bytes
+// per group). Each element is then one 16-bit LDS read at the address
+// region + 32 g + 2 q: per packed word of 8 codes, two shift/and-or
+// operations leave 2q in the low bits of each byte, with (g mod 8) * 32
+// merged into the same bytes (the region is 256-byte aligned, so the low byte
+// of an entry's address is (g mod 8) * 32 + 2q and the rest is region +
+// 256 (g / 8)), and one byte permute per element splices that byte into the
+// address. About 17 VALU operations per word against ~64 for computing the 8
+// values directly (and the tables cost 16 values per group of 64 elements).
+// Every value is the one deq() gives, for any scale, bias and output scale.
+//
+// At step s lane i reads packed word s*64 + i of the row (each load
+// instruction of the wave reads 256 contiguous bytes) and writes its 8
+// outputs with one 16-byte store (1 KB contiguous per instruction). The
+// scales and biases come first (the tables need them), then the codes.
+//  GSH: log2(group / 8) (words per group) when known at compile time (group
+//       64: 3), else 0 and the group's shift is read from the arguments;
+//  TG:  groups the wave's table region holds (64 or 256).
+typedef __attribute__((address_space(3))) uint16_t lds_u16;
+typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
 
-template <class S>
-__device__ inline bool deq_fast_ok(uint32_t s16, uint32_t b16) {
-  const bool neg_zero = (s16 & 0x8000u) && b16 == 0x8000u;
-  if constexpr (DeqK<S>::kOff == 128.0f) {  // bf16: exponent field e, |x| ~ 2^(e - 127)
-    const uint32_t se = (s16 >> 7) & 0xffu, be = (b16 >> 7) & 0xffu;
-    const bool s_ok = se >= 27u && se <= 226u;
-    const bool b_ok = (b16 & 0x7fffu) == 0u || (be >= 27u && be <= 252u);
-    return s_ok && b_ok && !neg_zero;
-  } else {  // f16: exponent field e, |x| ~ 2^(e - 15)
-    const uint32_t se = (s16 >> 10) & 0x1fu, be = (b16 >> 10) & 0x1fu;
-    return se >= 1u && se <= 26u && be <= 25u && !neg_zero;
-  }
-}
+constexpr int kLutWaves = 4;  // waves per workgroup
 
-// Constants of the dot2 form, held in registers for the whole kernel (made
-// once by DeqRegs::make): (1, 0) and (0, 1), the code mask and magic, and -0.
-// Given 0x00003f80 as an immediate, this compiler encodes it as the inline
-// constant 1.0, which the hardware reads in a dot2 as a different pair
-// (measured: the product then took the high element); a three-operand
-// and-or takes no literal here, so the mask and magic in registers let the
-// code extraction be one v_and_or_b32.
-struct DeqRegs {
-  uint32_t one_lo, one_hi, mask, magic;
-  float nzero;
-  template <class S>
-  __device__ static inline DeqRegs make() {
-    DeqRegs r{DeqK<S>::kOne, DeqK<S>::kOne << 16, 0x000f000fu, DeqK<S>::kMagic, -0.0f};
-    asm volatile("" : "+v"(r.one_lo), "+v"(r.one_hi), "+v"(r.mask), "+v"(r.magic), "+v"(r.nzero));
-    return r;
-  }
-};
-
-// One word's 8 outputs, packed in S (out[k] = elements 2k, 2k + 1); HS: the
-// output scale o16 applies.
-template <class S, bool HS>
-__device__ inline u32x4 deq_word_fast(uint32_t c, uint32_t s16, float sv, float bv, uint32_t o16,
-                                      const DeqRegs& R) {
-  const uint32_t slo = s16, shi = s16 << 16, olo = o16, ohi = o16 << 16;
-  const float nks = -DeqK<S>::kOff * sv;
-  float v[8];
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const uint32_t q = ((c >> (4 * k)) & R.mask) | R.magic;  // codes k, k + 4
-    const uint32_t p = S::pack(dot2_16<S>(q, slo, nks), dot2_16<S>(q, shi, nks));
-    float v0 = dot2_16<S>(p, R.one_lo, bv), v1 = dot2_16<S>(p, R.one_hi, bv);
-    if constexpr (HS) {
-      const uint32_t w = S::pack(v0, v1);
-      v0 = dot2_16<S>(w, olo, R.nzero);
-      v1 = dot2_16<S>(w, ohi, R.nzero);
-    }
-    v[k] = v0;
-    v[k + 4] = v1;
-  }
-  u32x4 o;
-#pragma unroll
-  for (int k = 0; k < 4; ++k) o[k] = S::pack(v[2 * k], v[2 * k + 1]);
-  return o;
-}
-
-// The loads of one token's row, issued together and kept as raw words until
-// used (converting a value where it is loaded would make the compiler wait for
-// it step by step). At step s lane i owns packed word w = s*64 + i (8 codes,
-// one group): each code load instruction of the wave reads 256 contiguous
-// bytes of the row. Addresses are clamped into the row instead of predicating
-// the loads, so no select has to wait on a loaded value before the next load
-// issues.
-//  PERM: the row's scales and biases (gpr even, gpr <= 64) come in with one
-//        32-bit load per lane -- lane l < gpr/2 holds scale pair l, lane
-//        gpr/2 + l bias pair l -- and each step takes its group's pair from
-//        the owning lane by a cross-lane permute: 1 load instruction per row
-//        instead of 2 per step (each of which read 16 useful bytes).
-//  else: one 16-bit scale and bias load per step.
-template <class S, int STEPS, bool PERM>
-struct QembRow {
-  uint32_t codes[STEPS];
-  uint32_t sraw[PERM ? 1 : STEPS], braw[PERM ? 1 : STEPS];
-  bool valid;
-
-  __device__ inline void load(const QembArgs& a, int64_t t, int lane) {
-    load_row(a, load_id(a, t), lane);
-  }
-
-  __device__ inline void load_row(const QembArgs& a, int64_t id, int lane) {
-    valid = id >= 0 && id < a.vocab;
-    const int64_t row = valid ? id : 0;
-    const uint32_t* wrow = a.wq + row * a.wpr;
-    const uint16_t* sc = reinterpret_cast<const uint16_t*>(a.sc) + row * a.gpr;
-    const uint16_t* bi = reinterpret_cast<const uint16_t*>(a.bi) + row * a.gpr;
-#pragma unroll
-    for (int s = 0; s < STEPS; ++s) {
-      const int w = s * 64 + lane;
-      codes[s] = wrow[w < a.wpr ? w : a.wpr - 1];
-    }
-    if constexpr (PERM) {
-      const int half = a.gpr >> 1;
-      const int l = lane < a.gpr ? lane : a.gpr - 1;
-      const uint16_t* p = l < half ? sc + 2 * l : bi + 2 * (l - half);
-      sraw[0] = *reinterpret_cast<const uint32_t*>(p);
-    } else {
-#pragma unroll
-      for (int s = 0; s < STEPS; ++s) {
-        const int w = s * 64 + lane;
-        const int g = ((w < a.wpr ? w : a.wpr - 1) * 8) / a.group;
-        sraw[s] = (uint32_t)sc[g];
-        braw[s] = (uint32_t)bi[g];
-      }
-    }
-  }
-
-  // The scale and bias of step s's group, as f32 and as their 16-bit codes.
-  __device__ inline void group_affine(const QembArgs& a, int s, int lane, float& sv, float& bv,
-                                      uint32_t& s16, uint32_t& b16) const {
-    if constexpr (PERM) {
-      const int w = s * 64 + lane;
-      int g = (w * 8) / a.group;
-      g = g < a.gpr ? g : a.gpr - 1;
-      const uint32_t sw = (uint32_t)__shfl((int)sraw[0], g >> 1);
-      const uint32_t bw = (uint32_t)__shfl((int)sraw[0], (a.gpr >> 1) + (g >> 1));
-      s16 = (g & 1) ? sw >> 16 : sw & 0xffffu;
-      b16 = (g & 1) ? bw >> 16 : bw & 0xffffu;
-    } else {
-      s16 = sraw[s] & 0xffffu;
-      b16 = braw[s] & 0xffffu;
-    }
-    sv = S::lo(s16);
-    bv = S::lo(b16);
-  }
-
-  // Whether every group of the row takes deq_word_fast (uniform over the
-  // wave; PERM rows only, whose lanes hold all of the row's scales and biases).
-  __device__ inline bool fast_row(const QembArgs& a, int lane) const {
-    if constexpr (PERM) {
-      const int half = a.gpr >> 1;
-      // lane l < half holds scale pair l; its biases are in lane half + l
-      const uint32_t bw = (uint32_t)__shfl((int)sraw[0], (lane < half ? lane : 0) + half);
-      bool ok = true;
-      if (lane < half)
-        ok = deq_fast_ok<S>(sraw[0] & 0xffffu, bw & 0xffffu) && deq_fast_ok<S>(sraw[0] >> 16, bw >> 16);
-      return __builtin_amdgcn_ballot_w64(!ok) == 0;
-    } else {
-      return false;
-    }
-  }
-};
-
-// Persistent waves over the tokens (wave w takes tokens w, w + W, w + 2W, ...
-// for W waves in the grid, sized to what the chip holds resident), software
-// pipelined: the next token's loads are issued before the current token's
-// row is dequantized and stored, so every wave keeps one row of reads in
-// flight under its stores. Each store writes 1 KB contiguous.
-template <class S, int STEPS, bool PERM>
-__global__ __launch_bounds__(256) void qembed_kernel(QembArgs a) {
+template <class S, int STEPS, int GSH, int TG>
+__global__ __launch_bounds__(64 * kLutWaves) void qembed_lut_kernel(QembArgs a) {
+  __shared__ __align__(256) uint16_t lut[kLutWaves][TG * 16];
   const int lane = threadIdx.x & 63;
-  const int wpb = blockDim.x >> 6;
-  const int64_t nw = (int64_t)gridDim.x * wpb;
-  int64_t t = (int64_t)blockIdx.x * wpb + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t t = (int64_t)blockIdx.x * (blockDim.x >> 6) + wv;
   if (t >= a.n) return;  // whole wave leaves together
-  const float osc = S::round(a.scale);
-  const uint32_t o16 = S::pack(osc, 0.0f) & 0xffffu;
-  const DeqRegs R = DeqRegs::make<S>();
-  QembRow<S, STEPS, PERM> cur, nxt;
-  cur.load(a, t, lane);
-  for (;;) {
-    const int64_t tn = t + nw;
-    const bool more = tn < a.n;
-    if (more) nxt.load(a, tn, lane);
-    const bool fast = HGK_QEMB_DOT2 && a.fast_scale_ok && cur.fast_row(a, lane);
+  const int64_t id = load_id(a, t);
+  const bool valid = id >= 0 && id < a.vocab;
+  const int64_t row = valid ? id : 0;
+  constexpr int GPL = TG / 64;  // groups per lane in the table
+  uint32_t sr[GPL], br[GPL], codes[STEPS];
+  const uint16_t* sc = reinterpret_cast<const uint16_t*>(a.sc) + row * a.gpr;
+  const uint16_t* bi = reinterpret_cast<const uint16_t*>(a.bi) + row * a.gpr;
 #pragma unroll
-    for (int s = 0; s < STEPS; ++s) {
-      float sv, bv;
-      uint32_t s16, b16;
-      cur.group_affine(a, s, lane, sv, bv, s16, b16);  // (a permute: every lane takes part)
-      const int w = s * 64 + lane;
-      if (w >= a.wpr) continue;
-      char* op = reinterpret_cast<char*>(a.out) + (t * a.os + (int64_t)w * 8) * S::kBytes;
-      if (fast) {
-        u32x4 o = a.has_scale ? deq_word_fast<S, true>(cur.codes[s], s16, sv, bv, o16, R)
-                              : deq_word_fast<S, false>(cur.codes[s], s16, sv, bv, o16, R);
-        if (!cur.valid) o = u32x4{0u, 0u, 0u, 0u};
-        __builtin_nontemporal_store(o, reinterpret_cast<u32x4*>(op));
-        continue;
-      }
-      float v[8];
-#pragma unroll
-      for (int nib = 0; nib < 8; ++nib) {
-        const uint32_t q = (cur.codes[s] >> (4 * nib)) & 0xfu;
-        float x = deq<S>(q, sv, bv);
-        x = a.has_scale ? S::round(x * osc) : x;
-        v[nib] = cur.valid ? x : 0.0f;
-      }
-      store_elems<S, 8>(a.out, t * a.os + (int64_t)w * 8, v);
-    }
-    if (!more) break;
-    t = tn;
-    cur = nxt;
+  for (int j = 0; j < GPL; ++j) {
+    const int g = lane + 64 * j;
+    const int gc = g < a.gpr ? g : a.gpr - 1;
+    sr[j] = sc[gc];
+    br[j] = bi[gc];
   }
-}
-
-// Many tokens (at least four per wave over half the resident waves): TPW
-// tokens per wave, t = w + k * W for W waves; lane k fetches token k's id, and
-// every one of the wave's TPW rows is loaded before the first row is stored,
-// so the wave keeps TPW rows of reads in flight (with one token in flight per
-// wave, the reads of 16384 random rows come back too slowly to keep the write
-// stream busy).
-template <class S, int STEPS, int TPW, bool HS>
-__global__ __launch_bounds__(256) void qembed_rows_kernel(QembArgs a, int64_t nwaves) {
-  const int lane = threadIdx.x & 63;
-  const int64_t w = (int64_t)blockIdx.x * (blockDim.x >> 6) +
-                    __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  if (w >= nwaves) return;  // whole wave leaves together
-  int64_t id = 0;
-  {
-    int64_t t = w + (int64_t)(lane < TPW ? lane : TPW - 1) * nwaves;
-    t = t < a.n ? t : a.n - 1;
-    id = load_id(a, t);
+  const uint32_t* wrow = a.wq + row * a.wpr;
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s) {
+    const int wd = s * 64 + lane;
+    codes[s] = wrow[wd < a.wpr ? wd : a.wpr - 1];
+  }
+  char* obase = reinterpret_cast<char*>(a.out) + (t * a.os + (int64_t)lane * 8) * S::kBytes;
+  if (!valid) {  // an id outside the table: a row of zeros (uniform over the wave)
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s)
+      if (s * 64 + lane < a.wpr)
+        __builtin_nontemporal_store(u32x4{0u, 0u, 0u, 0u},
+                                    reinterpret_cast<u32x4*>(obase + s * 512 * S::kBytes));
+    return;
   }
   const float osc = S::round(a.scale);
-  const uint32_t o16 = S::pack(osc, 0.0f) & 0xffffu;
-  const DeqRegs R = DeqRegs::make<S>();
-  QembRow<S, STEPS, true> rows[TPW];
-#pragma clang loop unroll(full)
-  for (int k = 0; k < TPW; ++k) {
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)id, k);
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)id >> 32), k);
-    rows[k].load_row(a, (int64_t)(((uint64_t)hi << 32) | lo), lane);
-  }
-#pragma clang loop unroll(full)
-  for (int k = 0; k < TPW; ++k) {
-    const int64_t t = w + (int64_t)k * nwaves;
-    const bool live = t < a.n;  // uniform over the wave
-    const QembRow<S, STEPS, true>& cur = rows[k];
-    if (!cur.valid) {  // an id outside the table: a row of zeros (uniform over the wave)
-#pragma clang loop unroll(full)
-      for (int s = 0; s < STEPS; ++s) {
-        const int wd = s * 64 + lane;
-        if (live && wd < a.wpr)
-          __builtin_nontemporal_store(u32x4{0u, 0u, 0u, 0u},
-                                      reinterpret_cast<u32x4*>(reinterpret_cast<char*>(a.out) +
-                                                               (t * a.os + (int64_t)wd * 8) * S::kBytes));
-      }
-      continue;
-    }
-    const bool fast = HGK_QEMB_DOT2 && a.fast_scale_ok && cur.fast_row(a, lane);
-#pragma clang loop unroll(full)
-    for (int s = 0; s < STEPS; ++s) {
-      float sv, bv;
-      uint32_t s16, b16;
-      cur.group_affine(a, s, lane, sv, bv, s16, b16);  // (a permute: every lane takes part)
-      const int wd = s * 64 + lane;
-      if (!live || wd >= a.wpr) continue;
-      char* op = reinterpret_cast<char*>(a.out) + (t * a.os + (int64_t)wd * 8) * S::kBytes;
-      if (fast) {
-        const u32x4 o = deq_word_fast<S, HS>(cur.codes[s], s16, sv, bv, o16, R);
-        __builtin_nontemporal_store(o, reinterpret_cast<u32x4*>(op));
-        continue;
-      }
-      float v[8];
+  const uint32_t tb = (uint32_t)(size_t)(lds_u16*)&lut[wv][0];
 #pragma unroll
-      for (int nib = 0; nib < 8; ++nib) {
-        const uint32_t q = (cur.codes[s] >> (4 * nib)) & 0xfu;
-        float x = deq<S>(q, sv, bv);
-        x = HS ? S::round(x * osc) : x;
-        v[nib] = x;
+  for (int j = 0; j < GPL; ++j) {
+    if (64 * j >= a.gpr) break;  // uniform
+    const float sv = S::lo(sr[j]), bv = S::lo(br[j]);
+    uint32_t e[8];
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      float p0 = (float)(2 * m) * sv, p1 = (float)(2 * m + 1) * sv;
+      round2<S>(p0, p1);
+      p0 += bv;
+      p1 += bv;
+      if (a.has_scale) {
+        round2<S>(p0, p1);
+        p0 *= osc;
+        p1 *= osc;
       }
-      store_elems<S, 8>(a.out, t * a.os + (int64_t)wd * 8, v);
+      e[m] = S::pack(p0, p1);
     }
+    if (lane + 64 * j < a.gpr) {
+      lds_u32x4* dst = (lds_u32x4*)(size_t)(tb + (uint32_t)(lane + 64 * j) * 32u);
+      dst[0] = u32x4{e[0], e[1], e[2], e[3]};
+      dst[1] = u32x4{e[4], e[5], e[6], e[7]};
+    }
+  }
+  // the wave's own LDS writes are performed before its later LDS reads;
+  // these keep the compiler from moving the reads above the writes
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  const int gsh = GSH ? GSH : a.group_shift;
+  // byte selectors of the permute (byte j of the code bytes, then the
+  // address's upper three bytes), in registers
+  uint32_t sel[4] = {0x07060500u, 0x07060501u, 0x07060502u, 0x07060503u};
+  asm volatile("" : "+v"(sel[0]), "+v"(sel[1]), "+v"(sel[2]), "+v"(sel[3]));
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s) {
+    const int wd = s * 64 + lane;
+    if (wd >= a.wpr) continue;
+    const uint32_t g = (uint32_t)wd >> gsh;
+    const uint32_t lo8 = ((g & 7u) << 5) * 0x01010101u;
+    const uint32_t hb = tb + ((g >> 3) << 8);
+    const uint32_t c = codes[s];
+    const uint32_t ev = ((c << 1) & 0x1e1e1e1eu) | lo8;  // byte j: entry of code 2j
+    const uint32_t od = ((c >> 3) & 0x1e1e1e1eu) | lo8;  // byte j: entry of code 2j + 1
+    u32x4 o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      u16x2 v;
+      v.x = *(const lds_u16*)(size_t)__builtin_amdgcn_perm(hb, ev, sel[j]);
+      v.y = *(const lds_u16*)(size_t)__builtin_amdgcn_perm(hb, od, sel[j]);
+      o[j] = __builtin_bit_cast(uint32_t, v);
+    }
+    __builtin_nontemporal_store(o, reinterpret_cast<u32x4*>(obase + s * 512 * S::kBytes));
   }
 }
 
@@ -397,7 +213,7 @@ __global__ __launch_bounds__(256) void qembed_generic_kernel(QembArgs a) {
   }
 }
 
-// Gather + dequantize + RMSNorm: one wave per token, as qembed_kernel. The
+// Gather + dequantize + RMSNorm: one wave per token, as the gather. The
 // row's values are kept packed in S (they are exactly S values) while the f64
 // sum of squares is reduced across the wave; the norm weights (W = S or f32)
 // are loaded with the codes. Computation type T = promote(S, w'), as in
@@ -530,46 +346,31 @@ __global__ __launch_bounds__(256) void qembed_norm_generic_kernel(QembArgs a) {
 
 namespace {
 
-template <class S, int TPW, bool HS>
-void launch_rows(const QembArgs& a, int steps, hipStream_t s) {
-  const int64_t nwaves = (a.n + TPW - 1) / TPW;
-  const dim3 g((unsigned)((nwaves + 3) / 4)), b(256);
-  if (steps <= 1) HGK_LAUNCH((qembed_rows_kernel<S, 1, TPW, HS>), g, b, 0, s, a, nwaves);
-  else if (steps <= 2) HGK_LAUNCH((qembed_rows_kernel<S, 2, TPW, HS>), g, b, 0, s, a, nwaves);
-  else if (steps <= 4) HGK_LAUNCH((qembed_rows_kernel<S, 4, TPW, HS>), g, b, 0, s, a, nwaves);
-  else if (steps <= 7) HGK_LAUNCH((qembed_rows_kernel<S, 7, TPW, HS>), g, b, 0, s, a, nwaves);
-  else HGK_LAUNCH((qembed_rows_kernel<S, 8, TPW, HS>), g, b, 0, s, a, nwaves);
-}
-
-template <class S, bool PERM>
-void launch_fast(const QembArgs& a, int steps, hipStream_t s) {
-  // waves: one per token up to what the chip keeps resident (8 per SIMD)
-  const int wpb = a.n >= 1024 ? 4 : 1;
-  const int64_t waves = std::min<int64_t>(a.n, (int64_t)resident_waves());
-  const dim3 g((unsigned)((waves + wpb - 1) / wpb)), b(64 * wpb);
-  if (steps <= 1) HGK_LAUNCH((qembed_kernel<S, 1, PERM>), g, b, 0, s, a);
-  else if (steps <= 2) HGK_LAUNCH((qembed_kernel<S, 2, PERM>), g, b, 0, s, a);
-  else if (steps <= 4) HGK_LAUNCH((qembed_kernel<S, 4, PERM>), g, b, 0, s, a);
-  else if (steps <= 7) HGK_LAUNCH((qembed_kernel<S, 7, PERM>), g, b, 0, s, a);
-  else if (steps <= 8) HGK_LAUNCH((qembed_kernel<S, 8, PERM>), g, b, 0, s, a);
-  else HGK_LAUNCH((qembed_kernel<S, 16, PERM>), g, b, 0, s, a);
+template <class S, int GSH>
+bool launch_lut(const QembArgs& a, hipStream_t s) {
+  const int steps = (a.wpr + 63) / 64;
+  // four waves per workgroup once there are enough tokens to fill the chip;
+  // fewer tokens spread one per workgroup over more CUs
+  const int wpb = a.n >= 1024 ? kLutWaves : 1;
+  const dim3 g((unsigned)((a.n + wpb - 1) / wpb)), b(64 * wpb);
+  const bool wide = a.gpr > 64;
+  if (steps <= 1) HGK_LAUNCH((qembed_lut_kernel<S, 1, GSH, 64>), g, b, 0, s, a);
+  else if (steps <= 2) HGK_LAUNCH((qembed_lut_kernel<S, 2, GSH, 64>), g, b, 0, s, a);
+  else if (steps <= 4) HGK_LAUNCH((qembed_lut_kernel<S, 4, GSH, 64>), g, b, 0, s, a);
+  else if (steps <= 7 && !wide) HGK_LAUNCH((qembed_lut_kernel<S, 7, GSH, 64>), g, b, 0, s, a);
+  else if (steps <= 7) HGK_LAUNCH((qembed_lut_kernel<S, 7, GSH, 256>), g, b, 0, s, a);
+  else if (steps <= 8 && !wide) HGK_LAUNCH((qembed_lut_kernel<S, 8, GSH, 64>), g, b, 0, s, a);
+  else if (steps <= 8) HGK_LAUNCH((qembed_lut_kernel<S, 8, GSH, 256>), g, b, 0, s, a);
+  else if (steps <= 16 && !wide) HGK_LAUNCH((qembed_lut_kernel<S, 16, GSH, 64>), g, b, 0, s, a);
+  else if (steps <= 16 && a.gpr <= 256) HGK_LAUNCH((qembed_lut_kernel<S, 16, GSH, 256>), g, b, 0, s, a);
+  else return false;
+  return true;
 }
 
 template <class S>
-void launch(const QembArgs& a, bool vec_ok, bool perm_ok, hipStream_t s) {
-  const int steps = (a.wpr + 63) / 64;
-  // four rows in flight per wave where that still leaves half the resident
-  // waves (measured at 16384 tokens of 256000 x 3584: 6 % faster than one
-  // token in flight; at 4096 tokens, with 1024 waves, 45 % slower)
-  if (vec_ok && perm_ok && steps <= 8 && a.n >= 2 * (int64_t)resident_waves()) {
-    if (a.has_scale) launch_rows<S, 4, true>(a, steps, s);
-    else launch_rows<S, 4, false>(a, steps, s);
-    return;
-  }
-  if (vec_ok && steps <= 16) {
-    if (perm_ok) launch_fast<S, true>(a, steps, s);
-    else launch_fast<S, false>(a, steps, s);
-    return;
+void launch(const QembArgs& a, bool vec_ok, hipStream_t s) {
+  if (vec_ok) {
+    if (a.group == 64 ? launch_lut<S, 3>(a, s) : launch_lut<S, 0>(a, s)) return;
   }
   const int64_t blocks = std::min<int64_t>((a.n * a.hidden + 255) / 256, (int64_t)1 << 20);
   HGK_LAUNCH((qembed_generic_kernel<S>), dim3((unsigned)blocks), dim3(256), 0, s, a);
@@ -610,19 +411,12 @@ extern "C" int hgk_quantized_embedding(const void* ids, int ids_dtype, int64_t n
   a.ids = ids; a.ids_i32 = ids_dtype == DT_I32; a.n = n_ids; a.wq = w_q; a.sc = scales;
   a.bi = biases; a.vocab = vocab; a.wpr = (int)(hidden / 8); a.gpr = (int)(hidden / group_size);
   a.group = group_size; a.scale = out_scale; a.has_scale = out_scale != 0.0f;
-  // the dot2 form takes positive output scales in [2^-19, 2^19]: every
-  // product stays normal, and no +0 element changes sign (a negative scale
-  // takes the element-by-element form, which gives the reference's -0)
-  a.fast_scale_ok = !a.has_scale || (out_scale >= 0x1p-19f && out_scale <= 0x1p19f);
+  a.group_shift = group_size == 32 ? 2 : group_size == 64 ? 3 : 4;
   a.out = out; a.os = out_row_stride; a.hidden = hidden;
   const bool vec_ok = (reinterpret_cast<uintptr_t>(w_q) & 3u) == 0 && aligned16(out) &&
                       hidden % 8 == 0 && out_row_stride % 8 == 0;
-  // one 32-bit load per lane brings a row's scales and biases when they fit
-  // one register across the wave and every row's pairs are 4-byte aligned
-  const bool perm_ok = a.gpr % 2 == 0 && a.gpr <= 64 &&
-                       ((reinterpret_cast<uintptr_t>(scales) | reinterpret_cast<uintptr_t>(biases)) & 3u) == 0;
-  if (scales_dtype == DT_BF16) launch<BF16>(a, vec_ok, perm_ok, as_stream(stream));
-  else launch<F16>(a, vec_ok, perm_ok, as_stream(stream));
+  if (scales_dtype == DT_BF16) launch<BF16>(a, vec_ok, as_stream(stream));
+  else launch<F16>(a, vec_ok, as_stream(stream));
   return launch_status(fn);
 }
 

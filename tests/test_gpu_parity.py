@@ -424,24 +424,24 @@ def test_qembed_codes_bitexact_and_variants(dev):
 
 
 @pytest.mark.parametrize("V,Hd,n,group,sdt,offset", [
-    (300, 4608, 9000, 32, O.BF16, 0),   # 144 groups a row: one scale/bias load per step
-    (300, 448, 9000, 64, O.BF16, 0),    # 7 groups (odd): one scale/bias load per step
-    (300, 3584, 9000, 64, O.F16, 0),    # 56 groups: one load per row, permuted
+    (300, 4608, 9000, 32, O.BF16, 0),   # 144 groups a row: the 256-group table, 9 of 16 steps
+    (300, 448, 9000, 64, O.BF16, 0),    # 7 groups, one partial step
+    (300, 3584, 9000, 64, O.F16, 0),    # 56 groups
     (300, 2048, 8193, 64, O.BF16, 1),   # scales/biases 2-byte aligned only
-    (300, 8192, 8500, 128, O.BF16, 0),  # 16 steps a row, permuted
-    # 16384 ids and more: four rows in flight per wave (permuted loads only)
-    (300, 3584, 16387, 64, O.F16, 0),   # f16, a ragged last stride of tokens
+    (300, 8192, 8500, 128, O.BF16, 0),  # 16 steps a row, group 128
+    (300, 3584, 16387, 64, O.F16, 0),   # f16, a ragged last workgroup
     (300, 2048, 20000, 32, O.BF16, 0),  # 64 groups a row
     (300, 1024, 16384, 128, O.BF16, 0), # 2 steps a row
-    (300, 2048, 16384, 64, O.BF16, 1),  # 2-byte aligned: the one-token kernel
+    (300, 3584, 5000, 32, O.BF16, 0),   # 112 groups: 7 steps, the 256-group table
+    (300, 4096, 5000, 32, O.F16, 1),    # 128 groups: 8 steps, two table groups per lane
+    (300, 8192, 3000, 32, O.BF16, 0),   # 256 groups: the largest table
+    (300, 8192, 700, 64, O.BF16, 0),    # 128 groups, fewer than 1024 ids (one wave a workgroup)
 ])
 def test_qembed_row_load_forms(dev, V, Hd, n, group, sdt, offset):
-    """Both ways of loading a row's scales and biases (one 32-bit load per
-    lane plus a cross-lane permute when the row's groups fit one register and
-    are 4-byte aligned, else a 16-bit load per step), each with more ids than
-    the chip keeps waves resident, so every wave runs the pipelined loop over
-    several tokens; from 16384 ids, the kernel that keeps four rows in flight
-    per wave. Bit-exact against the oracle."""
+    """The table gather at every table size (64 and 256 groups; one to four
+    groups per lane), group 32, 64 and 128, partial last steps, scales and
+    biases at a 2-byte offset, one and four waves per workgroup. Bit-exact
+    against the oracle."""
     key = 1870 + group + Hd
     wq = O.u32(key, (V, Hd // 8))
     s = O.from_f32(O.uniform(key + 1, (V, Hd // group), 0.005, 0.02), sdt)
@@ -460,9 +460,8 @@ def test_qembed_row_load_forms(dev, V, Hd, n, group, sdt, offset):
     assert np.array_equal(got, ref)
 
 
-def test_qembed_more_than_64_tokens_per_wave(dev):
-    """600,000 ids: more than 64 per resident wave (8192 waves on an MI355X),
-    so every persistent wave runs a long pipelined loop over its tokens; int32
+def test_qembed_600k_ids(dev):
+    """600,000 ids (150,000 workgroups, many rounds of resident waves); int32
     ids with negative (from the end) and out-of-range values. Bit-exact."""
     V, Hd, n = 1000, 256, 600000
     key = 1940
@@ -497,15 +496,16 @@ def _bits16(key, shape, sdt, exp_lo, exp_hi, zero_frac=0.0):
 @pytest.mark.parametrize("sdt", [O.BF16, O.F16])
 @pytest.mark.parametrize("out_scale", [0.0, math.sqrt(3584.0), -math.sqrt(3584.0), -0.75])
 def test_qembed_any_scale_and_bias_values(dev, sdt, out_scale):
-    """Rows whose scales and biases span every exponent the dot2 form takes
-    (bf16: scales of either sign from 2^-100 to 2^100, biases +-0 or from
-    2^-100 to 2^126, so that round(q s) + b is often inexact in f32; f16:
-    normal scales below 2^12, biases below 2^11), rows of arbitrary 16-bit
-    codes (zeros, subnormals, huge values, inf, NaN: those rows take the
-    element-by-element form and overflow) and ordinary rows, with and without
-    the output scale, positive or negative (a negative one turns row 7's +0
-    elements into -0). Bit-exact against the oracle, zero signs included (NaN
-    positions compared as a mask)."""
+    """Rows whose scales and biases span wide exponent ranges (bf16: scales
+    of either sign from 2^-100 to 2^100, biases +-0 or from 2^-100 to 2^126,
+    so that round(q s) + b is often inexact in f32; f16: normal scales below
+    2^12, biases below 2^11), rows of arbitrary 16-bit codes (zeros,
+    subnormals, huge values, inf, NaN, overflowing products) and ordinary
+    rows, with and without the output scale, positive or negative (a negative
+    one turns row 7's +0 elements into -0). The gather's tables hold each
+    group's 16 values from the element formula, so every such row must come
+    out as the oracle's: bit-exact, zero signs included (NaN positions
+    compared as a mask)."""
     V, Hd, n = 1536, 2048, 3000
     G = Hd // 64
     key = 1950 + 10 * sdt + int(out_scale > 0) + 2 * int(out_scale < 0)
