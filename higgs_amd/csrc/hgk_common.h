@@ -42,7 +42,12 @@ struct BF16 {
     bf16x2 h = __builtin_convertvector(v, bf16x2);
     return __builtin_bit_cast(uint32_t, h);
   }
-  __device__ static float round(float a) { return u2f(pack(a, 0.0f) << 16); }
+  // a rounded to bf16, as f32: one v_cvt_pk_bf16_f32 with +0 in the low half,
+  // whose result is the f32 bit pattern of the rounded value
+  __device__ static float round(float a) {
+    f32x2 v = {0.0f, f32_barrier(a)};
+    return __builtin_bit_cast(float, __builtin_convertvector(v, bf16x2));
+  }
 };
 
 struct F16 {
@@ -59,7 +64,7 @@ struct F16 {
     f16x2 h = __builtin_convertvector(v, f16x2);
     return __builtin_bit_cast(uint32_t, h);
   }
-  __device__ static float round(float a) { return lo(pack(a, 0.0f)); }
+  __device__ static float round(float a) { return (float)(_Float16)f32_barrier(a); }
 };
 
 struct F32 {
@@ -71,10 +76,15 @@ struct F32 {
 // Elements of T per 16-byte chunk.
 template <class T> struct Vec { static constexpr int N = 16 / T::kBytes; };
 
-// Round two f32 values to T in place with one packed conversion.
+// Round two f32 values to T in place: bf16 with one conversion each (the
+// rounded value lands in the high half, where it is already an f32); f16
+// with one packed conversion and two widenings.
 template <class T>
 __device__ inline void round2(float& a, float& b) {
-  if constexpr (T::kBytes == 2) {
+  if constexpr (T::kCode == DT_BF16) {
+    a = T::round(a);
+    b = T::round(b);
+  } else if constexpr (T::kBytes == 2) {
     const uint32_t p = T::pack(a, b);
     a = T::lo(p);
     b = T::hi(p);
@@ -317,6 +327,67 @@ __device__ inline double group_sum(double v) {
 __device__ inline float rms_scale(double ss, float inv_n, float eps) {
   const float ms = (float)ss * inv_n;
   return 1.0f / sqrtf(ms + eps);
+}
+
+// cos(th) and sin(th) of an f32 angle, evaluated in f64 and rounded to f32
+// (RoPE's tables). For |th| < 2^20: th - k pi/2 with k = rint(th 2/pi) and
+// pi/2 split in three parts (33 + 33 + 53 bits, so k P1 and k P2 are exact
+// for |k| < 2^20), then the Taylor series of sin to r^17 and cos to r^16 on
+// |r| <= pi/4 (truncation below 2^-57 relative) by Horner in f64, and the
+// quadrant k mod 4: about 35 f64 operations against ~150 for the library's
+// sincos, whose general reduction covers any double. Within 3 f64 ulps of the
+// true values (measured: 2.8 ulps over 2e8 angles, whose f32 roundings all
+// equal those of the C library's sin/cos); larger angles and non-finite ones
+// take the library's sincos.
+// The library's sincos for the angles the fast path does not take, out of
+// line: inlined, its general argument reduction would hold registers that the
+// callers' common path then cannot use.
+struct SinCos {
+  double s, c;
+};
+__device__ __attribute__((noinline)) SinCos sincos_wide(double x) {
+  SinCos r;
+  sincos(x, &r.s, &r.c);
+  return r;
+}
+
+__device__ inline void cos_sin_f32(float th, float& c, float& s) {
+  double sd, cd;
+  if (fabsf(th) < 0x1p20f) {
+    const double x = (double)th;
+    const double k = __builtin_rint(x * 0x1.45f306dc9c883p-1);  // 2/pi
+    double r = __builtin_fma(-k, 0x1.921fb54400000p+0, x);
+    r = __builtin_fma(-k, 0x1.0b4611a600000p-34, r);
+    r = __builtin_fma(-k, 0x1.3198a2e037073p-69, r);
+    const double r2 = r * r;
+    // (-1)^n / (2n+1)! and (-1)^n / (2n)!, n = 8 .. 1
+    double ps = 2.8114572543455206e-15, pc = 4.779477332387385e-14;
+    ps = __builtin_fma(ps, r2, -7.647163731819816e-13);
+    pc = __builtin_fma(pc, r2, -1.1470745597729725e-11);
+    ps = __builtin_fma(ps, r2, 1.6059043836821613e-10);
+    pc = __builtin_fma(pc, r2, 2.08767569878681e-09);
+    ps = __builtin_fma(ps, r2, -2.505210838544172e-08);
+    pc = __builtin_fma(pc, r2, -2.755731922398589e-07);
+    ps = __builtin_fma(ps, r2, 2.7557319223985893e-06);
+    pc = __builtin_fma(pc, r2, 2.48015873015873e-05);
+    ps = __builtin_fma(ps, r2, -0.0001984126984126984);
+    pc = __builtin_fma(pc, r2, -0.001388888888888889);
+    ps = __builtin_fma(ps, r2, 0.008333333333333333);
+    pc = __builtin_fma(pc, r2, 0.041666666666666664);
+    ps = __builtin_fma(ps, r2, -0.16666666666666666);
+    pc = __builtin_fma(pc, r2, -0.5);
+    const double sv = __builtin_fma(r * r2, ps, r), cv = __builtin_fma(r2, pc, 1.0);
+    const int q = (int)k & 3;
+    const double a = (q & 1) ? cv : sv, b = (q & 1) ? sv : cv;  // sin, cos up to sign
+    sd = (q & 2) ? -a : a;
+    cd = ((q + 1) & 2) ? -b : b;
+  } else {
+    const SinCos w = sincos_wide((double)th);
+    sd = w.s;
+    cd = w.c;
+  }
+  c = (float)cd;
+  s = (float)sd;
 }
 
 }  // namespace hgk

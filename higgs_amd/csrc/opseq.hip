@@ -220,11 +220,10 @@ __device__ void op_rope(const DevOp& op, int64_t t, float* cs, float* sn) {
       const int32_t off = op.offsets ? op.offsets[t] : op.offset;
       const float pos = (0.0f + (float)off) * op.scale;
       for (int i = threadIdx.x; i < op.half; i += kOpThreads) {
-        const float th = pos * op.inv_freq[i];
-        double s, c;
-        sincos((double)th, &s, &c);
-        cs[i] = X::round((float)c);
-        sn[i] = X::round((float)s);
+        float c, s;
+        cos_sin_f32(pos * op.inv_freq[i], c, s);
+        cs[i] = X::round(c);
+        sn[i] = X::round(s);
       }
       __syncthreads();
     }

@@ -26,8 +26,8 @@
 //   c = round_T(cos th), s = round_T(sin th)
 //   y1 = round_T(round_T(x1*c) - round_T(x2*s))
 //   y2 = round_T(round_T(x1*s) + round_T(x2*c))
-// cos/sin are evaluated in f64 and rounded to f32 (close to correctly rounded
-// even at |th| ~ 3e4), then to T.
+// cos/sin are evaluated in f64 and rounded to f32 (cos_sin_f32: within 3 f64
+// ulps of the true values at any |th| < 2^20), then to T.
 #include <algorithm>
 
 #include "../../include/higgs_hip.h"
@@ -69,11 +69,10 @@ __device__ inline void fill_table(const RopeArgs& a, float* cs, float* sn, uint3
     const uint32_t b = tok / a.L, l = tok - b * a.L;
     const int32_t off = a.offsets ? a.offsets[b] : a.offset;
     const float pos = ((float)l + (float)off) * a.scale;
-    const float th = pos * a.inv_freq[i];
-    double s, c;
-    sincos((double)th, &s, &c);
-    cs[e] = X::round((float)c);
-    sn[e] = X::round((float)s);
+    float c, s;
+    cos_sin_f32(pos * a.inv_freq[i], c, s);
+    cs[e] = X::round(c);
+    sn[e] = X::round(s);
   }
 }
 
@@ -192,7 +191,7 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
   // the square root and division of a batch's four rows are done once per
   // quad of lanes (lane j finishes row j % 4) and broadcast by DPP
   constexpr bool SHARED = NORM && RB == 4 && LPR >= 4;
-  extern __shared__ float smem[];
+  extern __shared__ __align__(16) float smem[];
   float* cs = smem;
   float* sn = smem + a.tpb * a.half;
   const uint32_t t0 = blockIdx.x * (uint32_t)a.tpb;
@@ -204,11 +203,17 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
   const int c0 = rot ? j : 2 * j;
   const int c1 = rot ? j + a.R : 2 * j + 1;
 
-  // norm weights of q and k for this lane's two chunks, packed
-  u32x4 w0q{1u, 1u, 1u, 1u}, w1q = w0q, w0k = w0q, w1k = w0q;
+  // norm weights of q and k, packed, staged in LDS after the table ([2][D / V]
+  // chunks, read per row): held in registers for the whole kernel they cost
+  // the 16 VGPRs that decide between 3 and 4 waves per SIMD
+  u32x4* wl = reinterpret_cast<u32x4*>(sn + a.tpb * a.half);
+  const int nch = a.D / V;
   if constexpr (NORM) {
-    if (a.t[0].nw) { w0q = ld16<X>(a.t[0].nw, c0 * V); w1q = ld16<X>(a.t[0].nw, c1 * V); }
-    if (a.t[1].nw) { w0k = ld16<X>(a.t[1].nw, c0 * V); w1k = ld16<X>(a.t[1].nw, c1 * V); }
+    for (int e = threadIdx.x; e < 2 * nch; e += blockDim.x) {
+      const int which = e >= nch ? 1 : 0;
+      const void* nw = a.t[which].nw;
+      wl[e] = nw ? ld16<X>(nw, (e - which * nch) * V) : u32x4{0u, 0u, 0u, 0u};
+    }
   }
 
   const RopePair pr = rope_pair(a);
@@ -250,7 +255,7 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
     }
   };
 
-  // the first batch's loads go out before the block spends time on sincos
+  // the first batch's loads go out before the block builds its table
   load_batch(slot);
   fill_table<X>(a, cs, sn, t0, ntok);
   __syncthreads();
@@ -308,7 +313,7 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
         const bool has = isk ? (a.t[1].nw != nullptr) : (a.t[0].nw != nullptr);
         if (has) {  // uniform across the row's lane group
           const float rs = rsk[k];
-          const u32x4 wa = isk ? w0k : w0q, wb = isk ? w1k : w1q;
+          const u32x4 wa = wl[(isk ? nch : 0) + c0], wb = wl[(isk ? nch : 0) + c1];
 #pragma unroll
           for (int e = 0; e < V; e += 2) {  // roundings paired: one conversion per two
             float p0 = v0[e] * rs, p1 = v0[e + 1] * rs, q0 = v1[e] * rs, q1 = v1[e + 1] * rs;
@@ -399,7 +404,7 @@ __global__ __launch_bounds__(256) void rope_lane_kernel(RopeArgs a) {
   constexpr int RB = kRopeLaneBatch;
   constexpr int slots = 256 / LPR;
   static_assert(2 * R <= LPR, "rotated chunks within the row");
-  extern __shared__ float smem[];
+  extern __shared__ __align__(16) float smem[];
   float* cs = smem;
   float* sn = smem + a.tpb * a.half;
   const uint32_t t0 = blockIdx.x * (uint32_t)a.tpb;
@@ -411,10 +416,14 @@ __global__ __launch_bounds__(256) void rope_lane_kernel(RopeArgs a) {
   const bool first = j < R;
   const int f0 = (j & (R - 1)) * V;  // this lane's first frequency index
 
-  u32x4 wq{1u, 1u, 1u, 1u}, wk = wq;
+  // norm weights of q and k, packed, in LDS after the table ([2][D / V] chunks)
+  u32x4* wl = reinterpret_cast<u32x4*>(sn + a.tpb * a.half);
   if constexpr (NORM) {
-    if (a.t[0].nw) wq = ld16<X>(a.t[0].nw, j * V);
-    if (a.t[1].nw) wk = ld16<X>(a.t[1].nw, j * V);
+    for (int e = threadIdx.x; e < 2 * LPR; e += blockDim.x) {
+      const int which = e >= LPR ? 1 : 0;
+      const void* nw = a.t[which].nw;
+      wl[e] = nw ? ld16<X>(nw, (e - which * LPR) * V) : u32x4{0u, 0u, 0u, 0u};
+    }
   }
 
   const RopePair pr = rope_pair(a);
@@ -472,7 +481,7 @@ __global__ __launch_bounds__(256) void rope_lane_kernel(RopeArgs a) {
           for (int e = 0; e < V; ++e) ss = __builtin_fma((double)v[e], (double)v[e], ss);
           ss = group_sum<LPR>(ss);
           const float rs = rms_scale(ss, a.inv_d, a.eps);
-          const u32x4 w = isk ? wk : wq;
+          const u32x4 w = wl[(isk ? LPR : 0) + j];
 #pragma unroll
           for (int e = 0; e < V; e += 2) {
             float p0 = v[e] * rs, p1 = v[e + 1] * rs;
@@ -554,10 +563,9 @@ __global__ __launch_bounds__(256) void rope_generic_kernel(RopeArgs a) {
     const bool act = d < a.D;
     if (act) {
       if (d < a.half) {
-        const float th = pos * a.inv_freq[d];
-        double s, c;
-        sincos((double)th, &s, &c);
-        const float cf = X::round((float)c), sf = X::round((float)s);
+        float c, s;
+        cos_sin_f32(pos * a.inv_freq[d], c, s);
+        const float cf = X::round(c), sf = X::round(s);
         const float x1 = val(d), x2 = val(d + a.half);
         o1 = X::round(X::round(x1 * cf) - X::round(x2 * sf));
         o2 = X::round(X::round(x1 * sf) + X::round(x2 * cf));
@@ -607,7 +615,8 @@ void launch_fast(RopeArgs& a, hipStream_t s) {
   a.tpb = tpb;
   a.hsum_magic = a.hsum >= 2 ? (uint32_t)((((uint64_t)1 << 32) + a.hsum - 1) / a.hsum) : 0u;
   const unsigned blocks = (a.tokens + tpb - 1) / tpb;
-  const size_t shmem = 2u * tpb * a.half * sizeof(float);
+  // the cos/sin table, then the packed norm weights of q and k
+  const size_t shmem = 2u * tpb * a.half * sizeof(float) + 2u * a.D * X::kBytes;
   if (fast_index_ok(a))
     HGK_LAUNCH((rope_kernel<X, LPR, NORM, true>), dim3(blocks), dim3(256), shmem, s, a);
   else
@@ -623,7 +632,7 @@ void launch_lane(RopeArgs& a, hipStream_t s) {
   a.tpb = tpb;
   a.hsum_magic = a.hsum >= 2 ? (uint32_t)((((uint64_t)1 << 32) + a.hsum - 1) / a.hsum) : 0u;
   const unsigned blocks = (a.tokens + tpb - 1) / tpb;
-  const size_t shmem = 2u * tpb * a.half * sizeof(float);
+  const size_t shmem = 2u * tpb * a.half * sizeof(float) + 2u * a.D * X::kBytes;
   if (fast_index_ok(a))
     HGK_LAUNCH((rope_lane_kernel<X, LPR, R, NORM, true>), dim3(blocks), dim3(256), shmem, s, a);
   else
