@@ -330,9 +330,23 @@ def test_fused_gate_up_swiglu_grouped_prefill(dev):
     three = O.glu(O.ACT_SILU, gh, uh, O.BF16)
     assert np.array_equal(got, three), "fused grouped result differs from the three calls"
     assert not got[[7, 20000]].any()
-    rows = np.r_[0:256, T * top_k - 256:T * top_k]
+    # the oracle on 2,560 pairs spread over the whole call (every 16th pair,
+    # so every expert's list contributes): both projections within the
+    # contraction bar, and the fused output equal to the oracle's SwiGLU of
+    # the oracle's projections wherever the device's projections are the
+    # oracle's (elsewhere SiLU's slope may widen a 1-ulp gate difference)
+    rows = np.arange(0, T * top_k, 16)
+    rows = rows[(rows != 7) & (rows != 20000)]
     rg = O.gather_qmm(x, O.BF16, g[0], g[1], g[2], O.BF16, ex[rows], lhs=rows // top_k)
+    ru = O.gather_qmm(x, O.BF16, u[0], u[1], u[2], O.BF16, ex[rows], lhs=rows // top_k)
     _check(gh[rows], rg, O.BF16, "grouped fused: gate projection (sampled pairs)")
+    _check(uh[rows], ru, O.BF16, "grouped fused: up projection (sampled pairs)")
+    full = O.glu(O.ACT_SILU, rg, ru, O.BF16)
+    same = (gh[rows] == rg) & (uh[rows] == ru)
+    assert same.mean() >= 0.98, f"projections equal to the oracle's on {same.mean():.4f}"
+    assert np.array_equal(got[rows][same], full[same]), "fused output differs from the oracle's SwiGLU"
+    print(f"[qmm] grouped fused: output vs oracle composition exact={exact_frac(got[rows], full, O.BF16):.5f}",
+          flush=True)
     # group 32: the fused grouped kernel does not take it
     T2, E2, K2 = 512, 8, 1024
     x2, g2, u2, ex2 = _fused_case(4211, T2, 4, E2, 256, K2, group=32)
