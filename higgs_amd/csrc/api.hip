@@ -57,6 +57,23 @@ int resident_waves() {
   return v;
 }
 
+int lds_per_cu() {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<int> cached[kMaxDevices];  // 0: not yet queried
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) dev = -1;
+  if (dev >= 0) {
+    const int v = cached[dev].load(std::memory_order_relaxed);
+    if (v > 0) return v;
+  }
+  int bytes = 0;
+  if (hipDeviceGetAttribute(&bytes, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor,
+                            dev < 0 ? 0 : dev) != hipSuccess || bytes <= 0)
+    bytes = 160 * 1024;
+  if (dev >= 0) cached[dev].store(bytes, std::memory_order_relaxed);
+  return bytes;
+}
+
 }  // namespace hgk
 
 using namespace hgk;

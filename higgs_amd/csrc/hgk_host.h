@@ -19,6 +19,8 @@ int launch_status(const char* what);
 // VGPRs: compute units x 4 SIMDs x 8 waves (256 x 32 = 8192 on MI355X).
 // Queried once per device; used to size persistent (grid-stride) launches.
 int resident_waves();
+// LDS bytes per CU of the current device (160 KB on gfx950).
+int lds_per_cu();
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 

@@ -354,15 +354,25 @@ bool launch_lut(const QembArgs& a, hipStream_t s) {
   const int wpb = a.n >= 1024 ? kLutWaves : 1;
   const dim3 g((unsigned)((a.n + wpb - 1) / wpb)), b(64 * wpb);
   const bool wide = a.gpr > 64;
-  if (steps <= 1) HGK_LAUNCH((qembed_lut_kernel<S, 1, GSH, 64>), g, b, 0, s, a);
-  else if (steps <= 2) HGK_LAUNCH((qembed_lut_kernel<S, 2, GSH, 64>), g, b, 0, s, a);
-  else if (steps <= 4) HGK_LAUNCH((qembed_lut_kernel<S, 4, GSH, 64>), g, b, 0, s, a);
-  else if (steps <= 7 && !wide) HGK_LAUNCH((qembed_lut_kernel<S, 7, GSH, 64>), g, b, 0, s, a);
-  else if (steps <= 7) HGK_LAUNCH((qembed_lut_kernel<S, 7, GSH, 256>), g, b, 0, s, a);
-  else if (steps <= 8 && !wide) HGK_LAUNCH((qembed_lut_kernel<S, 8, GSH, 64>), g, b, 0, s, a);
-  else if (steps <= 8) HGK_LAUNCH((qembed_lut_kernel<S, 8, GSH, 256>), g, b, 0, s, a);
-  else if (steps <= 16 && !wide) HGK_LAUNCH((qembed_lut_kernel<S, 16, GSH, 64>), g, b, 0, s, a);
-  else if (steps <= 16 && a.gpr <= 256) HGK_LAUNCH((qembed_lut_kernel<S, 16, GSH, 256>), g, b, 0, s, a);
+  // Four-wave workgroups ask for a quarter of the CU's LDS (dynamic shared
+  // memory the kernel leaves unused), so a CU holds at most four of them: 16
+  // waves rather than 32. At 16384 ids of 256000 x 3584 that took 26.4 us
+  // against 27.5 at 32 waves per CU, 26.7 at 20, 27.5 at 12 and 31.3 at 8:
+  // fewer rows read at random at once run faster, until too few waves hide
+  // the latency. (Walking several tokens per wave in a grid of that size
+  // instead took 29.5 us.)
+  const size_t table = (size_t)kLutWaves * (wide ? 256 : 64) * 32;
+  const size_t quarter = (size_t)lds_per_cu() / kLutWaves;
+  const size_t pad = wpb == kLutWaves && quarter > table ? quarter - table : 0;
+  if (steps <= 1) HGK_LAUNCH((qembed_lut_kernel<S, 1, GSH, 64>), g, b, pad, s, a);
+  else if (steps <= 2) HGK_LAUNCH((qembed_lut_kernel<S, 2, GSH, 64>), g, b, pad, s, a);
+  else if (steps <= 4) HGK_LAUNCH((qembed_lut_kernel<S, 4, GSH, 64>), g, b, pad, s, a);
+  else if (steps <= 7 && !wide) HGK_LAUNCH((qembed_lut_kernel<S, 7, GSH, 64>), g, b, pad, s, a);
+  else if (steps <= 7) HGK_LAUNCH((qembed_lut_kernel<S, 7, GSH, 256>), g, b, pad, s, a);
+  else if (steps <= 8 && !wide) HGK_LAUNCH((qembed_lut_kernel<S, 8, GSH, 64>), g, b, pad, s, a);
+  else if (steps <= 8) HGK_LAUNCH((qembed_lut_kernel<S, 8, GSH, 256>), g, b, pad, s, a);
+  else if (steps <= 16 && !wide) HGK_LAUNCH((qembed_lut_kernel<S, 16, GSH, 64>), g, b, pad, s, a);
+  else if (steps <= 16 && a.gpr <= 256) HGK_LAUNCH((qembed_lut_kernel<S, 16, GSH, 256>), g, b, pad, s, a);
   else return false;
   return true;
 }
