@@ -147,6 +147,31 @@ def test_rope_per_sequence_offsets_large(dev):
         _check_rope(got, ref, dt, f"rope offsets to 32768 dt={dt}")
 
 
+def test_rope_device_cos_sin_are_f32_of_f64(dev):
+    """The device's cos/sin table itself. In f32 with x1 = 1 and x2 = 0 a
+    RoPE returns its table entries: y1 = c, y2 = s. Over 4 sequences x 4096
+    positions x 64 frequencies (offsets 0 .. 2^21, so angles up to ~2.1e6
+    rad, through the fast evaluation below 2^20 rad and the library's beyond
+    it) every entry must equal the f32 rounding of the f64 cos/sin of the
+    same f32 angle, computed here by numpy (the oracle's TRIG_F64 choice)."""
+    B, L, D = 4, 4096, 128
+    offs = np.array([0, 5 * 4096, 2 ** 19 - 4096, 2 ** 21], np.int32)
+    x = torch.zeros((B, 1, L, D), dtype=torch.float32, device=dev)
+    x[..., : D // 2] = 1.0
+    y = H.rope(x, D, base=10000.0, offsets=torch.tensor(offs, device=dev))
+    got = to_host(y)[:, 0]
+    inv = np.array(H.rope_inv_freq(10000.0, D), np.float32)
+    pos = (np.arange(L, dtype=np.float32)[None, :] + offs[:, None].astype(np.float32)).astype(np.float32)
+    th = (pos[:, :, None] * inv[None, None, :]).astype(np.float32)
+    c = np.cos(th.astype(np.float64)).astype(np.float32)
+    s = np.sin(th.astype(np.float64)).astype(np.float32)
+    bad_c = got[..., : D // 2] != c
+    bad_s = got[..., D // 2:] != s
+    print(f"[rope] cos/sin table: {th.size} angles, max {float(np.abs(th).max()):.0f} rad, "
+          f"{int(bad_c.sum())} cos and {int(bad_s.sum())} sin entries differ", flush=True)
+    assert not bad_c.any() and not bad_s.any()
+
+
 def test_rope_generic_path_head80(dev):
     got, ref, dt = _rope_case(dev, B=2, L=9, Hq=3, D=80, dims=80, base=1e4, key=1107)
     _check_rope(got, ref, dt, "rope D=80 generic")
