@@ -100,6 +100,61 @@ typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kLutWaves = 4;  // waves per workgroup
 
+// Lane g's share of a row's table: the 16 values of groups g, g + 64, ...
+// (GPL of them) from their scales and biases, written at tb + 32 g.
+template <class S, int GPL>
+__device__ inline void lut_build(const QembArgs& a, const uint32_t* sr, const uint32_t* br,
+                                 float osc, uint32_t tb, int lane) {
+#pragma unroll
+  for (int j = 0; j < GPL; ++j) {
+    if (64 * j >= a.gpr) break;  // uniform
+    const float sv = S::lo(sr[j]), bv = S::lo(br[j]);
+    uint32_t e[8];
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      float p0 = (float)(2 * m) * sv, p1 = (float)(2 * m + 1) * sv;
+      round2<S>(p0, p1);
+      p0 += bv;
+      p1 += bv;
+      if (a.has_scale) {
+        round2<S>(p0, p1);
+        p0 *= osc;
+        p1 *= osc;
+      }
+      e[m] = S::pack(p0, p1);
+    }
+    if (lane + 64 * j < a.gpr) {
+      lds_u32x4* dst = (lds_u32x4*)(size_t)(tb + (uint32_t)(lane + 64 * j) * 32u);
+      dst[0] = u32x4{e[0], e[1], e[2], e[3]};
+      dst[1] = u32x4{e[4], e[5], e[6], e[7]};
+    }
+  }
+  // the wave's own LDS accesses are performed in order; these keep the
+  // compiler from moving the table reads above the writes
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+}
+
+// The 8 values of packed word wd (codes c) from the wave's table at tb:
+// out[j] = values 2j, 2j + 1. sel: the permute selectors 0x07060500 | j.
+template <int GSH>
+__device__ inline u32x4 lut_word(uint32_t c, int wd, int gsh, uint32_t tb, const uint32_t* sel) {
+  const uint32_t g = (uint32_t)wd >> (GSH ? GSH : gsh);
+  const uint32_t lo8 = ((g & 7u) << 5) * 0x01010101u;
+  const uint32_t hb = tb + ((g >> 3) << 8);
+  const uint32_t ev = ((c << 1) & 0x1e1e1e1eu) | lo8;  // byte j: entry of code 2j
+  const uint32_t od = ((c >> 3) & 0x1e1e1e1eu) | lo8;  // byte j: entry of code 2j + 1
+  u32x4 o;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    u16x2 v;
+    v.x = *(const lds_u16*)(size_t)__builtin_amdgcn_perm(hb, ev, sel[j]);
+    v.y = *(const lds_u16*)(size_t)__builtin_amdgcn_perm(hb, od, sel[j]);
+    o[j] = __builtin_bit_cast(uint32_t, v);
+  }
+  return o;
+}
+
 template <class S, int STEPS, int GSH, int TG>
 __global__ __launch_bounds__(64 * kLutWaves) void qembed_lut_kernel(QembArgs a) {
   __shared__ __align__(256) uint16_t lut[kLutWaves][TG * 16];
@@ -138,34 +193,7 @@ __global__ __launch_bounds__(64 * kLutWaves) void qembed_lut_kernel(QembArgs a) 
   }
   const float osc = S::round(a.scale);
   const uint32_t tb = (uint32_t)(size_t)(lds_u16*)&lut[wv][0];
-#pragma unroll
-  for (int j = 0; j < GPL; ++j) {
-    if (64 * j >= a.gpr) break;  // uniform
-    const float sv = S::lo(sr[j]), bv = S::lo(br[j]);
-    uint32_t e[8];
-#pragma unroll
-    for (int m = 0; m < 8; ++m) {
-      float p0 = (float)(2 * m) * sv, p1 = (float)(2 * m + 1) * sv;
-      round2<S>(p0, p1);
-      p0 += bv;
-      p1 += bv;
-      if (a.has_scale) {
-        round2<S>(p0, p1);
-        p0 *= osc;
-        p1 *= osc;
-      }
-      e[m] = S::pack(p0, p1);
-    }
-    if (lane + 64 * j < a.gpr) {
-      lds_u32x4* dst = (lds_u32x4*)(size_t)(tb + (uint32_t)(lane + 64 * j) * 32u);
-      dst[0] = u32x4{e[0], e[1], e[2], e[3]};
-      dst[1] = u32x4{e[4], e[5], e[6], e[7]};
-    }
-  }
-  // the wave's own LDS writes are performed before its later LDS reads;
-  // these keep the compiler from moving the reads above the writes
-  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-  __builtin_amdgcn_wave_barrier();
+  lut_build<S, GPL>(a, sr, br, osc, tb, lane);
   const int gsh = GSH ? GSH : a.group_shift;
   // byte selectors of the permute (byte j of the code bytes, then the
   // address's upper three bytes), in registers
@@ -175,21 +203,8 @@ __global__ __launch_bounds__(64 * kLutWaves) void qembed_lut_kernel(QembArgs a) 
   for (int s = 0; s < STEPS; ++s) {
     const int wd = s * 64 + lane;
     if (wd >= a.wpr) continue;
-    const uint32_t g = (uint32_t)wd >> gsh;
-    const uint32_t lo8 = ((g & 7u) << 5) * 0x01010101u;
-    const uint32_t hb = tb + ((g >> 3) << 8);
-    const uint32_t c = codes[s];
-    const uint32_t ev = ((c << 1) & 0x1e1e1e1eu) | lo8;  // byte j: entry of code 2j
-    const uint32_t od = ((c >> 3) & 0x1e1e1e1eu) | lo8;  // byte j: entry of code 2j + 1
-    u32x4 o;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      u16x2 v;
-      v.x = *(const lds_u16*)(size_t)__builtin_amdgcn_perm(hb, ev, sel[j]);
-      v.y = *(const lds_u16*)(size_t)__builtin_amdgcn_perm(hb, od, sel[j]);
-      o[j] = __builtin_bit_cast(uint32_t, v);
-    }
-    __builtin_nontemporal_store(o, reinterpret_cast<u32x4*>(obase + s * 512 * S::kBytes));
+    __builtin_nontemporal_store(lut_word<GSH>(codes[s], wd, gsh, tb, sel),
+                                reinterpret_cast<u32x4*>(obase + s * 512 * S::kBytes));
   }
 }
 
@@ -239,7 +254,7 @@ __global__ __launch_bounds__(256) void qembed_norm_kernel(QembArgs a) {
   for (int s = 0; s < STEPS; ++s) {
     const int w = s * 64 + lane;
     const int wc = w < a.wpr ? w : a.wpr - 1;
-    const int g = (wc * 8) / a.group;
+    const int g = wc >> a.group_shift;
     codes[s] = wrow[wc];
     sraw[s] = (uint32_t)sc[grow + g];
     braw[s] = (uint32_t)bi[grow + g];
@@ -271,6 +286,107 @@ __global__ __launch_bounds__(256) void qembed_norm_kernel(QembArgs a) {
       hp[s][k] = S::pack(v[0], v[1]);
     }
   }
+  ss = group_sum<64>(ss);
+  const float rr = rms_scale(ss, a.inv_n, a.eps);
+  const bool rx = a.round_x != 0;
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s) {
+    const int w = s * 64 + lane;
+    if (w >= a.wpr) continue;
+    if (a.out) {
+      u32x4 hv;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) hv[k] = hp[s][k];
+      __builtin_nontemporal_store(
+          hv, reinterpret_cast<u32x4*>(reinterpret_cast<char*>(a.out) +
+                                       (t * a.os + (int64_t)w * 8) * S::kBytes));
+    }
+    float o[8];
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+      float n0 = S::lo(hp[s][e / 2]) * rr, n1 = S::hi(hp[s][e / 2]) * rr;
+      if (rx) round2<S>(n0, n1);
+      float w0 = elem<W>(wr[s], e), w1 = elem<W>(wr[s], e + 1);
+      if (a.plus_one) {
+        w0 = w0 + 1.0f;
+        w1 = w1 + 1.0f;
+      }
+      n0 = n0 * w0;
+      n1 = n1 * w1;
+      if constexpr (Y::kCode != S::kCode) {
+        if (rx) round2<S>(n0, n1);
+      }
+      o[e] = n0;
+      o[e + 1] = n1;
+    }
+    store_elems<Y, 8>(a.y, t * a.ys + (int64_t)w * 8, o);
+  }
+}
+
+// The fused form through the row's lookup table (group 64, up to 64 groups a
+// row): the gather's table build and lookups give the row's values packed in
+// S, then the f64 sum of squares and the norm as above.
+template <class S, int STEPS, class W, class Y>
+__global__ __launch_bounds__(64 * kLutWaves) void qembed_norm_lut_kernel(QembArgs a) {
+  constexpr int WW = 8 * W::kBytes / 4;  // 32-bit words of weights per packed word
+  __shared__ __align__(256) uint16_t lut[kLutWaves][64 * 16];
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t t = (int64_t)blockIdx.x * (blockDim.x >> 6) + wv;
+  if (t >= a.n) return;  // whole wave leaves together
+  const int64_t id = load_id(a, t);
+  const bool valid = id >= 0 && id < a.vocab;
+  const int64_t row = valid ? id : 0;
+  uint32_t sr[1], br[1], codes[STEPS], wr[STEPS][WW];
+  {
+    const int gc = lane < a.gpr ? lane : a.gpr - 1;
+    sr[0] = reinterpret_cast<const uint16_t*>(a.sc)[row * a.gpr + gc];
+    br[0] = reinterpret_cast<const uint16_t*>(a.bi)[row * a.gpr + gc];
+  }
+  const uint32_t* wrow = a.wq + row * a.wpr;
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s) {
+    const int w = s * 64 + lane;
+    const int wc = w < a.wpr ? w : a.wpr - 1;
+    codes[s] = wrow[wc];
+#pragma unroll
+    for (int q = 0; q < WW / 4; ++q) {
+      const u32x4 tw = ld16<W>(a.nw, (int64_t)wc * 8 + q * Vec<W>::N);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) wr[s][4 * q + k] = tw[k];
+    }
+  }
+  // h values are S values, kept packed two per word (zeros past the row and
+  // for an id outside the table)
+  uint32_t hp[STEPS][4];
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s)
+#pragma unroll
+    for (int k = 0; k < 4; ++k) hp[s][k] = 0u;
+  if (valid) {  // uniform over the wave
+    const uint32_t tb = (uint32_t)(size_t)(lds_u16*)&lut[wv][0];
+    lut_build<S, 1>(a, sr, br, S::round(a.scale), tb, lane);
+    uint32_t sel[4] = {0x07060500u, 0x07060501u, 0x07060502u, 0x07060503u};
+    asm volatile("" : "+v"(sel[0]), "+v"(sel[1]), "+v"(sel[2]), "+v"(sel[3]));
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s) {
+      const int wd = s * 64 + lane;
+      if (wd < a.wpr) {
+        const u32x4 o = lut_word<3>(codes[s], wd, 3, tb, sel);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) hp[s][k] = o[k];
+      }
+    }
+  }
+  double ss = 0.0;
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s)
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const double d0 = (double)S::lo(hp[s][k]), d1 = (double)S::hi(hp[s][k]);
+      ss = __builtin_fma(d0, d0, ss);
+      ss = __builtin_fma(d1, d1, ss);
+    }
   ss = group_sum<64>(ss);
   const float rr = rms_scale(ss, a.inv_n, a.eps);
   const bool rx = a.round_x != 0;
@@ -434,7 +550,23 @@ namespace hgk {
 namespace {
 
 template <class S, class W, class Y>
+bool launch_norm_lut(const QembArgs& a, hipStream_t s) {
+  const int steps = (a.wpr + 63) / 64;
+  if (a.group != 64 || a.gpr > 64) return false;
+  const int wpb = a.n >= 1024 ? kLutWaves : 1;
+  const dim3 g((unsigned)((a.n + wpb - 1) / wpb)), b(64 * wpb);
+  if (steps <= 1) HGK_LAUNCH((qembed_norm_lut_kernel<S, 1, W, Y>), g, b, 0, s, a);
+  else if (steps <= 2) HGK_LAUNCH((qembed_norm_lut_kernel<S, 2, W, Y>), g, b, 0, s, a);
+  else if (steps <= 4) HGK_LAUNCH((qembed_norm_lut_kernel<S, 4, W, Y>), g, b, 0, s, a);
+  else if (steps <= 7) HGK_LAUNCH((qembed_norm_lut_kernel<S, 7, W, Y>), g, b, 0, s, a);
+  else if (steps <= 8) HGK_LAUNCH((qembed_norm_lut_kernel<S, 8, W, Y>), g, b, 0, s, a);
+  else return false;
+  return true;
+}
+
+template <class S, class W, class Y>
 bool launch_norm_fast(const QembArgs& a, hipStream_t s) {
+  if (launch_norm_lut<S, W, Y>(a, s)) return true;
   const int steps = (a.wpr + 63) / 64;
   const int wpb = a.n >= 1024 ? 4 : 1;
   const dim3 g((unsigned)((a.n + wpb - 1) / wpb)), b(64 * wpb);
@@ -503,6 +635,7 @@ extern "C" int hgk_quantized_embedding_rms_norm(
   a.ids = ids; a.ids_i32 = ids_dtype == DT_I32; a.n = n_ids; a.wq = w_q; a.sc = scales;
   a.bi = biases; a.vocab = vocab; a.wpr = (int)(hidden / 8); a.gpr = (int)(hidden / group_size);
   a.group = group_size; a.scale = out_scale; a.has_scale = out_scale != 0.0f;
+  a.group_shift = group_size == 32 ? 2 : group_size == 64 ? 3 : 4;
   a.out = h; a.os = h_row_stride; a.hidden = hidden;
   a.nw = norm_w; a.nwdt = norm_w_dtype; a.plus_one = w_plus_one ? 1 : 0;
   a.round_x = t_out == scales_dtype ? 1 : 0; a.eps = eps; a.inv_n = (float)(1.0 / (double)hidden);
