@@ -1066,6 +1066,8 @@ __global__ __launch_bounds__(kXpT) void gather_xp_kernel(GatherArgs a) {
   const __amdgpu_buffer_rsrc_t rb = buf_rsrc(upw ? a.bi2 : a.bi, (uint32_t)(a.E * a.N * G * 2));
   const int C8 = G / 8;
   const int wcol = SW ? (wave & 3) : wave;  // the wave's 64-column slice of the pass
+  // whole 16-byte output pieces (SW): 8-column rows, 16-byte aligned
+  const bool yvec = a.N % 8 == 0 && a.ys % 8 == 0 && (reinterpret_cast<uintptr_t>(a.y) & 15) == 0;
 
   // ---- per-pass addressing and loads (a pass: column chunk nt, rows t0 .. t0 + rp)
   uint32_t wo[NT], so, xo[XP];
@@ -1274,24 +1276,44 @@ __global__ __launch_bounds__(kXpT) void gather_xp_kernel(GatherArgs a) {
         }
         __syncthreads();
         if (wave < 4) {
+          // each gate lane replaces the up value it reads with the output
 #pragma unroll
           for (int i = 0; i < RT; ++i) {
             if (i >= rt) continue;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
               const int lr = i * 16 + 4 * lg + r;
-              if (lr >= rp) continue;
-              const int64_t p = list[t0 + lr];
 #pragma unroll
               for (int t = 0; t < NT; ++t) {
-                const int64_t n = n0 + 16 * t + l16;
+                uint16_t& u = ust[lr * BNO + 64 * wcol + 16 * t + l16];
                 const float gv = BF16::round(acc[i][t][r]);
-                const float uv = BF16::lo((uint32_t)ust[lr * BNO + 64 * wcol + 16 * t + l16]);
+                const float uv = BF16::lo((uint32_t)u);
                 float o;
                 swiglu16<BF16, 1>(&gv, &uv, &o);
-                if (n < a.N) a.y[p * a.ys + n] = (uint16_t)(BF16::pack(o, 0.0f) & 0xffffu);
+                u = (uint16_t)(BF16::pack(o, 0.0f) & 0xffffu);
               }
             }
+          }
+        }
+        __syncthreads();
+        // every wave writes the pass's rows: 16-byte pieces, 8 lanes to a
+        // 128-byte line (2-byte stores from the MFMA layout wrote 1.70x the
+        // output bytes to HBM)
+        const int64_t nb = (int64_t)nt * BNO;
+        if (yvec) {
+          constexpr int PR = BNO / 8;  // pieces per row
+          for (int c = tid; c < rp * PR; c += kXpT) {
+            const int lr = c / PR, j = c % PR;
+            const int64_t n = nb + 8 * j;
+            if (n < a.N)
+              *reinterpret_cast<u32x4*>(&a.y[(int64_t)list[t0 + lr] * a.ys + n]) =
+                  *reinterpret_cast<const u32x4*>(&ust[lr * BNO + 8 * j]);
+          }
+        } else {
+          for (int c = tid; c < rp * BNO; c += kXpT) {
+            const int lr = c / BNO, j = c % BNO;
+            const int64_t n = nb + j;
+            if (n < a.N) a.y[(int64_t)list[t0 + lr] * a.ys + n] = ust[lr * BNO + j];
           }
         }
       } else {

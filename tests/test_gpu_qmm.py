@@ -372,6 +372,16 @@ def test_fused_gate_up_swiglu_grouped_prefill(dev):
                                to_dev(ex3, O.I32, dev), lhs_indices=dl))
     assert np.array_equal(got3, O.glu(O.ACT_SILU, gh3, uh3, O.BF16))
     assert not got3[11].any() and got3[12].any()
+    # a partial last column tile written in 16-byte pieces (N 264) and rows
+    # whose length is no multiple of 8 (N 300: written element by element)
+    for N4 in (264, 300):
+        x4, g4, u4, ex4 = _fused_case(4231 + N4, 512, 8, 16, N4, 512)
+        got4 = to_host(_fused_dev(dev, x4, g4, u4, ex4, 8))
+        gh4 = to_host(H.gather_qmm(d(x4), words_dev(g4[0], dev), d(g4[1]), d(g4[2]),
+                                   to_dev(ex4, O.I32, dev), x_row_div=8))
+        uh4 = to_host(H.gather_qmm(d(x4), words_dev(u4[0], dev), d(u4[1]), d(u4[2]),
+                                   to_dev(ex4, O.I32, dev), x_row_div=8))
+        assert np.array_equal(got4, O.glu(O.ACT_SILU, gh4, uh4, O.BF16)), f"N={N4}"
 
 
 def test_fused_gate_up_swiglu_routing_and_fallback(dev):
