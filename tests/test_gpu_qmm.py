@@ -249,6 +249,18 @@ def test_grouped_path_routing_and_out_of_range(dev):
     assert not got[5].any() and not got[7].any() and got[2300].any() and got[9].any()
 
 
+@pytest.mark.parametrize("N", [200, 300])
+def test_grouped_partial_column_tiles(dev, N):
+    """The exact-product grouped kernel with a last column tile that is only
+    partly inside the matrix: rows of 200 columns leave the tile through LDS
+    as 16-byte pieces, rows of 300 (no multiple of 8) element by element."""
+    P, R, E, K = 2048, 256, 4, 512
+    x, w, s, b, ex = _case(2461 + N, P, R, E, N, K)
+    got = _run(dev, x, w, s, b, ex, O.BF16, x_div=8)
+    ref = O.gather_qmm(x, O.BF16, w, s, b, O.BF16, ex, x_div=8)
+    _check(got, ref, O.BF16, f"grouped N={N}")
+
+
 def test_grouped_size_with_unaligned_pair_count(dev):
     """A pair count that is not a multiple of 4 (the grouped kernel reads the
     expert ids 16 bytes at a time, so it leaves such a call to the per-pair
