@@ -116,6 +116,8 @@ QEMB_NORM_CASES = [
     (5000, 1024, 300, 32, O.BF16, O.F32, False, 0.0, O.F32, 1e-5),        # f32 norm weight
     (5000, 1024, 300, 128, O.BF16, O.F16, False, 0.0, O.F32, 1e-5),       # generic path
     (50, 96, 70, 32, O.BF16, O.BF16, False, 0.0, O.BF16, 1e-5),           # 12 words per row
+    (5000, 512, 300, 64, O.BF16, O.BF16, False, 0.0, O.BF16, 1e-5),       # 1 step per lane
+    (5000, 1024, 257, 64, O.F16, O.BF16, False, 0.0, O.F32, 1e-6),        # 2 steps, f16 scales
 ]
 
 
