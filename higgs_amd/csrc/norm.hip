@@ -78,7 +78,10 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(NormArgs a) {
 
   // Loads are unconditional: unit indices past the row are clamped to its
   // last unit (then ignored), so no select waits on a loaded value before
-  // the next load can issue.
+  // the next load can issue. x and z are read once, non-temporally: the
+  // residual add + RMSNorm at 16384 x 4096 took 90.6 us against 94.0 with
+  // the default policy, at 4096 x 2048 13.8 against 15.1, the plain norm
+  // at 16384 x 4096 46.6 against 47.5.
   XR xr[CPL];
   uint32_t wr[CPL][WW];
   XR zr[TWO ? CPL : 1];
@@ -87,8 +90,8 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(NormArgs a) {
   for (int c = 0; c < CPL; ++c) {
     const int ch = j + c * LPR;
     const int chc = ch < nchunks ? ch : nchunks - 1;
-    xr[c] = ld_raw<UB>(a.x, (r * a.xs + (int64_t)chc * UE) * X::kBytes);
-    if constexpr (TWO) zr[c] = ld_raw<UB>(a.z, (zoff + (int64_t)chc * UE) * X::kBytes);
+    xr[c] = ld_raw_nt<UB>(a.x, (r * a.xs + (int64_t)chc * UE) * X::kBytes);
+    if constexpr (TWO) zr[c] = ld_raw_nt<UB>(a.z, (zoff + (int64_t)chc * UE) * X::kBytes);
   }
   if (has_w) {
 #pragma unroll
