@@ -269,6 +269,11 @@ constexpr int kDecSubs = 4;                       // sub-chunks of 8 groups per 
 constexpr int kDecCG = 8 * kDecSubs;              // groups per chunk
 constexpr int kDecPitch = kDecCG * 32 + 16;       // LDS bytes per code row (conflict-free reads)
 constexpr int kBufWord3 = 0x00020000;             // raw buffer, 32-bit data format
+// Code loads of the decode kernel are non-temporal (each block reads its
+// columns' codes once): 12.68 against 12.89 us at M 64, N 12288, K 2048.
+// The grouped prefill kernel keeps the default policy: a lane reads 8 bytes
+// of a 128-byte code line per group, and the line serves four groups.
+constexpr int kDecNt = 2;
 
 template <int MT>
 struct DecX {
@@ -365,9 +370,9 @@ __global__ __launch_bounds__(kDecThreads) void qgemm_decode_kernel(QgemmArgs a) 
 #pragma unroll
       for (int i = 0; i < WP; ++i)
         if constexpr (PB == 16)
-          wv[s][i] = __builtin_bit_cast(piece_t, __builtin_amdgcn_raw_buffer_load_b128(bw, wgo[i], g0 * 32, 0));
+          wv[s][i] = __builtin_bit_cast(piece_t, __builtin_amdgcn_raw_buffer_load_b128(bw, wgo[i], g0 * 32, kDecNt));
         else
-          wv[s][i] = __builtin_bit_cast(piece_t, __builtin_amdgcn_raw_buffer_load_b64(bw, wgo[i], g0 * 32, 0));
+          wv[s][i] = __builtin_bit_cast(piece_t, __builtin_amdgcn_raw_buffer_load_b64(bw, wgo[i], g0 * 32, kDecNt));
       const __amdgpu_buffer_rsrc_t bs = buf_rsrc(sct_w ? a.sc : a.bi, wave < 2 * SW ? sbytes & live : 0u);
       sbv[s] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(bs, sgo, g0 * 2, 0));
       asm volatile("" ::: "memory");
