@@ -179,10 +179,17 @@ void launch(const GluArgs& a0, bool vec_ok, int64_t rows, int64_t n, hipStream_t
   }
   const GluArgs& a = a0;
   if (vec_ok) {
-    if (a.total >= 256u * 4u * 1024u) {
+    // units of 8 elements per thread: 4 from 8M units (the Qwen3-8B prefill's
+    // 25M: 183.7 us against 190.7 with 2), 2 below it (the Llama-3.2-1B
+    // chain's 4.2M: 32.8 against 34.0 us with 4), 1 below 1M
+    if (a.total >= 8u * 1024u * 1024u) {
       const unsigned blocks = (a.total + 1024u - 1u) / 1024u;
       if (a.contig) HGK_LAUNCH((glu_kernel<X, Y, ACT, 4, true>), dim3(blocks), dim3(256), 0, s, a);
       else HGK_LAUNCH((glu_kernel<X, Y, ACT, 4, false>), dim3(blocks), dim3(256), 0, s, a);
+    } else if (a.total >= 256u * 4u * 1024u) {
+      const unsigned blocks = (a.total + 512u - 1u) / 512u;
+      if (a.contig) HGK_LAUNCH((glu_kernel<X, Y, ACT, 2, true>), dim3(blocks), dim3(256), 0, s, a);
+      else HGK_LAUNCH((glu_kernel<X, Y, ACT, 2, false>), dim3(blocks), dim3(256), 0, s, a);
     } else {
       const unsigned blocks = (a.total + 255u) / 256u;
       if (a.contig) HGK_LAUNCH((glu_kernel<X, Y, ACT, 1, true>), dim3(blocks), dim3(256), 0, s, a);
