@@ -1239,6 +1239,12 @@ __global__ __launch_bounds__(512) void gated_delta_wy_kernel(GdnArgs g) {
   }
 }
 
+// The state after zero steps when no input state is given: zeros.
+__global__ __launch_bounds__(256) void gdn_zero_kernel(uint32_t* p, int64_t words) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < words; i += (int64_t)gridDim.x * 256)
+    p[i] = 0u;
+}
+
 namespace {
 
 template <class X, bool NORM>
@@ -1381,10 +1387,27 @@ extern "C" int hgk_gated_delta(int dtype, const void* q, const void* k, const vo
   if ((q_norm_w == nullptr) != (k_norm_w == nullptr))
     return fail(HGK_ERR_ARG, "%s: pass both q and k norm weights or neither", fn);
   if (!(eps >= 0.0f)) return fail(HGK_ERR_ARG, "%s: eps must be >= 0", fn);
-  if (!q || !k || !v || !a_log || !a || !dt_bias || !b || !y || !state_out)
+  // an empty call (no sequences, or no steps) may pass null data pointers
+  if (!a_log || !dt_bias || (!state_out && batch > 0) ||
+      ((!q || !k || !v || !a || !b || !y) && batch > 0 && seq_len > 0))
     return fail(HGK_ERR_ARG, "%s: null pointer", fn);
   if (batch > 65535 || v_heads > 65535) return fail(HGK_ERR_UNSUPPORTED, "%s: batch or v_heads > 65535", fn);
   if (batch == 0) return HGK_OK;
+  if (seq_len == 0) {
+    // no steps: the state passes through unchanged (zeros without an input state)
+    const hipStream_t s0 = as_stream(stream);
+    const int64_t bytes = batch * v_heads * head_v_dim * head_k_dim * dtype_bytes(dtype);
+    if (state_in && state_in != state_out) {
+      if (hipMemcpyAsync(state_out, state_in, (size_t)bytes, hipMemcpyDeviceToDevice, s0) != hipSuccess)
+        return fail(HGK_ERR_HIP, "%s: state copy failed", fn);
+    } else if (!state_in) {
+      const int64_t words = bytes / 4;  // head_k_dim >= 32: whole words
+      const int64_t blocks = std::min<int64_t>((words + 255) / 256, 4096);
+      HGK_LAUNCH(gdn_zero_kernel, dim3((unsigned)blocks), dim3(256), 0, s0,
+                 static_cast<uint32_t*>(state_out), words);
+    }
+    return launch_status(fn);
+  }
   GdnArgs g{};
   g.q = q; g.k = k; g.v = v; g.a_log = a_log; g.a = a; g.dt_bias = dt_bias; g.b = b;
   g.state_in = state_in; g.qw = q_norm_w; g.kw = k_norm_w; g.pdt = param_dtype; g.eps = eps;
@@ -1431,7 +1454,8 @@ extern "C" int hgk_gated_delta_gated_norm(
   if ((q_norm_w == nullptr) != (k_norm_w == nullptr))
     return fail(HGK_ERR_ARG, "%s: pass both q and k norm weights or neither", fn);
   if (!(eps >= 0.0f) || !(norm_eps >= 0.0f)) return fail(HGK_ERR_ARG, "%s: eps must be >= 0", fn);
-  if (!q || !k || !v || !a_log || !a || !dt_bias || !b || !state_out || !z || !norm_w || !out)
+  if (!a_log || !dt_bias || !norm_w ||
+      ((!q || !k || !v || !a || !b || !state_out || !z || !out) && batch > 0))
     return fail(HGK_ERR_ARG, "%s: null pointer", fn);
   const int64_t rows = batch * v_heads;
   if (z_group_rows <= 0 || z_group_rows > rows) {

@@ -338,7 +338,8 @@ int check_common(const char* fn, const void* x, int xdt, int64_t xs, const void*
   if (rows < 0 || n < 0) return fail(HGK_ERR_ARG, "%s: negative shape rows=%lld n=%lld", fn,
                                      (long long)rows, (long long)n);
   if (n > (int64_t)1 << 30) return fail(HGK_ERR_UNSUPPORTED, "%s: n=%lld too large", fn, (long long)n);
-  if (!x || !y) return fail(HGK_ERR_ARG, "%s: null x or y", fn);
+  // an empty call (no rows or columns) may pass null data pointers
+  if ((!x || !y) && rows > 0 && n > 0) return fail(HGK_ERR_ARG, "%s: null x or y", fn);
   if (!is_float_dtype(xdt) || !is_float_dtype(ydt))
     return fail(HGK_ERR_ARG, "%s: x/y dtype must be f32, bf16 or f16 (got %d, %d)", fn, xdt, ydt);
   if (w && !is_float_dtype(wdt)) return fail(HGK_ERR_ARG, "%s: bad weight dtype %d", fn, wdt);
@@ -390,7 +391,7 @@ extern "C" int hgk_gated_rms_norm(int dtype, const void* x, int64_t x_row_stride
   int st = check_common("hgk_gated_rms_norm", x, dtype, x_row_stride, w, w_dtype, out,
                         out_dtype, out_row_stride, rows, n, eps);
   if (st) return st;
-  if (!w || !z) return fail(HGK_ERR_ARG, "hgk_gated_rms_norm: null z or weight");
+  if (!w || (!z && rows > 0 && n > 0)) return fail(HGK_ERR_ARG, "hgk_gated_rms_norm: null z or weight");
   if (z_group_rows <= 0 || z_group_rows > rows) {
     z_group_rows = rows > 0 ? rows : 1;
     z_group_stride = 0;
@@ -425,7 +426,7 @@ extern "C" int hgk_add_rms_norm(int dtype, const void* x, int64_t x_row_stride, 
   int st = check_common(fn, x, dtype, x_row_stride, w, w_dtype, y, y_dtype, y_row_stride, rows,
                         n, eps);
   if (st) return st;
-  if (!r) return fail(HGK_ERR_ARG, "%s: null residual r", fn);
+  if (!r && rows > 0 && n > 0) return fail(HGK_ERR_ARG, "%s: null residual r", fn);
   if (w_plus_one && !w) return fail(HGK_ERR_ARG, "%s: w_plus_one needs a weight", fn);
   if (rows > 1 && (r_row_stride < n || (h && h_row_stride < n)))
     return fail(HGK_ERR_ARG, "%s: r/h row strides (%lld, %lld) smaller than n=%lld", fn,

@@ -529,7 +529,8 @@ extern "C" int hgk_quantized_embedding(const void* ids, int ids_dtype, int64_t n
                 (long long)hidden, group_size);
   if (n_ids > 1 && out_row_stride < hidden)
     return fail(HGK_ERR_ARG, "%s: out row stride < hidden", fn);
-  if (!ids || !w_q || !scales || !biases || !out) return fail(HGK_ERR_ARG, "%s: null pointer", fn);
+  if (!w_q || !scales || !biases || ((!ids || !out) && n_ids > 0))
+    return fail(HGK_ERR_ARG, "%s: null pointer", fn);
   if (hidden > (1 << 24) || n_ids * hidden >= ((int64_t)1 << 40))
     return fail(HGK_ERR_UNSUPPORTED, "%s: problem too large", fn);
   if (n_ids == 0) return HGK_OK;
@@ -616,7 +617,7 @@ extern "C" int hgk_quantized_embedding_rms_norm(
                 (long long)hidden, group_size);
   if (n_ids > 1 && ((h && h_row_stride < hidden) || y_row_stride < hidden))
     return fail(HGK_ERR_ARG, "%s: h/y row stride < hidden", fn);
-  if (!ids || !w_q || !scales || !biases || !norm_w || !y)
+  if (!w_q || !scales || !biases || !norm_w || ((!ids || !y) && n_ids > 0))
     return fail(HGK_ERR_ARG, "%s: null pointer", fn);
   if (!is_float_dtype(norm_w_dtype) || !is_float_dtype(y_dtype))
     return fail(HGK_ERR_ARG, "%s: norm weight / y dtype must be f32, bf16 or f16", fn);

@@ -357,13 +357,14 @@ extern "C" int hgk_gather_qmm(int dtype, const void* x, int64_t x_rows, int64_t 
     return fail(HGK_ERR_ARG, "%s: bad shape pairs=%lld E=%lld N=%lld K=%lld (K a multiple of %d)", fn,
                 (long long)pairs, (long long)n_experts, (long long)n, (long long)k, group_size);
   if (!lhs_indices && x_row_div <= 0) return fail(HGK_ERR_ARG, "%s: x_row_div must be >= 1", fn);
-  if (x_rows <= 0 || (!lhs_indices && (pairs - 1) / (x_row_div > 0 ? x_row_div : 1) >= x_rows))
+  if (pairs > 0 && (x_rows <= 0 || (!lhs_indices && (pairs - 1) / (x_row_div > 0 ? x_row_div : 1) >= x_rows)))
     return fail(HGK_ERR_ARG, "%s: %lld pairs with x_row_div %lld need more than %lld rows of x", fn,
                 (long long)pairs, (long long)x_row_div, (long long)x_rows);
   if ((x_rows > 1 && x_row_stride < k) || (pairs > 1 && y_row_stride < n))
     return fail(HGK_ERR_ARG, "%s: row strides (%lld, %lld) smaller than K=%lld / N=%lld", fn,
                 (long long)x_row_stride, (long long)y_row_stride, (long long)k, (long long)n);
-  if (!x || !w || !scales || !biases || !rhs_indices || !y) return fail(HGK_ERR_ARG, "%s: null pointer", fn);
+  if (!w || !scales || !biases || ((!x || !rhs_indices || !y) && pairs > 0))
+    return fail(HGK_ERR_ARG, "%s: null pointer", fn);
   if (n_experts * n * k >= ((int64_t)1 << 42) || pairs * n >= ((int64_t)1 << 32) || pairs >= ((int64_t)1 << 31))
     return fail(HGK_ERR_UNSUPPORTED, "%s: problem too large", fn);
   if (pairs == 0) return HGK_OK;
@@ -414,7 +415,7 @@ extern "C" int hgk_quantized_matmul(int dtype, const void* x, int64_t m, int64_t
   if ((m > 1 && x_row_stride < k) || (m > 1 && y_row_stride < n))
     return fail(HGK_ERR_ARG, "%s: row strides (%lld, %lld) smaller than K=%lld / N=%lld", fn,
                 (long long)x_row_stride, (long long)y_row_stride, (long long)k, (long long)n);
-  if (!x || !w || !scales || !biases || !y) return fail(HGK_ERR_ARG, "%s: null pointer", fn);
+  if (!w || !scales || !biases || ((!x || !y) && m > 0)) return fail(HGK_ERR_ARG, "%s: null pointer", fn);
   if (n * k >= ((int64_t)1 << 42) || m >= ((int64_t)1 << 31))
     return fail(HGK_ERR_UNSUPPORTED, "%s: problem too large", fn);
   if (m == 0) return HGK_OK;
@@ -470,15 +471,16 @@ extern "C" int hgk_gather_qmm_swiglu(int dtype, const void* x, int64_t x_rows,
   if (k != 512 && k != 1024 && k != 2048 && k != 4096)
     return fail(HGK_ERR_UNSUPPORTED, "%s: K=%lld (512, 1024, 2048 or 4096)", fn, (long long)k);
   if (!lhs_indices && x_row_div <= 0) return fail(HGK_ERR_ARG, "%s: x_row_div must be >= 1", fn);
-  if (x_rows <= 0 || (!lhs_indices && (pairs - 1) / (x_row_div > 0 ? x_row_div : 1) >= x_rows))
+  if (pairs > 0 && (x_rows <= 0 || (!lhs_indices && (pairs - 1) / (x_row_div > 0 ? x_row_div : 1) >= x_rows)))
     return fail(HGK_ERR_ARG, "%s: %lld pairs with x_row_div %lld need more than %lld rows of x", fn,
                 (long long)pairs, (long long)x_row_div, (long long)x_rows);
   if ((x_rows > 1 && x_row_stride < k) || (pairs > 1 && y_row_stride < n))
     return fail(HGK_ERR_ARG, "%s: row strides (%lld, %lld) smaller than K=%lld / N=%lld", fn,
                 (long long)x_row_stride, (long long)y_row_stride, (long long)k, (long long)n);
-  if (!x || !w_gate || !scales_gate || !biases_gate || !w_up || !scales_up || !biases_up ||
-      !rhs_indices || !y)
+  if (!w_gate || !scales_gate || !biases_gate || !w_up || !scales_up || !biases_up ||
+      ((!x || !rhs_indices || !y) && pairs > 0))
     return fail(HGK_ERR_ARG, "%s: null pointer", fn);
+  if (pairs == 0) return HGK_OK;
   if (n_experts * n * k >= ((int64_t)1 << 42) || pairs * n >= ((int64_t)1 << 32) || pairs >= ((int64_t)1 << 31))
     return fail(HGK_ERR_UNSUPPORTED, "%s: problem too large", fn);
   const auto odd = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 1) != 0; };

@@ -739,10 +739,10 @@ int run(const char* fn, int dtype, const void* q, const int64_t* qs, void* qo, c
                 fn, dtype_name(wdt), dtype_name(dtype));
   if (!(eps >= 0.0f)) return fail(HGK_ERR_ARG, "%s: eps must be >= 0", fn);
   int st;
-  if (qh > 0) {
+  if (B > 0 && L > 0 && qh > 0) {
     if ((st = check_strides(fn, "q", q, qs)) || (st = check_strides(fn, "q_out", qo, qos))) return st;
   }
-  if (kh > 0) {
+  if (B > 0 && L > 0 && kh > 0) {
     if ((st = check_strides(fn, "k", k, ks)) || (st = check_strides(fn, "k_out", ko, kos))) return st;
   }
   RopeArgs a{};

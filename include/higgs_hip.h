@@ -44,6 +44,13 @@ typedef enum {
 
 typedef enum { HGK_ACT_SILU = 0, HGK_ACT_GELU_TANH = 1 } hgk_act;
 
+/* Empty calls: a call with no rows, tokens, ids or pairs (or, for the
+ * gated-delta recurrence, no steps) is valid, enqueues nothing, and may pass
+ * NULL for the data it would have read or written; the recurrence over zero
+ * steps writes the input state (zeros without one) to state_out. Weights,
+ * tables and other operands that do not scale with the call still have to be
+ * given. */
+
 #define HGK_ABI_VERSION 1
 
 /* Error message of the last failed call on this thread ("" if none).

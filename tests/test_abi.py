@@ -152,7 +152,27 @@ def test_error_paths_return_status_and_message():
     assert L.hgk_glu(0, 1, fake, 8, fake, 8, fake, 1, 8, 0, 8, None) == 0
     assert L.hgk_quantized_embedding(fake, 4, 0, fake, fake, fake, 1, 10, 2048, 64, 4, 0.0,
                                      fake, 2048, None) == 0
+    # ... with NULL for the data an empty call would read or write
+    assert L.hgk_rms_norm(None, 1, 8, None, 1, 0, 1e-5, None, 1, 8, 0, 8, None) == 0
+    assert L.hgk_add_rms_norm(1, None, 8, None, 8, None, 1, 0, 1e-5, None, 8, None, 1, 8, 0, 8,
+                              None) == 0
+    assert L.hgk_glu(0, 1, None, 8, None, 8, None, 1, 8, 0, 8, None) == 0
+    assert L.hgk_quantized_embedding(None, 4, 0, fake, fake, fake, 1, 10, 2048, 64, 4, 0.0,
+                                     None, 2048, None) == 0
+    assert L.hgk_gather_qmm(1, None, 0, 64, 1, None, fake, fake, fake, 1, 2, 64, 64, 64, 4, None,
+                            4, 0, None, 64, None) == 0
+    assert L.hgk_quantized_matmul(1, None, 0, 64, fake, fake, fake, 1, 64, 64, 64, 4, None, 64,
+                                  None) == 0
     assert _lib.lib().hgk_last_error() == b""
+    # the checks still hold for calls with data
+    st, msg = _status(L.hgk_glu, 0, 1, None, 8, fake, 8, fake, 1, 8, 1, 8, None)
+    assert st == _lib.ERR_ARG and "null" in msg
+    st, msg = _status(L.hgk_gather_qmm, 1, None, 4, 64, 1, None, fake, fake, fake, 1, 2, 64, 64,
+                      64, 4, fake, 4, 4, fake, 64, None)
+    assert st == _lib.ERR_ARG and "null" in msg
+    st, msg = _status(L.hgk_quantized_embedding, fake, 4, 0, None, fake, fake, 1, 10, 2048, 64,
+                      4, 0.0, None, 2048, None)
+    assert st == _lib.ERR_ARG and "null" in msg
 
 
 def test_python_mirror_raises_on_missing_library(monkeypatch, tmp_path):
