@@ -739,9 +739,14 @@ __device__ inline int64_t ga_row(const GatherArgs& a, int64_t p) {
 // round's ids are requested before the current round is compared, into the
 // other of two arrays, so no register copy waits for them) and expert e's
 // pairs appended to the LDS list, until the ids run out or the list could
-// overflow on the next round. A thread's matches are counted first; one
-// wave-wide prefix sum and one LDS atomic per wave reserve their slots. The
-// list order is free: every listed pair's output row is computed on its own.
+// overflow on the next round. Each id slot's matches are one ballot per
+// wave; one LDS atomic per wave reserves the wave's slots and each match
+// takes its place from scalar popcounts and its lane's mbcnt rank. This
+// replaced a wave-wide prefix sum of per-thread counts (six dependent lane
+// shuffles per round): gate 188.3 -> 183.8 us, down 210.8 -> 206.5 and the
+// fused gate + up + SwiGLU 327.2 -> 322.7 at the 4096-token Qwen3-Next MoE
+// prefill. The list order is free: every listed pair's output row is
+// computed on its own.
 // Contains barriers: every thread of the block calls it. Returns the count.
 template <int RND>
 __device__ inline int ga_list_phase(const GatherArgs& a, __amdgpu_buffer_rsrc_t rid, int64_t e,
@@ -762,26 +767,27 @@ __device__ inline int ga_list_phase(const GatherArgs& a, __amdgpu_buffer_rsrc_t 
   };
   auto round = [&](const uint32_t (&ids)[RND]) {
     const uint32_t p0 = (uint32_t)scan + RND * tid;
-    uint32_t mb = 0;
+    // one ballot per id slot: a wave's matches are counted and placed with
+    // scalar popcounts and mbcnt (no cross-lane prefix sum)
+    uint64_t bal[RND];
+    int tot = 0;
 #pragma unroll
-    for (int i = 0; i < RND; ++i)
-      if (p0 + i < pairs && (ids[i] == e1 || ids[i] == e2)) mb |= 1u << i;
-    const int c = __popc(mb);
-    int incl = c;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const int t = __shfl_up(incl, d, 64);
-      if (lane >= d) incl += t;
+    for (int i = 0; i < RND; ++i) {
+      bal[i] = __ballot(p0 + i < pairs && (ids[i] == e1 || ids[i] == e2));
+      tot += __popcll(bal[i]);
     }
-    const int tot = __shfl(incl, 63, 64);
     if (tot > 0) {  // uniform per wave
       int base = 0;
-      if (lane == 63) base = atomicAdd(cnt, tot);
-      base = __shfl(base, 63, 64);
-      int pos = base + incl - c;
-      while (mb) {
-        list[pos++] = (int32_t)(p0 + __builtin_ctz(mb));
-        mb &= mb - 1u;
+      if (lane == 0) base = atomicAdd(cnt, tot);
+      base = __builtin_amdgcn_readfirstlane(base);
+#pragma unroll
+      for (int i = 0; i < RND; ++i) {
+        if (bal[i]) {  // uniform
+          const uint32_t lo = (uint32_t)bal[i], hi = (uint32_t)(bal[i] >> 32);
+          const int rank = (int)__builtin_amdgcn_mbcnt_hi(hi, __builtin_amdgcn_mbcnt_lo(lo, 0u));
+          if ((bal[i] >> lane) & 1u) list[base + rank] = (int32_t)(p0 + i);
+          base += __popcll(bal[i]);
+        }
       }
     }
     scan += kGaRoundIds;
