@@ -1013,8 +1013,8 @@ __global__ __launch_bounds__(WAVES * 64) void gather_hl_kernel(GatherArgs a) {
 // per-lane offsets; a row past the pass's last reads zeros through an
 // out-of-range offset, so the load sequence is the same on every path.
 // Measured at a 4096-token Qwen3-Next MoE prefill (40,960 pairs, top-10 of
-// 512): gate 190 us against 342 for the hi/lo kernel, down 224 against 414.
-// Passes of 112 rows (7 row tiles) rather than 96 took gate from 218 to
+// 512): gate 184 us against 342 for the hi/lo kernel, down 207-212 against
+// 414. Passes of 112 rows (7 row tiles) rather than 96 took gate from 218 to
 // 190 us and down from 261 to 224. An expert holds about 80 pairs here, but
 // with 96 rows per pass those holding more than 96 took a second pass, and
 // the CUs running them set the launch's end. 128-row passes measured 191 us
