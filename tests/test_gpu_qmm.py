@@ -212,6 +212,11 @@ def test_grouped_prefill_qwen3_next_shape(dev, proj):
         sel = np.arange(lo, lo + 1024)
         ref = O.gather_qmm(x, O.BF16, w, s, b, O.BF16, ex[sel], lhs=(sel // div).astype(np.int32))
         _check(got[sel], ref, O.BF16, f"{proj} pairs {lo}..{lo + 1024}")
+    # the order in which a block lists its expert's pairs depends on which
+    # waves reach the list first; every row is computed on its own, so a
+    # second call gives the same bits
+    again = _run(dev, x, w, s, b, ex, O.BF16, x_div=div)
+    assert np.array_equal(got, again), "a second call differs"
 
 
 def test_grouped_hilo_path_for_other_k(dev):
@@ -334,6 +339,8 @@ def test_fused_gate_up_swiglu_grouped_prefill(dev):
     x, g, u, ex = _fused_case(4201, T, top_k, E, N, K)
     ex[[7, 20000]] = [E, -E - 1]
     got = to_host(_fused_dev(dev, x, g, u, ex, top_k))
+    # same bits on a second call, whatever order the pairs are listed in
+    assert np.array_equal(got, to_host(_fused_dev(dev, x, g, u, ex, top_k))), "a second call differs"
     d = lambda t: to_dev(t, O.BF16, dev)
     gh = to_host(H.gather_qmm(d(x), words_dev(g[0], dev), d(g[1]), d(g[2]), to_dev(ex, O.I32, dev),
                               x_row_div=top_k))
