@@ -235,7 +235,13 @@ template <class X, class Y, class W, int LPR, int CPL, int MODE, int UB = unit_b
 void launch_fast(const NormArgs& a, hipStream_t s) {
   constexpr int RPW = 64 / LPR;
   const int64_t waves = (a.rows + RPW - 1) / RPW;
-  const int wpb = waves >= 4096 ? 4 : 1;  // small problems: spread over CUs
+  // small problems: one wave per block, spread over CUs. Large ones: 2 waves
+  // per block for the plain norm (against 4, in two probe calls: Llama-3.2-1B
+  // 4096 x 2048 7.44 -> 7.22 and 7.25 -> 7.20 us, Qwen3-8B 16384 x 4096
+  // 47.02 -> 46.33 and 46.13 -> 45.70, the Gemma-2 (1+w) norm unchanged),
+  // 4 for the residual add + RMSNorm (14.18 with 2 against 13.90 at
+  // 4096 x 2048).
+  const int wpb = waves < 4096 ? 1 : MODE == kPlain ? 2 : 4;
   const int64_t blocks = (waves + wpb - 1) / wpb;
   HGK_LAUNCH((rms_norm_kernel<X, Y, W, LPR, CPL, MODE, UB>),
              dim3((unsigned)blocks), dim3(64 * wpb), 0, s, a);
