@@ -485,11 +485,16 @@ __global__ __launch_bounds__(256) void gated_delta_chunk_kernel(GdnArgs a) {
   }
 }
 
+// State rows per lane and rows in flight per lane group of the token kernel.
+// At 64 sequences x 32 value heads of 128 x 128 (two probe calls each): 4
+// rows per lane 24.80-24.91 us and 16 rows 26.49-26.56 against 24.59-24.78
+// with 8; 3 and 6 rows in flight 25.11-25.12 and 25.26-25.27 against
+// 24.49-24.62 with 4 (8, all of them: 3-4 % slower).
 #ifndef HGK_GDN_RPL
 #define HGK_GDN_RPL 8
 #endif
 #ifndef HGK_GDN_WIN
-#define HGK_GDN_WIN 4  // state rows in flight per lane group (8: all, 3-4% slower)
+#define HGK_GDN_WIN 4
 #endif
 #ifndef HGK_GDN_WPB
 #define HGK_GDN_WPB 4
